@@ -1,0 +1,69 @@
+/* neurogrid_ext.h - entry points of libgpu_engine.so (gfx950 build) that the
+ * reference's C ABI does not have. Each one is a fusion or an exported stage
+ * of an existing reference path; the comment names the composition it
+ * replaces. Return convention as in kernels.h (0 ok, -1 error on stderr).
+ */
+#ifndef NG_EXT_H
+#define NG_EXT_H
+
+#include <stddef.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Library identification string. */
+const char* ng_version(void);
+
+/* Fused RMSNorm + per-token int8 absmax quantisation (fp16 in):
+ * y = fp16 RMSNorm(x) as cuda_rmsnorm computes it, then q/scales as
+ * cuda_quantize_weights_per_row(q, scales, y, num_tokens, hidden_dim) computes
+ * them; y itself is never written. Replaces the composition
+ * gpu/cuda/kernels.cu:97-119 followed by gpu/cuda/quantize.cu:320-354.
+ * q_out int8 [T, H], scales_out fp32 [T]. */
+int ng_rmsnorm_quant_int8(void* q_out, void* scales_out, const void* input, const void* weight,
+                          int num_tokens, int hidden_dim, float eps);
+
+/* Residual add + RMSNorm + per-token int8: residual_output as in
+ * cuda_add_rmsnorm, then q/scales of the normed row. Replaces
+ * gpu/cuda/kernels.cu:237-262 followed by gpu/cuda/quantize.cu:320-354.
+ * residual_output may alias residual_input. */
+int ng_add_rmsnorm_quant_int8(void* q_out, void* scales_out, void* residual_output, const void* input,
+                              const void* residual_input, const void* weight, int num_tokens,
+                              int hidden_dim, float eps);
+
+/* bf16 residual add + RMSNorm in one pass, same semantics as cuda_add_rmsnorm.
+ * Replaces the bf16 engine's cuda_bf16_add + copy + cuda_bf16_rmsnorm
+ * (gpu/engine/layer.cu:1584-1595). */
+int ng_bf16_add_rmsnorm(void* normed_output, void* residual_output, const void* input,
+                        const void* residual_input, const void* weight, int num_tokens,
+                        int hidden_dim, float eps);
+
+/* bf16 SwiGLU in one pass, same semantics as cuda_silu_mul. Replaces the bf16
+ * engine's cuda_bf16_silu + cuda_bf16_mul (gpu/engine/layer.cu:1603-1607). */
+int ng_bf16_silu_mul(void* output, const void* gate, const void* up, size_t num_elements);
+
+/* fp32 <-> fp16 on the device (round to nearest even / exact widening): the
+ * converters behind gpu/cuda/memory.cu:130-143, exported. */
+int ng_fp32_to_fp16(void* output, const void* input, size_t num_elements);
+int ng_fp16_to_fp32(void* output, const void* input, size_t num_elements);
+
+/* int8 [rows, cols] -> fp16 [rows, cols], out = fp16(float(q) * scale) with
+ * scales[rows] (scale_per_row != 0) or scales[cols]. The dequantisation stage
+ * of cuda_gemm_int8, gpu/cuda/matmul.cu:169-187 (dequantize_and_copy), exported
+ * so that the caller owns the fp16 buffer instead of a per-call cudaMalloc. */
+int cuda_dequantize_weights(void* output, const void* input, const void* scales, int rows, int cols,
+                            int scale_per_row);
+
+/* cuda_gather_embeddings with the vocabulary check the Go caller does on the
+ * host (pkg/inference/gpu_embeddings.go:52): rows whose id is outside
+ * [0, vocab_size) are zero-filled and counted into *d_error_count (device
+ * int, not cleared here). */
+int ng_gather_embeddings_checked(void* output, const void* embed_table, const int* d_token_ids,
+                                 int hidden_size, int num_tokens, int vocab_size, int* d_error_count);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* NG_EXT_H */

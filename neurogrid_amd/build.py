@@ -1,0 +1,97 @@
+"""Build the gfx950 kernel library ``neurogrid_amd/lib/libgpu_engine.so``.
+
+The library is the drop-in for the reference's ``build/libgpu_engine.so``
+(reference Makefile:44,71-73). Each ``csrc/*.hip`` file is compiled with
+hipcc for gfx950 only, in parallel, and linked into one shared object that
+exports the C ABI declared in ``include/*.h``.
+
+Flags worth noting:
+  * no fast-math: fp32 division and sqrt stay IEEE-correct, which the
+    bit-exact RMSNorm and int8 codes rely on;
+  * ``-target-feature -packed-fp32-ops`` keeps the compiler from emitting
+    packed fp32 VALU instructions.
+"""
+from __future__ import annotations
+
+import os
+import shutil
+import subprocess
+import sys
+from concurrent.futures import ThreadPoolExecutor
+from pathlib import Path
+
+PKG = Path(__file__).resolve().parent
+ROOT = PKG.parent
+CSRC = PKG / "csrc"
+BUILD = PKG / "_build"
+LIBDIR = PKG / "lib"
+LIBNAME = "libgpu_engine.so"
+
+ARCH = "gfx950"
+HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
+
+COMMON_FLAGS = [
+    f"--offload-arch={ARCH}",
+    "-O3",
+    "-std=c++17",
+    "-fPIC",
+    "-Wall",
+    "-Wno-unused-function",
+    "-Wno-unused-variable",
+    "-Wno-unused-but-set-variable",
+    "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    f"-I{ROOT / 'include'}",
+]
+
+
+def _run(cmd: list[str]) -> None:
+    proc = subprocess.run(cmd, capture_output=True, text=True)
+    # hipcc's host pass does not know the packed-fp32 feature and says so;
+    # that line is expected and not a problem.
+    err = "\n".join(
+        line for line in proc.stderr.splitlines()
+        if "is not a recognized feature for this target" not in line
+    )
+    if proc.returncode != 0:
+        raise RuntimeError(f"command failed ({proc.returncode}): {' '.join(cmd)}\n{err}")
+    if err.strip():
+        sys.stderr.write(err + "\n")
+
+
+def sources() -> list[Path]:
+    return sorted(CSRC.glob("*.hip"))
+
+
+def build_library(jobs: int | None = None, verbose: bool = False) -> Path:
+    """Compile every kernel source for gfx950 and link libgpu_engine.so."""
+    if shutil.which(HIPCC) is None and not Path(HIPCC).exists():
+        raise RuntimeError(f"hipcc not found at {HIPCC}")
+    BUILD.mkdir(exist_ok=True)
+    LIBDIR.mkdir(exist_ok=True)
+    srcs = sources()
+    objs = [BUILD / (s.stem + ".o") for s in srcs]
+    jobs = jobs or min(len(srcs), max(1, min(8, os.cpu_count() or 1)))
+
+    def compile_one(pair: tuple[Path, Path]) -> None:
+        src, obj = pair
+        cmd = [HIPCC, *COMMON_FLAGS, "-c", str(src), "-o", str(obj)]
+        if verbose:
+            print(" ".join(cmd), flush=True)
+        _run(cmd)
+
+    with ThreadPoolExecutor(max_workers=jobs) as ex:
+        list(ex.map(compile_one, zip(srcs, objs)))
+
+    out = LIBDIR / LIBNAME
+    tmp = LIBDIR / (LIBNAME + ".tmp")
+    cmd = [HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", str(tmp), *map(str, objs)]
+    if verbose:
+        print(" ".join(cmd), flush=True)
+    _run(cmd)
+    os.replace(tmp, out)
+    return out
+
+
+if __name__ == "__main__":
+    path = build_library(verbose="-v" in sys.argv)
+    print(path)

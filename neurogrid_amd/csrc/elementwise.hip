@@ -1,0 +1,251 @@
+// elementwise.hip - streaming element-wise kernels: SwiGLU (silu * up), SiLU,
+// add, mul, scale, and the fp16/bf16/fp32 converters.
+//
+// Semantics, in fp32 with one final round-to-nearest-even to the element type
+// (reference: gpu/cuda/kernels.cu:126-188, 269-359, 653-664; bf16_utils.cu:122-321):
+//   add  c = RN(a + b)           mul  c = RN(a * b)        scale y = RN(x * s)
+//   silu y = RN(x * sig(x))      silu_mul out = RN((g * sig(g)) * u)
+//   sig(x) = 1 / (1 + exp(-x))
+// add, mul and scale are exact-rounded; exp and the reciprocal in sig use the
+// hardware v_exp_f32 / v_rcp_f32 (a few fp32 ulp, far below half an ulp of
+// the 16-bit result).
+//
+// Layout: each thread moves U 16-byte vectors per operand (8 elements each),
+// lane-contiguous so a wave covers 1 KiB per operand per step; loads and
+// stores are non-temporal because every byte is used exactly once.
+#include "ng_common.hpp"
+
+namespace ng {
+
+enum EwOp : int { EW_ADD = 0, EW_MUL = 1, EW_SILU = 2, EW_SILU_MUL = 3, EW_SCALE = 4 };
+
+__device__ __forceinline__ float sigmoid_fast(float x) {
+    const float e = __builtin_amdgcn_exp2f(-x * 1.4426950408889634f);
+    return __builtin_amdgcn_rcpf(1.0f + e);
+}
+
+template <int OP>
+__device__ __forceinline__ float ew_apply(float a, float b, float s) {
+    if (OP == EW_ADD) return a + b;
+    if (OP == EW_MUL) return a * b;
+    if (OP == EW_SILU) return a * sigmoid_fast(a);
+    if (OP == EW_SILU_MUL) return (a * sigmoid_fast(a)) * b;
+    return a * s;  // EW_SCALE
+}
+
+template <int OP>
+struct EwArity {
+    static constexpr bool binary = (OP == EW_ADD || OP == EW_MUL || OP == EW_SILU_MUL);
+};
+
+constexpr int kEwThreads = 256;
+constexpr int kEwUnroll = 4;
+
+template <typename T, int OP, int U>
+__global__ __launch_bounds__(kEwThreads) void ew_vec_kernel(void* out, const void* a, const void* b,
+                                                            float s, size_t nvec) {
+    const size_t base = static_cast<size_t>(blockIdx.x) * (kEwThreads * U) + threadIdx.x;
+    const uint16_t* A = static_cast<const uint16_t*>(a);
+    const uint16_t* B = static_cast<const uint16_t*>(b);
+    uint16_t* O = static_cast<uint16_t*>(out);
+    u32x4 va[U], vb[U];
+#pragma unroll
+    for (int k = 0; k < U; ++k) {
+        const size_t i = base + static_cast<size_t>(k) * kEwThreads;
+        if (i < nvec) {
+            va[k] = ld16_stream(A + i * 8);
+            if (EwArity<OP>::binary) vb[k] = ld16_stream(B + i * 8);
+        }
+    }
+#pragma unroll
+    for (int k = 0; k < U; ++k) {
+        const size_t i = base + static_cast<size_t>(k) * kEwThreads;
+        if (i < nvec) {
+            float fa[8], fb[8], fo[8];
+            unpack8<T>(va[k], fa);
+            if (EwArity<OP>::binary) unpack8<T>(vb[k], fb);
+#pragma unroll
+            for (int e = 0; e < 8; ++e) fo[e] = ew_apply<OP>(fa[e], EwArity<OP>::binary ? fb[e] : 0.0f, s);
+            st16_stream(O + i * 8, pack8<T>(fo));
+        }
+    }
+}
+
+// Any length and alignment: one element per thread per step.
+template <typename T, int OP>
+__global__ __launch_bounds__(kEwThreads) void ew_scalar_kernel(void* out, const void* a, const void* b,
+                                                               float s, size_t begin, size_t n) {
+    const uint16_t* A = static_cast<const uint16_t*>(a);
+    const uint16_t* B = static_cast<const uint16_t*>(b);
+    uint16_t* O = static_cast<uint16_t*>(out);
+    const size_t stride = static_cast<size_t>(gridDim.x) * kEwThreads;
+    for (size_t i = begin + static_cast<size_t>(blockIdx.x) * kEwThreads + threadIdx.x; i < n; i += stride) {
+        const float fa = to_f32<T>(A[i]);
+        const float fb = EwArity<OP>::binary ? to_f32<T>(B[i]) : 0.0f;
+        O[i] = from_f32<T>(ew_apply<OP>(fa, fb, s));
+    }
+}
+
+template <typename T, int OP>
+static int launch_ew(const char* name, void* out, const void* a, const void* b, float s, size_t n) {
+    NG_REQUIRE(out && a && (!EwArity<OP>::binary || b), "%s: null pointer", name);
+    NG_REQUIRE(n > 0, "%s: num_elements must be > 0", name);
+    const bool vec = aligned16(out) && aligned16(a) && (!EwArity<OP>::binary || aligned16(b));
+    size_t done = 0;
+    if (vec) {
+        const size_t nvec = n / 8;
+        if (nvec > 0) {
+            const size_t per_block = static_cast<size_t>(kEwThreads) * kEwUnroll;
+            const size_t blocks = (nvec + per_block - 1) / per_block;
+            ew_vec_kernel<T, OP, kEwUnroll><<<dim3(static_cast<unsigned>(blocks)), dim3(kEwThreads), 0, stream()>>>(
+                out, a, b, s, nvec);
+            NG_CHECK_LAUNCH(name);
+        }
+        done = nvec * 8;
+    }
+    if (done < n) {
+        const size_t rem = n - done;
+        size_t blocks = (rem + kEwThreads - 1) / kEwThreads;
+        if (blocks > 65536) blocks = 65536;
+        ew_scalar_kernel<T, OP><<<dim3(static_cast<unsigned>(blocks)), dim3(kEwThreads), 0, stream()>>>(
+            out, a, b, s, done, n);
+        NG_CHECK_LAUNCH(name);
+    }
+    return 0;
+}
+
+// ---------------------------------------------------------------------------
+// Converters. 16-bit side in 16-byte vectors of 8; fp32 side in two vectors.
+// ---------------------------------------------------------------------------
+enum CvtKind : int { CVT_BF16_TO_F32 = 0, CVT_F32_TO_BF16 = 1, CVT_F16_TO_BF16 = 2, CVT_BF16_TO_F16 = 3,
+                     CVT_F32_TO_F16 = 4, CVT_F16_TO_F32 = 5 };
+
+template <int K>
+__device__ __forceinline__ void cvt_load8(const void* in, size_t e0, float (&f)[8]) {
+    if (K == CVT_F32_TO_BF16 || K == CVT_F32_TO_F16) {
+        const u32x4 v0 = ld16_stream(static_cast<const float*>(in) + e0);
+        const u32x4 v1 = ld16_stream(static_cast<const float*>(in) + e0 + 4);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            f[i] = __builtin_bit_cast(float, v0[i]);
+            f[4 + i] = __builtin_bit_cast(float, v1[i]);
+        }
+    } else {
+        const u32x4 v = ld16_stream(static_cast<const uint16_t*>(in) + e0);
+        if (K == CVT_F16_TO_BF16 || K == CVT_F16_TO_F32) unpack8<f16>(v, f);
+        else unpack8<bf16>(v, f);
+    }
+}
+
+template <int K>
+__device__ __forceinline__ void cvt_store8(void* out, size_t e0, const float (&f)[8]) {
+    if (K == CVT_BF16_TO_F32 || K == CVT_F16_TO_F32) {
+        u32x4 v0, v1;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            v0[i] = __builtin_bit_cast(uint32_t, f[i]);
+            v1[i] = __builtin_bit_cast(uint32_t, f[4 + i]);
+        }
+        st16_stream(static_cast<float*>(out) + e0, v0);
+        st16_stream(static_cast<float*>(out) + e0 + 4, v1);
+    } else if (K == CVT_BF16_TO_F16 || K == CVT_F32_TO_F16) {
+        st16_stream(static_cast<uint16_t*>(out) + e0, pack8<f16>(f));
+    } else {
+        st16_stream(static_cast<uint16_t*>(out) + e0, pack8<bf16>(f));
+    }
+}
+
+template <int K>
+__device__ __forceinline__ float cvt_load1(const void* in, size_t i) {
+    if (K == CVT_F32_TO_BF16 || K == CVT_F32_TO_F16) return static_cast<const float*>(in)[i];
+    const uint16_t b = static_cast<const uint16_t*>(in)[i];
+    return (K == CVT_F16_TO_BF16 || K == CVT_F16_TO_F32) ? to_f32<f16>(b) : to_f32<bf16>(b);
+}
+
+template <int K>
+__device__ __forceinline__ void cvt_store1(void* out, size_t i, float v) {
+    if (K == CVT_BF16_TO_F32 || K == CVT_F16_TO_F32) static_cast<float*>(out)[i] = v;
+    else if (K == CVT_BF16_TO_F16 || K == CVT_F32_TO_F16) static_cast<uint16_t*>(out)[i] = from_f32<f16>(v);
+    else static_cast<uint16_t*>(out)[i] = from_f32<bf16>(v);
+}
+
+template <int K>
+__global__ __launch_bounds__(kEwThreads) void cvt_kernel(void* out, const void* in, size_t n, int vec) {
+    const size_t stride = static_cast<size_t>(gridDim.x) * kEwThreads;
+    const size_t t0 = static_cast<size_t>(blockIdx.x) * kEwThreads + threadIdx.x;
+    if (vec) {
+        const size_t nvec = n / 8;
+        for (size_t i = t0; i < nvec; i += stride) {
+            float f[8];
+            cvt_load8<K>(in, i * 8, f);
+            cvt_store8<K>(out, i * 8, f);
+        }
+        for (size_t i = nvec * 8 + t0; i < n; i += stride) cvt_store1<K>(out, i, cvt_load1<K>(in, i));
+    } else {
+        for (size_t i = t0; i < n; i += stride) cvt_store1<K>(out, i, cvt_load1<K>(in, i));
+    }
+}
+
+template <int K>
+static int launch_cvt(const char* name, void* out, const void* in, size_t n) {
+    NG_REQUIRE(out && in, "%s: null pointer", name);
+    NG_REQUIRE(n > 0, "%s: num_elements must be > 0", name);
+    const int vec = aligned16(out) && aligned16(in);
+    size_t blocks = (n / 8 + kEwThreads - 1) / kEwThreads;
+    if (blocks < 1) blocks = 1;
+    const size_t cap = static_cast<size_t>(device_cu_count()) * 16;
+    if (blocks > cap) blocks = cap;
+    cvt_kernel<K><<<dim3(static_cast<unsigned>(blocks)), dim3(kEwThreads), 0, stream()>>>(out, in, n, vec);
+    NG_CHECK_LAUNCH(name);
+    return 0;
+}
+
+}  // namespace ng
+
+using namespace ng;
+
+extern "C" int cuda_add(void* c, const void* a, const void* b, size_t n) {
+    return launch_ew<f16, EW_ADD>("cuda_add", c, a, b, 0.0f, n);
+}
+extern "C" int cuda_mul(void* c, const void* a, const void* b, size_t n) {
+    return launch_ew<f16, EW_MUL>("cuda_mul", c, a, b, 0.0f, n);
+}
+extern "C" int cuda_silu(void* output, const void* input, size_t n) {
+    return launch_ew<f16, EW_SILU>("cuda_silu", output, input, nullptr, 0.0f, n);
+}
+extern "C" int cuda_silu_mul(void* output, const void* gate, const void* up, size_t n) {
+    return launch_ew<f16, EW_SILU_MUL>("cuda_silu_mul", output, gate, up, 0.0f, n);
+}
+extern "C" int cuda_scale(void* output, const void* input, float scale, size_t n) {
+    return launch_ew<f16, EW_SCALE>("cuda_scale", output, input, nullptr, scale, n);
+}
+extern "C" int cuda_bf16_add(void* c, const void* a, const void* b, size_t n) {
+    return launch_ew<bf16, EW_ADD>("cuda_bf16_add", c, a, b, 0.0f, n);
+}
+extern "C" int cuda_bf16_mul(void* c, const void* a, const void* b, size_t n) {
+    return launch_ew<bf16, EW_MUL>("cuda_bf16_mul", c, a, b, 0.0f, n);
+}
+extern "C" int cuda_bf16_silu(void* output, const void* input, size_t n) {
+    return launch_ew<bf16, EW_SILU>("cuda_bf16_silu", output, input, nullptr, 0.0f, n);
+}
+extern "C" int ng_bf16_silu_mul(void* output, const void* gate, const void* up, size_t n) {
+    return launch_ew<bf16, EW_SILU_MUL>("ng_bf16_silu_mul", output, gate, up, 0.0f, n);
+}
+extern "C" int cuda_bf16_to_fp32(void* output, const void* input, size_t n) {
+    return launch_cvt<CVT_BF16_TO_F32>("cuda_bf16_to_fp32", output, input, n);
+}
+extern "C" int cuda_fp32_to_bf16(void* output, const void* input, size_t n) {
+    return launch_cvt<CVT_F32_TO_BF16>("cuda_fp32_to_bf16", output, input, n);
+}
+extern "C" int cuda_fp16_to_bf16(void* output, const void* input, size_t n) {
+    return launch_cvt<CVT_F16_TO_BF16>("cuda_fp16_to_bf16", output, input, n);
+}
+extern "C" int cuda_bf16_to_fp16(void* output, const void* input, size_t n) {
+    return launch_cvt<CVT_BF16_TO_F16>("cuda_bf16_to_fp16", output, input, n);
+}
+extern "C" int ng_fp32_to_fp16(void* output, const void* input, size_t n) {
+    return launch_cvt<CVT_F32_TO_F16>("ng_fp32_to_fp16", output, input, n);
+}
+extern "C" int ng_fp16_to_fp32(void* output, const void* input, size_t n) {
+    return launch_cvt<CVT_F16_TO_F32>("ng_fp16_to_fp32", output, input, n);
+}

@@ -1,0 +1,492 @@
+// norm.hip - row kernels: RMSNorm, residual-add + RMSNorm, fused RMSNorm +
+// per-token int8 quantisation, and per-row int8 absmax quantisation.
+//
+// Semantics (one row of H elements; fp32 arithmetic, IEEE division/sqrt):
+//   s_i  = x_i                       (plain)   or  RN_f32(x_i + res_i)  (ADD)
+//   ro_i = RN_T(s_i)                 residual_output (ADD only)
+//   ss   = RN_f32(exact sum s_i^2)   see ng_exact.hpp
+//   r    = 1 / sqrt(ss / H + eps)
+//   y_i  = RN_T((o_i * r) * w_i),    o_i = x_i (plain) or ro_i (ADD)
+// The reference computes the same quantities with an fp32 tree sum
+// (gpu/cuda/kernels.cu:58-95 and 196-235; bf16_utils.cu:57-93).
+// Quantisation of a row v (v = y for the fused kernels, v = x otherwise):
+//   m = max|v_i|, scale = m / 127 (1 if 0), q_i = clamp(rint(v_i / scale), +-127)
+// (reference: quantize.cu:274-316, with half-to-even rounding).
+//
+// Layout: one workgroup per row, the row held in registers. Lane l of a
+// workgroup of nthr threads owns the 16-byte vectors l, l + nthr, ...; a row
+// is read from HBM exactly once and each output is written once. Rows up to
+// 8 vectors per lane and 16 waves fit; wider rows or rows that are not a
+// multiple of 8 elements, or unaligned buffers, use the element-wise kernel.
+#include "ng_common.hpp"
+#include "ng_exact.hpp"
+
+namespace ng {
+
+struct RowArgs {
+    void* y;             // normed output [rows, H]            (NORM and !QUANT)
+    void* res_out;       // residual output [rows, H]          (ADD)
+    int8_t* q;           // int8 codes [rows, H]               (QUANT)
+    float* scales;       // fp32 scale per row [rows]          (QUANT)
+    const void* x;       // input [rows, H]
+    const void* res;     // residual input [rows, H]           (ADD)
+    const void* w;       // weight [H]                         (NORM)
+    int H;
+    int nvec;            // H / 8
+    float eps;
+};
+
+// Quantise one element given the row scale and its reciprocal. The product
+// with the reciprocal decides rint(v / scale) unless it lies within 2^-14 of
+// a half-integer; those elements take the IEEE quotient.
+__device__ __forceinline__ int quant_code(float v, float scale, float inv) {
+    float z = v * inv;
+    const float fr = z - floorf(z);
+    const bool near_tie = fabsf(fr - 0.5f) < 0x1p-14f;
+    if (__builtin_expect(near_tie, 0)) z = v / scale;
+    float q = __builtin_rintf(z);
+    q = fminf(fmaxf(q, -127.0f), 127.0f);
+    return static_cast<int>(q);
+}
+
+template <int V>
+struct MaxThreads {
+    static constexpr int value = V <= 4 ? 1024 : 256;
+};
+
+template <typename T, int V, bool NORM, bool ADD, bool QUANT>
+__global__ __launch_bounds__(MaxThreads<V>::value) void row_kernel(RowArgs a) {
+    __shared__ double s_part[16];
+    __shared__ uint64_t s_u[16][2];
+    __shared__ int s_flag[16];
+    __shared__ uint32_t s_max[16];
+
+    const int tid = threadIdx.x;
+    const int nthr = blockDim.x;
+    const int wid = tid >> 6;
+    const int nw = nthr >> 6;
+    const int lane = tid & 63;
+    const size_t rowoff = static_cast<size_t>(blockIdx.x) * static_cast<size_t>(a.H);
+
+    const uint16_t* xr = static_cast<const uint16_t*>(a.x) + rowoff;
+    const uint16_t* rr = ADD ? static_cast<const uint16_t*>(a.res) + rowoff : nullptr;
+    const uint16_t* wr = static_cast<const uint16_t*>(a.w);
+
+    u32x4 xv[V], rv[V], wv[V];
+    bool act[V];
+#pragma unroll
+    for (int k = 0; k < V; ++k) {
+        const int vi = tid + k * nthr;
+        act[k] = vi < a.nvec;
+        xv[k] = act[k] ? ld16(xr + vi * 8) : u32x4{0, 0, 0, 0};
+        if (ADD) rv[k] = act[k] ? ld16(rr + vi * 8) : u32x4{0, 0, 0, 0};
+    }
+    if (NORM) {
+#pragma unroll
+        for (int k = 0; k < V; ++k) {
+            const int vi = tid + k * nthr;
+            wv[k] = act[k] ? ld16(wr + vi * 8) : u32x4{0, 0, 0, 0};
+        }
+    }
+
+    // o = the values the second pass scales: x, or the rounded residual sum.
+    u32x4 ov[V];
+    float r = 1.0f;
+    if (NORM) {
+        double acc = 0.0;
+#pragma unroll
+        for (int k = 0; k < V; ++k) {
+            float fx[8];
+            unpack8<T>(xv[k], fx);
+            if (ADD) {
+                float fr[8];
+                unpack8<T>(rv[k], fr);
+#pragma unroll
+                for (int i = 0; i < 8; ++i) fx[i] = fx[i] + fr[i];
+                ov[k] = pack8<T>(fx);
+            } else {
+                ov[k] = xv[k];
+            }
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                const double d = static_cast<double>(fx[i]);
+                acc = __builtin_fma(d, d, acc);
+            }
+        }
+        acc = wave_sum_f64(acc);
+        double S = acc;
+        if (nw > 1) {
+            if (lane == 0) s_part[wid] = acc;
+            __syncthreads();
+            S = 0.0;
+            for (int j = 0; j < nw; ++j) S += s_part[j];
+        }
+        float ss;
+        if (!ss_fast_resolve(S, a.H, ss)) {
+            // Exact path (identical decision in every thread of the row). It
+            // re-reads the row: nothing has been stored yet, so in-place
+            // calls still see their inputs, and the registers above stay free.
+            u128 u = 0;
+            int bad = 0;
+#pragma unroll 1
+            for (int vi = tid; vi < a.nvec; vi += nthr) {
+                float fx[8];
+                unpack8<T>(ld16(xr + vi * 8), fx);
+                if (ADD) {
+                    float fr[8];
+                    unpack8<T>(ld16(rr + vi * 8), fr);
+#pragma unroll
+                    for (int i = 0; i < 8; ++i) fx[i] = fx[i] + fr[i];
+                }
+#pragma unroll
+                for (int i = 0; i < 8; ++i) {
+                    u128 t;
+                    if (sq_units(fx[i], t)) u += t; else bad = 1;
+                }
+            }
+            u = wave_sum_u128(u);
+            bad = wave_or(bad);
+            if (nw > 1) {
+                if (lane == 0) {
+                    s_u[wid][0] = static_cast<uint64_t>(u);
+                    s_u[wid][1] = static_cast<uint64_t>(u >> 64);
+                    s_flag[wid] = bad;
+                }
+                __syncthreads();
+                u = 0;
+                bad = 0;
+                for (int j = 0; j < nw; ++j) {
+                    u += (static_cast<u128>(s_u[j][1]) << 64) | s_u[j][0];
+                    bad |= s_flag[j];
+                }
+            }
+            if (!bad) ss = units_to_f32(u);
+        }
+        r = 1.0f / __builtin_sqrtf(ss / static_cast<float>(a.H) + a.eps);
+        if (ADD) {
+#pragma unroll
+            for (int k = 0; k < V; ++k)
+                if (act[k]) st16(static_cast<uint16_t*>(a.res_out) + rowoff + (tid + k * nthr) * 8, ov[k]);
+        }
+    } else {
+#pragma unroll
+        for (int k = 0; k < V; ++k) ov[k] = xv[k];
+    }
+
+    // Second pass: y = RN_T((o * r) * w), or v = x when only quantising.
+    u32x4 yv[V];
+    if (NORM) {
+#pragma unroll
+        for (int k = 0; k < V; ++k) {
+            float fo[8], fw[8], fy[8];
+            unpack8<T>(ov[k], fo);
+            unpack8<T>(wv[k], fw);
+#pragma unroll
+            for (int i = 0; i < 8; ++i) fy[i] = (fo[i] * r) * fw[i];
+            yv[k] = pack8<T>(fy);
+        }
+    } else {
+#pragma unroll
+        for (int k = 0; k < V; ++k) yv[k] = xv[k];
+    }
+
+    if (!QUANT) {
+        uint16_t* yr = static_cast<uint16_t*>(a.y) + rowoff;
+#pragma unroll
+        for (int k = 0; k < V; ++k)
+            if (act[k]) st16(yr + (tid + k * nthr) * 8, yv[k]);
+        return;
+    }
+
+    // Row absmax on the 16-bit patterns: for finite values |v| orders like
+    // the integer (bits & 0x7fff).
+    uint32_t mx = 0;
+#pragma unroll
+    for (int k = 0; k < V; ++k) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const uint32_t lo = yv[k][i] & 0x7fffu, hi = (yv[k][i] >> 16) & 0x7fffu;
+            mx = mx > lo ? mx : lo;
+            mx = mx > hi ? mx : hi;
+        }
+    }
+    mx = wave_max_u32(mx);
+    if (nw > 1) {
+        if (lane == 0) s_max[wid] = mx;
+        __syncthreads();
+        mx = 0;
+        for (int j = 0; j < nw; ++j) mx = mx > s_max[j] ? mx : s_max[j];
+    }
+    const float m = to_f32<T>(static_cast<uint16_t>(mx));
+    float scale = m / 127.0f;
+    if (scale == 0.0f) scale = 1.0f;
+    const float inv = 1.0f / scale;
+    if (tid == 0) a.scales[blockIdx.x] = scale;
+
+    int8_t* qr = a.q + rowoff;
+#pragma unroll
+    for (int k = 0; k < V; ++k) {
+        float fy[8];
+        unpack8<T>(yv[k], fy);
+        uint32_t c[2] = {0, 0};
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const uint32_t b = static_cast<uint32_t>(quant_code(fy[i], scale, inv)) & 0xffu;
+            c[i >> 2] |= b << ((i & 3) * 8);
+        }
+        if (act[k]) *reinterpret_cast<u32x2*>(qr + (tid + k * nthr) * 8) = u32x2{c[0], c[1]};
+    }
+}
+
+// Element-wise fallback for any H and any alignment: one workgroup per row,
+// the row re-read from memory for each pass. Same arithmetic as row_kernel.
+template <typename T, bool NORM, bool ADD, bool QUANT>
+__global__ __launch_bounds__(256) void row_kernel_scalar(RowArgs a) {
+    __shared__ double s_part[4];
+    __shared__ uint64_t s_u[4][2];
+    __shared__ int s_flag[4];
+    __shared__ uint32_t s_max[4];
+    const int tid = threadIdx.x, nthr = blockDim.x;
+    const int wid = tid >> 6, nw = nthr >> 6, lane = tid & 63;
+    const size_t rowoff = static_cast<size_t>(blockIdx.x) * static_cast<size_t>(a.H);
+    const uint16_t* xr = static_cast<const uint16_t*>(a.x) + rowoff;
+    const uint16_t* rr = ADD ? static_cast<const uint16_t*>(a.res) + rowoff : nullptr;
+    const uint16_t* wr = static_cast<const uint16_t*>(a.w);
+
+    auto sval = [&](int i) -> float {
+        float v = to_f32<T>(xr[i]);
+        if (ADD) v = v + to_f32<T>(rr[i]);
+        return v;
+    };
+
+    float r = 1.0f;
+    if (NORM) {
+        double acc = 0.0;
+        for (int i = tid; i < a.H; i += nthr) {
+            const double d = static_cast<double>(sval(i));
+            acc = __builtin_fma(d, d, acc);
+        }
+        acc = wave_sum_f64(acc);
+        if (lane == 0) s_part[wid] = acc;
+        __syncthreads();
+        double S = 0.0;
+        for (int j = 0; j < nw; ++j) S += s_part[j];
+        float ss;
+        if (!ss_fast_resolve(S, a.H, ss)) {
+            u128 u = 0;
+            int bad = 0;
+            for (int i = tid; i < a.H; i += nthr) {
+                u128 t;
+                if (sq_units(sval(i), t)) u += t; else bad = 1;
+            }
+            u = wave_sum_u128(u);
+            bad = wave_or(bad);
+            if (lane == 0) {
+                s_u[wid][0] = static_cast<uint64_t>(u);
+                s_u[wid][1] = static_cast<uint64_t>(u >> 64);
+                s_flag[wid] = bad;
+            }
+            __syncthreads();
+            u = 0;
+            bad = 0;
+            for (int j = 0; j < nw; ++j) {
+                u += (static_cast<u128>(s_u[j][1]) << 64) | s_u[j][0];
+                bad |= s_flag[j];
+            }
+            if (!bad) ss = units_to_f32(u);
+        }
+        r = 1.0f / __builtin_sqrtf(ss / static_cast<float>(a.H) + a.eps);
+    }
+
+    // v_i as the 16-bit pattern that is stored or quantised.
+    auto vbits = [&](int i) -> uint16_t {
+        if (!NORM) return xr[i];
+        float o = ADD ? to_f32<T>(from_f32<T>(sval(i))) : to_f32<T>(xr[i]);
+        return from_f32<T>((o * r) * to_f32<T>(wr[i]));
+    };
+
+    if (!QUANT) {
+        uint16_t* yr = static_cast<uint16_t*>(a.y) + rowoff;
+        uint16_t* ror = ADD ? static_cast<uint16_t*>(a.res_out) + rowoff : nullptr;
+        for (int i = tid; i < a.H; i += nthr) {
+            // Both values are computed before either store: the outputs may
+            // alias the inputs element for element.
+            const uint16_t yb = vbits(i);
+            const uint16_t rb = ADD ? from_f32<T>(sval(i)) : 0;
+            if (ADD) ror[i] = rb;
+            yr[i] = yb;
+        }
+        return;
+    }
+
+    uint32_t mx = 0;
+    for (int i = tid; i < a.H; i += nthr) {
+        const uint32_t b = vbits(i) & 0x7fffu;
+        mx = mx > b ? mx : b;
+    }
+    mx = wave_max_u32(mx);
+    if (lane == 0) s_max[wid] = mx;
+    __syncthreads();
+    mx = 0;
+    for (int j = 0; j < nw; ++j) mx = mx > s_max[j] ? mx : s_max[j];
+    const float m = to_f32<T>(static_cast<uint16_t>(mx));
+    float scale = m / 127.0f;
+    if (scale == 0.0f) scale = 1.0f;
+    const float inv = 1.0f / scale;
+    if (tid == 0) a.scales[blockIdx.x] = scale;
+    int8_t* qr = a.q + rowoff;
+    uint16_t* ror = ADD ? static_cast<uint16_t*>(a.res_out) + rowoff : nullptr;
+    for (int i = tid; i < a.H; i += nthr) {
+        const uint16_t vb = vbits(i);
+        const uint16_t rb = ADD ? from_f32<T>(sval(i)) : 0;
+        if (ADD) ror[i] = rb;
+        qr[i] = static_cast<int8_t>(quant_code(to_f32<T>(vb), scale, inv));
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Host dispatch.
+// ---------------------------------------------------------------------------
+template <typename T, bool NORM, bool ADD, bool QUANT>
+struct RowDispatch {
+    template <int V>
+    static void go(dim3 g, dim3 b, const RowArgs& a) {
+        row_kernel<T, V, NORM, ADD, QUANT><<<g, b, 0, stream()>>>(a);
+    }
+    static bool launch(int V, dim3 g, dim3 b, const RowArgs& a) {
+        switch (V) {
+            case 1: go<1>(g, b, a); return true;
+            case 2: go<2>(g, b, a); return true;
+            case 3: go<3>(g, b, a); return true;
+            case 4: go<4>(g, b, a); return true;
+            case 5: go<5>(g, b, a); return true;
+            case 6: go<6>(g, b, a); return true;
+            case 7: go<7>(g, b, a); return true;
+            case 8: go<8>(g, b, a); return true;
+            default: return false;
+        }
+    }
+};
+
+// Workgroup shape for a row of nvec 16-byte vectors: returns false when the
+// row does not fit in registers.
+static bool pick_row_shape(int nvec, int rows, int& nw, int& V) {
+    // Many rows: few waves per row, more vectors in flight per lane. Few
+    // rows (decode): spread each row over more waves.
+    int target_v = rows >= 2048 ? 8 : (rows >= 512 ? 4 : 2);
+    nw = (nvec + 64 * target_v - 1) / (64 * target_v);
+    if (nw < 1) nw = 1;
+    if (nw > 16) nw = 16;
+    V = (nvec + 64 * nw - 1) / (64 * nw);
+    if (V > 4 && nw > 4) {
+        nw = 16;
+        V = (nvec + 64 * nw - 1) / (64 * nw);
+    }
+    return V >= 1 && V <= 8 && !(V > 4 && nw > 4);
+}
+
+template <typename T, bool NORM, bool ADD, bool QUANT>
+static int launch_rows(const char* name, int rows, const RowArgs& a0) {
+    RowArgs a = a0;
+    a.nvec = a.H / 8;
+    bool vec_ok = (a.H % 8 == 0) && aligned16(a.x) && (!ADD || aligned16(a.res)) &&
+                  (!ADD || aligned16(a.res_out)) && (!NORM || aligned16(a.w)) &&
+                  (QUANT || !NORM || aligned16(a.y)) && (!QUANT || aligned8(a.q));
+    int nw = 0, V = 0;
+    if (vec_ok && pick_row_shape(a.nvec, rows, nw, V)) {
+        RowDispatch<T, NORM, ADD, QUANT>::launch(V, dim3(rows), dim3(nw * 64), a);
+    } else {
+        row_kernel_scalar<T, NORM, ADD, QUANT><<<dim3(rows), dim3(256), 0, stream()>>>(a);
+    }
+    NG_CHECK_LAUNCH(name);
+    return 0;
+}
+
+}  // namespace ng
+
+using namespace ng;
+
+// ---------------------------------------------------------------------------
+// C ABI
+// ---------------------------------------------------------------------------
+extern "C" int cuda_rmsnorm(void* output, const void* input, const void* weight,
+                            int num_tokens, int hidden_dim, float eps) {
+    NG_REQUIRE(output && input && weight, "cuda_rmsnorm: null pointer");
+    NG_REQUIRE(num_tokens > 0 && hidden_dim > 0, "cuda_rmsnorm: num_tokens=%d hidden_dim=%d must be > 0",
+               num_tokens, hidden_dim);
+    RowArgs a{};
+    a.y = output; a.x = input; a.w = weight; a.H = hidden_dim; a.eps = eps;
+    return launch_rows<f16, true, false, false>("cuda_rmsnorm", num_tokens, a);
+}
+
+extern "C" int cuda_bf16_rmsnorm(void* output, const void* input, const void* weight,
+                                 int num_tokens, int hidden_dim, float eps) {
+    NG_REQUIRE(output && input && weight, "cuda_bf16_rmsnorm: null pointer");
+    NG_REQUIRE(num_tokens > 0 && hidden_dim > 0, "cuda_bf16_rmsnorm: num_tokens=%d hidden_dim=%d must be > 0",
+               num_tokens, hidden_dim);
+    RowArgs a{};
+    a.y = output; a.x = input; a.w = weight; a.H = hidden_dim; a.eps = eps;
+    return launch_rows<bf16, true, false, false>("cuda_bf16_rmsnorm", num_tokens, a);
+}
+
+extern "C" int cuda_add_rmsnorm(void* normed_output, void* residual_output, const void* input,
+                                const void* residual_input, const void* weight, int num_tokens,
+                                int hidden_dim, float eps) {
+    NG_REQUIRE(normed_output && residual_output && input && residual_input && weight,
+               "cuda_add_rmsnorm: null pointer");
+    NG_REQUIRE(num_tokens > 0 && hidden_dim > 0, "cuda_add_rmsnorm: num_tokens=%d hidden_dim=%d must be > 0",
+               num_tokens, hidden_dim);
+    RowArgs a{};
+    a.y = normed_output; a.res_out = residual_output; a.x = input; a.res = residual_input;
+    a.w = weight; a.H = hidden_dim; a.eps = eps;
+    return launch_rows<f16, true, true, false>("cuda_add_rmsnorm", num_tokens, a);
+}
+
+extern "C" int ng_bf16_add_rmsnorm(void* normed_output, void* residual_output, const void* input,
+                                   const void* residual_input, const void* weight, int num_tokens,
+                                   int hidden_dim, float eps) {
+    NG_REQUIRE(normed_output && residual_output && input && residual_input && weight,
+               "ng_bf16_add_rmsnorm: null pointer");
+    NG_REQUIRE(num_tokens > 0 && hidden_dim > 0, "ng_bf16_add_rmsnorm: num_tokens=%d hidden_dim=%d must be > 0",
+               num_tokens, hidden_dim);
+    RowArgs a{};
+    a.y = normed_output; a.res_out = residual_output; a.x = input; a.res = residual_input;
+    a.w = weight; a.H = hidden_dim; a.eps = eps;
+    return launch_rows<bf16, true, true, false>("ng_bf16_add_rmsnorm", num_tokens, a);
+}
+
+extern "C" int ng_rmsnorm_quant_int8(void* q_out, void* scales_out, const void* input,
+                                     const void* weight, int num_tokens, int hidden_dim, float eps) {
+    NG_REQUIRE(q_out && scales_out && input && weight, "ng_rmsnorm_quant_int8: null pointer");
+    NG_REQUIRE(num_tokens > 0 && hidden_dim > 0, "ng_rmsnorm_quant_int8: num_tokens=%d hidden_dim=%d must be > 0",
+               num_tokens, hidden_dim);
+    RowArgs a{};
+    a.q = static_cast<int8_t*>(q_out); a.scales = static_cast<float*>(scales_out);
+    a.x = input; a.w = weight; a.H = hidden_dim; a.eps = eps;
+    return launch_rows<f16, true, false, true>("ng_rmsnorm_quant_int8", num_tokens, a);
+}
+
+extern "C" int ng_add_rmsnorm_quant_int8(void* q_out, void* scales_out, void* residual_output,
+                                         const void* input, const void* residual_input,
+                                         const void* weight, int num_tokens, int hidden_dim,
+                                         float eps) {
+    NG_REQUIRE(q_out && scales_out && residual_output && input && residual_input && weight,
+               "ng_add_rmsnorm_quant_int8: null pointer");
+    NG_REQUIRE(num_tokens > 0 && hidden_dim > 0,
+               "ng_add_rmsnorm_quant_int8: num_tokens=%d hidden_dim=%d must be > 0", num_tokens, hidden_dim);
+    RowArgs a{};
+    a.q = static_cast<int8_t*>(q_out); a.scales = static_cast<float*>(scales_out);
+    a.res_out = residual_output; a.x = input; a.res = residual_input;
+    a.w = weight; a.H = hidden_dim; a.eps = eps;
+    return launch_rows<f16, true, true, true>("ng_add_rmsnorm_quant_int8", num_tokens, a);
+}
+
+extern "C" int cuda_quantize_weights_per_row(void* output, void* scales, const void* input,
+                                             int rows, int cols) {
+    NG_REQUIRE(output && scales && input, "cuda_quantize_weights_per_row: null pointer");
+    NG_REQUIRE(rows > 0 && cols > 0, "cuda_quantize_weights_per_row: rows=%d cols=%d must be > 0", rows, cols);
+    RowArgs a{};
+    a.q = static_cast<int8_t*>(output); a.scales = static_cast<float*>(scales);
+    a.x = input; a.H = cols;
+    return launch_rows<f16, false, false, true>("cuda_quantize_weights_per_row", rows, a);
+}

@@ -1,0 +1,126 @@
+"""RMSNorm / add+RMSNorm on the GPU vs the oracle: bit-exact.
+
+The row statistic is RN_f32 of the exact sum of squares on both sides and all
+other steps are single IEEE operations, so fp16 and bf16 outputs must match
+the oracle bit for bit, at every shape and for both the register-resident
+and the element-wise kernels.
+"""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+from gpu_util import C, assert_bits_equal, banner, dev, empty, get, ok
+
+pytestmark = pytest.mark.gpu
+
+RNG = np.random.Generator(np.random.PCG64(7))
+
+SHAPES = [(1, 4096), (7, 4096), (64, 4096), (300, 5120), (33, 2048), (5, 14336), (3, 13824),
+          (2, 65536), (4, 4100), (4, 8), (17, 24), (2049, 4096), (600, 1000)]
+
+
+def bits(x, dtype):
+    x = np.asarray(x, np.float32)
+    if dtype == "bf16":
+        from oracle.oracle import f32_to_bf16_bits
+
+        return f32_to_bf16_bits(x)
+    return x.astype(np.float16).view(np.uint16)
+
+
+def run_rmsnorm(lib, x, w, eps, dtype, inplace=False, misalign=False):
+    T, H = x.shape
+    off = 2 if misalign else 0
+    xb = empty(x.nbytes + off)
+    xb.upload(np.concatenate([np.zeros(off // 2, np.uint16), x.ravel()]) if off else x)
+    wb = dev(w)
+    yb = xb if inplace else empty(x.nbytes + off)
+    fn = lib.cuda_bf16_rmsnorm if dtype == "bf16" else lib.cuda_rmsnorm
+    ok(fn(yb.offset(off), xb.offset(off), wb.vp, T, H, C.c_float(eps)), "rmsnorm")
+    out = get(yb, np.uint16, (x.size + off // 2,))
+    return out[off // 2:].reshape(T, H)
+
+
+@pytest.mark.parametrize("dtype", ["f16", "bf16"])
+@pytest.mark.parametrize("T,H", SHAPES)
+def test_rmsnorm_bit_exact(lib, ora, dtype, T, H):
+    banner(f"rmsnorm {dtype} T={T} H={H}")
+    x = bits(RNG.standard_normal((T, H)) * 3, dtype)
+    w = bits(1 + 0.02 * RNG.standard_normal(H), dtype)
+    got = run_rmsnorm(lib, x, w, 1e-5, dtype)
+    assert_bits_equal(got, ora.rmsnorm(x, w, 1e-5, dtype), f"rmsnorm {dtype} {T}x{H}")
+
+
+@pytest.mark.parametrize("dtype", ["f16", "bf16"])
+def test_rmsnorm_in_place_and_unaligned(lib, ora, dtype):
+    banner(f"rmsnorm in-place/unaligned {dtype}")
+    x = bits(RNG.standard_normal((9, 4096)), dtype)
+    w = bits(1 + 0.02 * RNG.standard_normal(4096), dtype)
+    want = ora.rmsnorm(x, w, 1e-6, dtype)
+    assert_bits_equal(run_rmsnorm(lib, x, w, 1e-6, dtype, inplace=True), want, "in place")
+    assert_bits_equal(run_rmsnorm(lib, x, w, 1e-6, dtype, misalign=True), want, "unaligned")
+
+
+def adversarial_rows(H):
+    """Rows whose exact sum of squares sits on (or next to) an fp32 rounding
+    boundary, so the kernel's fp64 fast path cannot decide them."""
+    rows = []
+    for extra in ([], [2.0 ** -24], [2.0 ** -24, 2.0 ** -24]):
+        r = np.zeros(H, np.float32)
+        r[0], r[H // 2] = 2.0 ** 15, 8.0
+        for j, v in enumerate(extra):
+            r[H - 1 - j] = v
+        rows.append(r)
+    r = np.zeros(H, np.float32)
+    r[3], r[H - 5] = 1.0, 2.0 ** -12
+    rows.append(r)
+    r = r.copy()
+    r[7] = 2.0 ** -24
+    rows.append(r)
+    return np.stack(rows)
+
+
+@pytest.mark.parametrize("H", [4096, 5120, 4100])
+def test_rmsnorm_exact_path_rows(lib, ora, H):
+    banner(f"rmsnorm exact-path rows H={H}")
+    x = bits(adversarial_rows(H), "f16")
+    w = bits(np.ones(H), "f16")
+    got = run_rmsnorm(lib, x, w, 0.0, "f16")
+    assert_bits_equal(got, ora.rmsnorm(x, w, 0.0), "adversarial")
+
+
+def run_add_rmsnorm(lib, x, r, w, eps, dtype, inplace=False):
+    T, H = x.shape
+    xb, rb, wb = dev(x), dev(r), dev(w)
+    yb = xb if inplace else empty(x.nbytes)
+    rob = rb if inplace else empty(x.nbytes)
+    fn = lib.ng_bf16_add_rmsnorm if dtype == "bf16" else lib.cuda_add_rmsnorm
+    ok(fn(yb.vp, rob.vp, xb.vp, rb.vp, wb.vp, T, H, C.c_float(eps)), "add_rmsnorm")
+    return get(yb, np.uint16, (T, H)), get(rob, np.uint16, (T, H))
+
+
+@pytest.mark.parametrize("dtype", ["f16", "bf16"])
+@pytest.mark.parametrize("T,H", [(1, 4096), (64, 4096), (257, 5120), (5, 4100), (2, 65536), (1030, 2048)])
+@pytest.mark.parametrize("inplace", [False, True])
+def test_add_rmsnorm_bit_exact(lib, ora, dtype, T, H, inplace):
+    banner(f"add_rmsnorm {dtype} T={T} H={H} inplace={inplace}")
+    x = bits(RNG.standard_normal((T, H)), dtype)
+    r = bits(RNG.standard_normal((T, H)) * 2, dtype)
+    w = bits(1 + 0.02 * RNG.standard_normal(H), dtype)
+    y, ro = run_add_rmsnorm(lib, x, r, w, 1e-5, dtype, inplace)
+    y_want, ro_want = ora.add_rmsnorm(x, r, w, 1e-5, dtype)
+    assert_bits_equal(ro, ro_want, "residual_out")
+    assert_bits_equal(y, y_want, "normed")
+
+
+def test_add_rmsnorm_exact_path_rows(lib, ora):
+    banner("add_rmsnorm exact-path rows")
+    H = 4096
+    x = bits(adversarial_rows(H), "f16")
+    r = np.zeros_like(x)
+    w = bits(np.ones(H), "f16")
+    y, ro = run_add_rmsnorm(lib, x, r, w, 0.0, "f16")
+    y_want, ro_want = ora.add_rmsnorm(x, r, w, 0.0)
+    assert_bits_equal(ro, ro_want, "residual_out")
+    assert_bits_equal(y, y_want, "normed")
