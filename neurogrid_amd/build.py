@@ -8,6 +8,11 @@ exports the C ABI declared in ``include/*.h``.
 Flags worth noting:
   * no fast-math: fp32 division and sqrt stay IEEE-correct, which the
     bit-exact RMSNorm and int8 codes rely on;
+  * ``-ffp-contract=off``: every fp32 product is rounded to fp32 before the
+    next operation. Without it the compiler fuses ``fp16(a * w)`` into one
+    mixed-precision FMA (v_fma_mixlo_f16) that rounds once from the exact
+    product, which differs from fp32-then-fp16 rounding in about 1 element in
+    2^13-2^15;
   * ``-target-feature -packed-fp32-ops`` keeps the compiler from emitting
     packed fp32 VALU instructions.
 """
@@ -35,6 +40,7 @@ COMMON_FLAGS = [
     "-O3",
     "-std=c++17",
     "-fPIC",
+    "-ffp-contract=off",
     "-Wall",
     "-Wno-unused-function",
     "-Wno-unused-variable",

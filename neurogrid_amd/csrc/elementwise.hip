@@ -127,8 +127,8 @@ __device__ __forceinline__ void cvt_load8(const void* in, size_t e0, float (&f)[
         const u32x4 v1 = ld16_stream(static_cast<const float*>(in) + e0 + 4);
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-            f[i] = __builtin_bit_cast(float, v0[i]);
-            f[4 + i] = __builtin_bit_cast(float, v1[i]);
+            f[i] = as_float(v0[i]);
+            f[4 + i] = as_float(v1[i]);
         }
     } else {
         const u32x4 v = ld16_stream(static_cast<const uint16_t*>(in) + e0);

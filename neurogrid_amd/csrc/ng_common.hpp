@@ -1,7 +1,7 @@
 // ng_common.hpp - shared device/host helpers for the gfx950 kernels.
 //
 // Element types are the compiler's native _Float16 and __bf16; conversions
-// from fp32 round to nearest even (v_cvt_f16_f32, v_cvt_pk_bf16_f32).
+// from fp32 round to nearest even (v_cvt_pk_f16_f32, v_cvt_pk_bf16_f32).
 // Global memory is moved in 16-byte vectors (8 x 16-bit elements per lane,
 // global_load_dwordx4 / global_store_dwordx4).
 #pragma once
@@ -75,12 +75,43 @@ template <> __device__ __forceinline__ float to_f32<bf16>(uint16_t bits) {
     return __builtin_bit_cast(float, static_cast<uint32_t>(bits) << 16);
 }
 
+// Reinterpret a 32-bit lane as fp32. Takes the lane by value: clang's
+// __builtin_bit_cast applied directly to an ext_vector element (v[i]) reads
+// element 0 instead of element i.
+__device__ __forceinline__ float as_float(uint32_t bits) { return __builtin_bit_cast(float, bits); }
+
+// fp32 -> 16-bit, round to nearest even, from a value already rounded to
+// fp32. The empty asm makes the fp32 value opaque: without it the backend
+// folds "multiply, then convert to f16" into one v_fma_mixlo_f16, which
+// rounds once from the exact product and so differs from the fp32-then-f16
+// rounding these kernels are specified with (about 1 element in 2^14).
+__device__ __forceinline__ float fp32_barrier(float v) {
+    __asm__("" : "+v"(v));
+    return v;
+}
+
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+
 template <typename T> __device__ __forceinline__ uint16_t from_f32(float v);
 template <> __device__ __forceinline__ uint16_t from_f32<f16>(float v) {
-    return __builtin_bit_cast(uint16_t, static_cast<f16>(v));
+    return __builtin_bit_cast(uint16_t, static_cast<f16>(fp32_barrier(v)));
 }
 template <> __device__ __forceinline__ uint16_t from_f32<bf16>(float v) {
-    return __builtin_bit_cast(uint16_t, static_cast<bf16>(v));
+    return __builtin_bit_cast(uint16_t, static_cast<bf16>(fp32_barrier(v)));
+}
+
+// Two fp32 values -> one dword of two 16-bit values (v_cvt_pk_f16_f32 /
+// v_cvt_pk_bf16_f32, round to nearest even), low half first.
+template <typename T> __device__ __forceinline__ uint32_t pack2(float a, float b);
+template <> __device__ __forceinline__ uint32_t pack2<f16>(float a, float b) {
+    const f32x2 v = {fp32_barrier(a), fp32_barrier(b)};
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, f16x2));
+}
+template <> __device__ __forceinline__ uint32_t pack2<bf16>(float a, float b) {
+    const f32x2 v = {fp32_barrier(a), fp32_barrier(b)};
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, bf16x2));
 }
 
 // Unpack / pack 8 16-bit elements held in a 16-byte vector.
@@ -97,10 +128,7 @@ template <typename T>
 __device__ __forceinline__ u32x4 pack8(const float (&f)[8]) {
     u32x4 v;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        v[i] = static_cast<uint32_t>(from_f32<T>(f[2 * i])) |
-               (static_cast<uint32_t>(from_f32<T>(f[2 * i + 1])) << 16);
-    }
+    for (int i = 0; i < 4; ++i) v[i] = pack2<T>(f[2 * i], f[2 * i + 1]);
     return v;
 }
 

@@ -195,7 +195,7 @@ __global__ __launch_bounds__(kQThreads) void dequant_vec_kernel(uint16_t* out, c
             for (int k = 0; k < 4; ++k) {
                 const u32x4 sv = ld16(scales + g * 16 + 4 * k);
 #pragma unroll
-                for (int e = 0; e < 4; ++e) s[4 * k + e] = __builtin_bit_cast(float, sv[e]);
+                for (int e = 0; e < 4; ++e) s[4 * k + e] = as_float(sv[e]);
             }
         } else {
 #pragma unroll
