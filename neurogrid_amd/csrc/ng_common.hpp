@@ -163,6 +163,58 @@ __device__ __forceinline__ double wave_sum_f64(double v) {
     return v;
 }
 
+// DPP variants: four in-row butterflies (quad_perm 1032, quad_perm 2301,
+// row_half_mirror, row_mirror) leave every lane of a 16-lane row with the
+// row total; the four row totals are read with v_readlane and combined in a
+// fixed order, so the result is wave-uniform (scalar) and identical in every
+// lane. No LDS round trip, unlike the __shfl_xor (ds_bpermute) versions.
+template <int CTRL>
+__device__ __forceinline__ uint32_t dpp_u32(uint32_t v) {
+    return static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, static_cast<int>(v), CTRL, 0xf, 0xf, false));
+}
+
+template <int CTRL>
+__device__ __forceinline__ double dpp_f64(double v) {
+    const uint64_t b = __builtin_bit_cast(uint64_t, v);
+    const uint64_t lo = dpp_u32<CTRL>(static_cast<uint32_t>(b));
+    const uint64_t hi = dpp_u32<CTRL>(static_cast<uint32_t>(b >> 32));
+    return __builtin_bit_cast(double, (hi << 32) | lo);
+}
+
+__device__ __forceinline__ uint32_t readlane_u32(uint32_t v, int lane) {
+    return static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(v), lane));
+}
+
+__device__ __forceinline__ double readlane_f64(double v, int lane) {
+    const uint64_t b = __builtin_bit_cast(uint64_t, v);
+    const uint64_t lo = readlane_u32(static_cast<uint32_t>(b), lane);
+    const uint64_t hi = readlane_u32(static_cast<uint32_t>(b >> 32), lane);
+    return __builtin_bit_cast(double, (hi << 32) | lo);
+}
+
+constexpr int kDppQuadSwap1 = 0xB1;   // quad_perm [1,0,3,2]
+constexpr int kDppQuadSwap2 = 0x4E;   // quad_perm [2,3,0,1]
+constexpr int kDppRowHalfMirror = 0x141;
+constexpr int kDppRowMirror = 0x140;
+
+__device__ __forceinline__ double wave_sum_f64_dpp(double v) {
+    v += dpp_f64<kDppQuadSwap1>(v);
+    v += dpp_f64<kDppQuadSwap2>(v);
+    v += dpp_f64<kDppRowHalfMirror>(v);
+    v += dpp_f64<kDppRowMirror>(v);
+    return (readlane_f64(v, 0) + readlane_f64(v, 16)) + (readlane_f64(v, 32) + readlane_f64(v, 48));
+}
+
+__device__ __forceinline__ uint32_t umax32(uint32_t a, uint32_t b) { return a > b ? a : b; }
+
+__device__ __forceinline__ uint32_t wave_max_u32_dpp(uint32_t v) {
+    v = umax32(v, dpp_u32<kDppQuadSwap1>(v));
+    v = umax32(v, dpp_u32<kDppQuadSwap2>(v));
+    v = umax32(v, dpp_u32<kDppRowHalfMirror>(v));
+    v = umax32(v, dpp_u32<kDppRowMirror>(v));
+    return umax32(umax32(readlane_u32(v, 0), readlane_u32(v, 16)), umax32(readlane_u32(v, 32), readlane_u32(v, 48)));
+}
+
 __device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
 #pragma unroll
     for (int off = 1; off < kWave; off <<= 1) {

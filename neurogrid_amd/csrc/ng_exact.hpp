@@ -5,18 +5,24 @@
 // not depend on how a row is split over lanes and waves, which is what lets
 // the GPU result match a sequential CPU oracle bit for bit.
 //
-// Fast path: every v_i is an fp32 value with at most 24 significant bits, so
-// v_i^2 is exact in fp64 and an fp64 sum of n non-negative exact terms, in
-// any association order, has relative error below (n-1) 2^-53 (1 + 2^-40).
-// With k = ceil(log2 n) the interval S (1 +- 2^(k-51)) therefore contains the
-// exact sum; when both of its ends round to the same fp32 value, so does the
-// exact sum, and that value is RN_f32(S).
+// Fast path. Every v_i is an fp32 value with at most 24 significant bits, so
+// v_i^2 is exact in fp64. Each lane sums its squares into a few fp64
+// accumulators of at most m terms each (relative error below (m-1) 2^-53);
+// the accumulators of the lane, of the wave and of the workgroup are then
+// combined with error-free transformations (two_sum), so the final fp64 value
+// S differs from the exact sum by less than m 2^-53 S (1 + 2^-40). With
+// k = ceil(log2 m) + 1, the interval S (1 +- 2^(k-53)) contains the exact sum;
+// when both of its ends round to the same fp32 value, that value is
+// RN_f32(exact sum). Otherwise (about 2^(k-23) of rows) the slow path runs.
 //
-// Slow path (taken when an interval end sits on the other side of an fp32
-// rounding boundary, about 2^(k-27) of rows): each v_i that lies on the
-// 2^-24 grid with |v_i| < 2^20 -- every value derived from fp16 inputs --
-// contributes v_i^2 as an exact 128-bit integer in units of 2^-48; the
-// integer total is rounded to fp32 exactly.
+// Slow path. A value v on the 2^-24 grid with |v| < 2^17 (every value derived
+// from fp16 inputs) has v^2 = t 2^16 + u 2^-16 + w 2^-48 with integers
+// t < 2^18, u < 2^32, w < 2^32, obtained exactly with two fp64 truncations.
+// Summed over up to 65536 values each limb stays an integer below 2^53, so
+// three fp64 accumulators hold the sum exactly in any order; the limbs are
+// then joined into a 128-bit integer (units of 2^-48) and rounded once.
+// Rows holding a value off that grid (possible for bf16) keep the fast-path
+// value.
 #pragma once
 
 #include "ng_common.hpp"
@@ -25,35 +31,89 @@ namespace ng {
 
 typedef unsigned __int128 u128;
 
-// v^2 in units of 2^-48. Returns false when v is off the 2^-24 grid, has
-// |v| >= 2^20, or is not finite (the row then keeps the fast-path value).
-__device__ __forceinline__ bool sq_units(float v, u128& out) {
-    uint32_t b = __builtin_bit_cast(uint32_t, v) & 0x7fffffffu;
-    out = 0;
-    if (b == 0) return true;
-    uint32_t E = b >> 23;
-    if (E == 0 || E >= 147) return false;  // fp32 subnormal, |v| >= 2^20, inf or nan
-    uint32_t M = (b & 0x7fffffu) | 0x800000u;
-    int tz = __builtin_ctz(M);
-    M >>= tz;
-    int e = static_cast<int>(E) - 150 + tz;  // v = M * 2^e, M odd
-    if (e < -24) return false;
-    int sh = 2 * e + 48;                     // 0 <= sh, M^2 2^sh < 2^88
-    out = static_cast<u128>(static_cast<uint64_t>(M) * M) << sh;
-    return true;
+// ---------------------------------------------------------------- fast path
+struct DD {
+    double hi, lo;
+};
+
+__device__ __forceinline__ DD two_sum(double a, double b) {
+    const double s = a + b;
+    const double bp = s - a;
+    const double e = (a - (s - bp)) + (b - bp);
+    return {s, e};
+}
+
+// (a.hi + a.lo) + (b.hi + b.lo), renormalised so that |lo| <= ulp(hi) / 2.
+__device__ __forceinline__ DD dd_add(DD a, DD b) {
+    DD s = two_sum(a.hi, b.hi);
+    const double lo = s.lo + (a.lo + b.lo);
+    const double hi = s.hi + lo;
+    return {hi, lo - (hi - s.hi)};
+}
+
+template <int CTRL>
+__device__ __forceinline__ DD dpp_dd(DD v) {
+    return {dpp_f64<CTRL>(v.hi), dpp_f64<CTRL>(v.lo)};
+}
+
+__device__ __forceinline__ DD readlane_dd(DD v, int lane) {
+    return {readlane_f64(v.hi, lane), readlane_f64(v.lo, lane)};
+}
+
+// Wave sum with error-free combination; the result is wave-uniform.
+__device__ __forceinline__ DD wave_sum_dd(DD v) {
+    v = dd_add(v, dpp_dd<kDppQuadSwap1>(v));
+    v = dd_add(v, dpp_dd<kDppQuadSwap2>(v));
+    v = dd_add(v, dpp_dd<kDppRowHalfMirror>(v));
+    v = dd_add(v, dpp_dd<kDppRowMirror>(v));
+    return dd_add(dd_add(readlane_dd(v, 0), readlane_dd(v, 16)), dd_add(readlane_dd(v, 32), readlane_dd(v, 48)));
+}
+
+// Resolve the fp64 estimate S (error below m 2^-53 S, m terms per lane
+// accumulator) to RN_f32(exact), or report that the slow path is needed.
+__device__ __forceinline__ bool ss_fast_resolve(double S, int m, float& ss) {
+    ss = static_cast<float>(S);
+    if (!__builtin_isfinite(S)) return true;
+    const int mm = m < 2 ? 2 : m;
+    const int k = 32 - __builtin_clz(static_cast<uint32_t>(mm - 1)) + 1;
+    const double d = __builtin_ldexp(S, k - 53);
+    return static_cast<float>(S - d) == static_cast<float>(S + d);
+}
+
+// ---------------------------------------------------------------- slow path
+struct Limbs {
+    double t, u, w;  // integer-valued: units of 2^16, 2^-16, 2^-48
+    int bad;         // a value off the 2^-24 grid or with |v| >= 2^17
+};
+
+__device__ __forceinline__ void limbs_add(Limbs& L, float v) {
+    const double d = static_cast<double>(v);
+    const double g = d * 0x1p24;
+    if (!(__builtin_fabs(d) < 0x1p17) || g != __builtin_trunc(g)) {
+        L.bad = 1;
+        return;
+    }
+    const double sq = d * d;                                  // exact, < 2^34
+    const double t = __builtin_trunc(sq * 0x1p-16);           // < 2^18
+    const double r1 = __builtin_fma(t, -0x1p16, sq);          // exact, in [0, 2^16)
+    const double u = __builtin_trunc(r1 * 0x1p16);            // < 2^32
+    const double r2 = __builtin_fma(u, -0x1p-16, r1);         // exact, in [0, 2^-16)
+    L.t += t;
+    L.u += u;
+    L.w += r2 * 0x1p48;                                       // < 2^32
 }
 
 // Round a non-negative integer S (units of 2^-48, S < 2^120) to fp32, ties to even.
 __device__ __forceinline__ float units_to_f32(u128 S) {
     if (S == 0) return 0.0f;
-    uint64_t hi = static_cast<uint64_t>(S >> 64);
-    uint64_t lo = static_cast<uint64_t>(S);
-    int p = hi ? 127 - __builtin_clzll(hi) : 63 - __builtin_clzll(lo);
+    const uint64_t hi = static_cast<uint64_t>(S >> 64);
+    const uint64_t lo = static_cast<uint64_t>(S);
+    const int p = hi ? 127 - __builtin_clzll(hi) : 63 - __builtin_clzll(lo);
     if (p <= 23) return __builtin_ldexpf(static_cast<float>(static_cast<uint32_t>(lo)), -48);
     int sh = p - 23;
-    u128 m = S >> sh;
-    u128 rem = S - (m << sh);
-    u128 half = static_cast<u128>(1) << (sh - 1);
+    const u128 m = S >> sh;
+    const u128 rem = S - (m << sh);
+    const u128 half = static_cast<u128>(1) << (sh - 1);
     uint32_t mant = static_cast<uint32_t>(m);
     if (rem > half || (rem == half && (mant & 1u))) ++mant;
     if (mant == (1u << 24)) {
@@ -63,27 +123,11 @@ __device__ __forceinline__ float units_to_f32(u128 S) {
     return __builtin_ldexpf(static_cast<float>(mant), sh - 48);
 }
 
-// Fast-path resolution of an fp64 sum S of n exact squares (see header).
-__device__ __forceinline__ bool ss_fast_resolve(double S, int n, float& ss) {
-    ss = static_cast<float>(S);
-    if (!__builtin_isfinite(S)) return true;
-    int nn = n < 2 ? 2 : n;
-    int k = 32 - __builtin_clz(static_cast<uint32_t>(nn - 1));
-    double d = __builtin_ldexp(S, k - 51);
-    return static_cast<float>(S - d) == static_cast<float>(S + d);
-}
-
-__device__ __forceinline__ u128 shfl_xor_u128(u128 v, int off) {
-    uint64_t lo = static_cast<uint64_t>(v), hi = static_cast<uint64_t>(v >> 64);
-    lo = __shfl_xor(lo, off, kWave);
-    hi = __shfl_xor(hi, off, kWave);
-    return (static_cast<u128>(hi) << 64) | lo;
-}
-
-__device__ __forceinline__ u128 wave_sum_u128(u128 v) {
-#pragma unroll
-    for (int off = 1; off < kWave; off <<= 1) v += shfl_xor_u128(v, off);
-    return v;
+// Exact total of the three limb sums, rounded to fp32.
+__device__ __forceinline__ float limbs_to_f32(double t, double u, double w) {
+    const u128 S = (static_cast<u128>(static_cast<uint64_t>(t)) << 64) +
+                   (static_cast<u128>(static_cast<uint64_t>(u)) << 32) + static_cast<u128>(static_cast<uint64_t>(w));
+    return units_to_f32(S);
 }
 
 }  // namespace ng

@@ -15,7 +15,10 @@
 //
 // Layout: one workgroup per row, the row held in registers. Lane l of a
 // workgroup of nthr threads owns the 16-byte vectors l, l + nthr, ...; a row
-// is read from HBM exactly once and each output is written once. Rows up to
+// is read from HBM exactly once and each output is written once. Row data and
+// outputs move with non-temporal loads/stores (single use; dirty lines would
+// otherwise be flushed from L2 at the end of the kernel); the weight vector,
+// shared by every row, keeps the default cache policy. Rows up to
 // 8 vectors per lane and 16 waves fit; wider rows or rows that are not a
 // multiple of 8 elements, or unaligned buffers, use the element-wise kernel.
 #include "ng_common.hpp"
@@ -56,8 +59,7 @@ struct MaxThreads {
 
 template <typename T, int V, bool NORM, bool ADD, bool QUANT>
 __global__ __launch_bounds__(MaxThreads<V>::value) void row_kernel(RowArgs a) {
-    __shared__ double s_part[16];
-    __shared__ uint64_t s_u[16][2];
+    __shared__ double s_part[16][3];
     __shared__ int s_flag[16];
     __shared__ uint32_t s_max[16];
 
@@ -72,14 +74,15 @@ __global__ __launch_bounds__(MaxThreads<V>::value) void row_kernel(RowArgs a) {
     const uint16_t* rr = ADD ? static_cast<const uint16_t*>(a.res) + rowoff : nullptr;
     const uint16_t* wr = static_cast<const uint16_t*>(a.w);
 
+    // All of the row's loads are issued before any arithmetic.
     u32x4 xv[V], rv[V], wv[V];
     bool act[V];
 #pragma unroll
     for (int k = 0; k < V; ++k) {
         const int vi = tid + k * nthr;
         act[k] = vi < a.nvec;
-        xv[k] = act[k] ? ld16(xr + vi * 8) : u32x4{0, 0, 0, 0};
-        if (ADD) rv[k] = act[k] ? ld16(rr + vi * 8) : u32x4{0, 0, 0, 0};
+        xv[k] = act[k] ? ld16_stream(xr + vi * 8) : u32x4{0, 0, 0, 0};
+        if (ADD) rv[k] = act[k] ? ld16_stream(rr + vi * 8) : u32x4{0, 0, 0, 0};
     }
     if (NORM) {
 #pragma unroll
@@ -93,7 +96,7 @@ __global__ __launch_bounds__(MaxThreads<V>::value) void row_kernel(RowArgs a) {
     u32x4 ov[V];
     float r = 1.0f;
     if (NORM) {
-        double acc = 0.0;
+        double acc[4] = {0.0, 0.0, 0.0, 0.0};
 #pragma unroll
         for (int k = 0; k < V; ++k) {
             float fx[8];
@@ -110,24 +113,31 @@ __global__ __launch_bounds__(MaxThreads<V>::value) void row_kernel(RowArgs a) {
 #pragma unroll
             for (int i = 0; i < 8; ++i) {
                 const double d = static_cast<double>(fx[i]);
-                acc = __builtin_fma(d, d, acc);
+                acc[i & 3] = __builtin_fma(d, d, acc[i & 3]);
             }
         }
-        acc = wave_sum_f64(acc);
-        double S = acc;
+        // Keep only the packed row live across the reduction: the second pass
+        // converts again instead of holding 8 V unpacked floats.
+#pragma unroll
+        for (int k = 0; k < V; ++k) __asm__("" : "+v"(ov[k]));
+        DD S = dd_add(two_sum(acc[0], acc[1]), two_sum(acc[2], acc[3]));
+        S = wave_sum_dd(S);
         if (nw > 1) {
-            if (lane == 0) s_part[wid] = acc;
+            if (lane == 0) {
+                s_part[wid][0] = S.hi;
+                s_part[wid][1] = S.lo;
+            }
             __syncthreads();
-            S = 0.0;
-            for (int j = 0; j < nw; ++j) S += s_part[j];
+            S = {s_part[0][0], s_part[0][1]};
+            for (int j = 1; j < nw; ++j) S = dd_add(S, DD{s_part[j][0], s_part[j][1]});
         }
         float ss;
-        if (!ss_fast_resolve(S, a.H, ss)) {
+        // Each accumulator holds 2 V squares.
+        if (!ss_fast_resolve(S.hi, 2 * V, ss)) {
             // Exact path (identical decision in every thread of the row). It
             // re-reads the row: nothing has been stored yet, so in-place
             // calls still see their inputs, and the registers above stay free.
-            u128 u = 0;
-            int bad = 0;
+            Limbs Lm{0.0, 0.0, 0.0, 0};
 #pragma unroll 1
             for (int vi = tid; vi < a.nvec; vi += nthr) {
                 float fx[8];
@@ -139,34 +149,36 @@ __global__ __launch_bounds__(MaxThreads<V>::value) void row_kernel(RowArgs a) {
                     for (int i = 0; i < 8; ++i) fx[i] = fx[i] + fr[i];
                 }
 #pragma unroll
-                for (int i = 0; i < 8; ++i) {
-                    u128 t;
-                    if (sq_units(fx[i], t)) u += t; else bad = 1;
-                }
+                for (int i = 0; i < 8; ++i) limbs_add(Lm, fx[i]);
             }
-            u = wave_sum_u128(u);
-            bad = wave_or(bad);
+            // Limb sums are exact integers: any summation order gives the same bits.
+            double t = wave_sum_f64_dpp(Lm.t), u = wave_sum_f64_dpp(Lm.u), w = wave_sum_f64_dpp(Lm.w);
+            int bad = static_cast<int>(wave_max_u32_dpp(static_cast<uint32_t>(Lm.bad)));
             if (nw > 1) {
+                __syncthreads();
                 if (lane == 0) {
-                    s_u[wid][0] = static_cast<uint64_t>(u);
-                    s_u[wid][1] = static_cast<uint64_t>(u >> 64);
+                    s_part[wid][0] = t;
+                    s_part[wid][1] = u;
+                    s_part[wid][2] = w;
                     s_flag[wid] = bad;
                 }
                 __syncthreads();
-                u = 0;
+                t = u = w = 0.0;
                 bad = 0;
                 for (int j = 0; j < nw; ++j) {
-                    u += (static_cast<u128>(s_u[j][1]) << 64) | s_u[j][0];
+                    t += s_part[j][0];
+                    u += s_part[j][1];
+                    w += s_part[j][2];
                     bad |= s_flag[j];
                 }
             }
-            if (!bad) ss = units_to_f32(u);
+            if (!bad) ss = limbs_to_f32(t, u, w);
         }
         r = 1.0f / __builtin_sqrtf(ss / static_cast<float>(a.H) + a.eps);
         if (ADD) {
 #pragma unroll
             for (int k = 0; k < V; ++k)
-                if (act[k]) st16(static_cast<uint16_t*>(a.res_out) + rowoff + (tid + k * nthr) * 8, ov[k]);
+                if (act[k]) st16_stream(static_cast<uint16_t*>(a.res_out) + rowoff + (tid + k * nthr) * 8, ov[k]);
         }
     } else {
 #pragma unroll
@@ -194,7 +206,7 @@ __global__ __launch_bounds__(MaxThreads<V>::value) void row_kernel(RowArgs a) {
         uint16_t* yr = static_cast<uint16_t*>(a.y) + rowoff;
 #pragma unroll
         for (int k = 0; k < V; ++k)
-            if (act[k]) st16(yr + (tid + k * nthr) * 8, yv[k]);
+            if (act[k]) st16_stream(yr + (tid + k * nthr) * 8, yv[k]);
         return;
     }
 
@@ -205,17 +217,16 @@ __global__ __launch_bounds__(MaxThreads<V>::value) void row_kernel(RowArgs a) {
     for (int k = 0; k < V; ++k) {
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-            const uint32_t lo = yv[k][i] & 0x7fffu, hi = (yv[k][i] >> 16) & 0x7fffu;
-            mx = mx > lo ? mx : lo;
-            mx = mx > hi ? mx : hi;
+            mx = umax32(mx, yv[k][i] & 0x7fffu);
+            mx = umax32(mx, (yv[k][i] >> 16) & 0x7fffu);
         }
     }
-    mx = wave_max_u32(mx);
+    mx = wave_max_u32_dpp(mx);
     if (nw > 1) {
         if (lane == 0) s_max[wid] = mx;
         __syncthreads();
         mx = 0;
-        for (int j = 0; j < nw; ++j) mx = mx > s_max[j] ? mx : s_max[j];
+        for (int j = 0; j < nw; ++j) mx = umax32(mx, s_max[j]);
     }
     const float m = to_f32<T>(static_cast<uint16_t>(mx));
     float scale = m / 127.0f;
@@ -234,7 +245,7 @@ __global__ __launch_bounds__(MaxThreads<V>::value) void row_kernel(RowArgs a) {
             const uint32_t b = static_cast<uint32_t>(quant_code(fy[i], scale, inv)) & 0xffu;
             c[i >> 2] |= b << ((i & 3) * 8);
         }
-        if (act[k]) *reinterpret_cast<u32x2*>(qr + (tid + k * nthr) * 8) = u32x2{c[0], c[1]};
+        if (act[k]) __builtin_nontemporal_store(u32x2{c[0], c[1]}, reinterpret_cast<u32x2*>(qr + (tid + k * nthr) * 8));
     }
 }
 
@@ -242,8 +253,7 @@ __global__ __launch_bounds__(MaxThreads<V>::value) void row_kernel(RowArgs a) {
 // the row re-read from memory for each pass. Same arithmetic as row_kernel.
 template <typename T, bool NORM, bool ADD, bool QUANT>
 __global__ __launch_bounds__(256) void row_kernel_scalar(RowArgs a) {
-    __shared__ double s_part[4];
-    __shared__ uint64_t s_u[4][2];
+    __shared__ double s_part[4][3];
     __shared__ int s_flag[4];
     __shared__ uint32_t s_max[4];
     const int tid = threadIdx.x, nthr = blockDim.x;
@@ -266,34 +276,37 @@ __global__ __launch_bounds__(256) void row_kernel_scalar(RowArgs a) {
             const double d = static_cast<double>(sval(i));
             acc = __builtin_fma(d, d, acc);
         }
-        acc = wave_sum_f64(acc);
-        if (lane == 0) s_part[wid] = acc;
+        DD S = wave_sum_dd(DD{acc, 0.0});
+        if (lane == 0) {
+            s_part[wid][0] = S.hi;
+            s_part[wid][1] = S.lo;
+        }
         __syncthreads();
-        double S = 0.0;
-        for (int j = 0; j < nw; ++j) S += s_part[j];
+        S = {s_part[0][0], s_part[0][1]};
+        for (int j = 1; j < nw; ++j) S = dd_add(S, DD{s_part[j][0], s_part[j][1]});
         float ss;
-        if (!ss_fast_resolve(S, a.H, ss)) {
-            u128 u = 0;
-            int bad = 0;
-            for (int i = tid; i < a.H; i += nthr) {
-                u128 t;
-                if (sq_units(sval(i), t)) u += t; else bad = 1;
-            }
-            u = wave_sum_u128(u);
-            bad = wave_or(bad);
+        if (!ss_fast_resolve(S.hi, (a.H + nthr - 1) / nthr, ss)) {
+            Limbs Lm{0.0, 0.0, 0.0, 0};
+            for (int i = tid; i < a.H; i += nthr) limbs_add(Lm, sval(i));
+            double t = wave_sum_f64_dpp(Lm.t), u = wave_sum_f64_dpp(Lm.u), w = wave_sum_f64_dpp(Lm.w);
+            int bad = static_cast<int>(wave_max_u32_dpp(static_cast<uint32_t>(Lm.bad)));
+            __syncthreads();
             if (lane == 0) {
-                s_u[wid][0] = static_cast<uint64_t>(u);
-                s_u[wid][1] = static_cast<uint64_t>(u >> 64);
+                s_part[wid][0] = t;
+                s_part[wid][1] = u;
+                s_part[wid][2] = w;
                 s_flag[wid] = bad;
             }
             __syncthreads();
-            u = 0;
+            t = u = w = 0.0;
             bad = 0;
             for (int j = 0; j < nw; ++j) {
-                u += (static_cast<u128>(s_u[j][1]) << 64) | s_u[j][0];
+                t += s_part[j][0];
+                u += s_part[j][1];
+                w += s_part[j][2];
                 bad |= s_flag[j];
             }
-            if (!bad) ss = units_to_f32(u);
+            if (!bad) ss = limbs_to_f32(t, u, w);
         }
         r = 1.0f / __builtin_sqrtf(ss / static_cast<float>(a.H) + a.eps);
     }
@@ -324,7 +337,7 @@ __global__ __launch_bounds__(256) void row_kernel_scalar(RowArgs a) {
         const uint32_t b = vbits(i) & 0x7fffu;
         mx = mx > b ? mx : b;
     }
-    mx = wave_max_u32(mx);
+    mx = wave_max_u32_dpp(mx);
     if (lane == 0) s_max[wid] = mx;
     __syncthreads();
     mx = 0;

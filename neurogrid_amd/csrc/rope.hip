@@ -33,70 +33,86 @@ struct RopeArgs {
     int D;             // head_dim
     int half;          // D / 2
     int upt;           // work units per token
-    int tb;            // tokens per workgroup
+    int units;         // T * upt
     FastDiv div_upt;   // divide by units per token
     FastDiv div_uph;   // divide by units per head
+    FastDiv div_half;  // divide by D / 2
     float inv_freq[kRopeMaxHalf];
 };
 
-// Split-half vector unit: pairs [8j, 8j+8) of one head, i.e. the 16-byte
-// vectors at offsets 8j and D/2 + 8j. Interleaved vector unit: the 16-byte
-// vector at offset 8j, holding pairs [4j, 4j+4).
-template <typename T, int STYLE>
+// A work unit is one 16-byte vector of a head (interleaved style: pairs
+// [4j, 4j+4) at offset 8j) or a matching pair of vectors (split-half style:
+// pairs [8j, 8j+8) at offsets 8j and D/2 + 8j). A workgroup takes U * 256
+// consecutive units, i.e. a run of consecutive tokens:
+//   1. issue every global load of its units;
+//   2. while they are in flight, evaluate (cos, sin) once per (token, pair)
+//      of its tokens into LDS;
+//   3. rotate and store.
+template <typename T, int STYLE, int U>
 __global__ __launch_bounds__(kRopeThreads) void rope_vec_kernel(RopeArgs a) {
-    extern __shared__ float2 cs[];  // [tb][half]
-    const int t0 = blockIdx.x * a.tb;
-    const int ncs = a.tb * a.half;
+    extern __shared__ float2 cs[];  // [tokens of this workgroup][half]
+    const int u0 = blockIdx.x * (kRopeThreads * U);
+    const int ulast = min(u0 + kRopeThreads * U, a.units) - 1;
+    const int tfirst = static_cast<int>(fdiv(static_cast<uint32_t>(u0), a.div_upt));
+    const int ntok = static_cast<int>(fdiv(static_cast<uint32_t>(ulast), a.div_upt)) - tfirst + 1;
+    const uint16_t* in = static_cast<const uint16_t*>(a.in);
+    uint16_t* out = static_cast<uint16_t*>(a.out);
+
+    u32x4 v1[U], v2[U];
+    size_t base[U];
+    int tl[U], jj[U];
+#pragma unroll
+    for (int k = 0; k < U; ++k) {
+        const int u = u0 + k * kRopeThreads + static_cast<int>(threadIdx.x);
+        const int uc = u < a.units ? u : ulast;
+        const int t = static_cast<int>(fdiv(static_cast<uint32_t>(uc), a.div_upt));
+        const int rem = uc - t * a.upt;
+        const int h = static_cast<int>(fdiv(static_cast<uint32_t>(rem), a.div_uph));
+        jj[k] = rem - h * static_cast<int>(a.div_uph.d);
+        tl[k] = t - tfirst;
+        base[k] = (static_cast<size_t>(t) * a.nh + h) * a.D + 8 * jj[k];
+        v1[k] = ld16_stream(in + base[k]);
+        if (STYLE == 0) v2[k] = ld16_stream(in + base[k] + a.half);
+    }
+
+    const int ncs = ntok * a.half;
     for (int idx = threadIdx.x; idx < ncs; idx += kRopeThreads) {
-        const int tl = idx / a.half;
-        const int i = idx - tl * a.half;
-        const int t = t0 + tl;
-        float c = 1.0f, s = 0.0f;
-        if (t < a.T) {
-            const float ang = static_cast<float>(a.pos[t]) * a.inv_freq[i];
-            sincosf(ang, &s, &c);
-        }
-        cs[idx] = make_float2(c, s);
+        const int t = static_cast<int>(fdiv(static_cast<uint32_t>(idx), a.div_half));
+        const int i = idx - t * a.half;
+        const float ang = static_cast<float>(a.pos[tfirst + t]) * a.inv_freq[i];
+        float sn, c;
+        sincosf(ang, &sn, &c);
+        cs[idx] = make_float2(c, sn);
     }
     __syncthreads();
 
-    const int units = a.tb * a.upt;
-    const uint16_t* in = static_cast<const uint16_t*>(a.in);
-    uint16_t* out = static_cast<uint16_t*>(a.out);
-    for (int u = threadIdx.x; u < units; u += kRopeThreads) {
-        const int tl = static_cast<int>(fdiv(static_cast<uint32_t>(u), a.div_upt));
-        const int t = t0 + tl;
-        if (t >= a.T) break;
-        const int rem = u - tl * a.upt;
-        const int h = static_cast<int>(fdiv(static_cast<uint32_t>(rem), a.div_uph));
-        const int j = rem - h * static_cast<int>(a.div_uph.d);
-        const size_t base = (static_cast<size_t>(t) * a.nh + h) * a.D;
-        const float2* c = cs + tl * a.half;
+#pragma unroll
+    for (int k = 0; k < U; ++k) {
+        const int u = u0 + k * kRopeThreads + static_cast<int>(threadIdx.x);
+        if (u >= a.units) break;
+        const float2* c = cs + tl[k] * a.half;
         if (STYLE == 0) {
-            const u32x4 v1 = ld16(in + base + 8 * j);
-            const u32x4 v2 = ld16(in + base + a.half + 8 * j);
             float x1[8], x2[8], y1[8], y2[8];
-            unpack8<T>(v1, x1);
-            unpack8<T>(v2, x2);
+            unpack8<T>(v1[k], x1);
+            unpack8<T>(v2[k], x2);
 #pragma unroll
             for (int e = 0; e < 8; ++e) {
-                const float2 k = c[8 * j + e];
-                y1[e] = x1[e] * k.x - x2[e] * k.y;
-                y2[e] = x1[e] * k.y + x2[e] * k.x;
+                const float2 q = c[8 * jj[k] + e];
+                y1[e] = x1[e] * q.x - x2[e] * q.y;
+                y2[e] = x1[e] * q.y + x2[e] * q.x;
             }
-            st16(out + base + 8 * j, pack8<T>(y1));
-            st16(out + base + a.half + 8 * j, pack8<T>(y2));
+            st16_stream(out + base[k], pack8<T>(y1));
+            st16_stream(out + base[k] + a.half, pack8<T>(y2));
         } else {
-            const u32x4 v = ld16(in + base + 8 * j);
             float x[8], y[8];
-            unpack8<T>(v, x);
+            unpack8<T>(v1[k], x);
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
-                const float2 k = c[4 * j + e];
-                y[2 * e] = x[2 * e] * k.x - x[2 * e + 1] * k.y;
-                y[2 * e + 1] = x[2 * e] * k.y + x[2 * e + 1] * k.x;
+                const float2 q = c[4 * jj[k] + e];
+                y[2 * e] = x[2 * e] * q.x - x[2 * e + 1] * q.y;
+                y[2 * e + 1] = x[2 * e] * q.y + x[2 * e + 1] * q.x;
             }
-            st16(out + base + 8 * j, pack8<T>(y));
+            st16_stream(out + base[k], pack8<T>(y));
         }
     }
 }
@@ -172,21 +188,31 @@ static int launch_rope(const char* name, void* output, const void* input, const 
     if (vec) {
         const int uph = style == 0 ? head_dim / 16 : head_dim / 8;
         a.upt = num_heads * uph;
-        // About 1024 units per workgroup; at least one token; LDS <= 32 KiB.
-        int tb = (1024 + a.upt - 1) / a.upt;
-        const int max_tb_lds = (32 * 1024) / (a.half * static_cast<int>(sizeof(float2)));
-        if (tb > max_tb_lds) tb = max_tb_lds;
-        if (tb < 1) tb = 1;
-        if (tb > a.T) tb = a.T;
-        a.tb = tb;
+        const long long units = static_cast<long long>(a.T) * a.upt;
+        NG_REQUIRE(units < (1ll << 31), "%s: tensor too large", name);
+        a.units = static_cast<int>(units);
         a.div_upt = make_fastdiv(static_cast<uint32_t>(a.upt));
         a.div_uph = make_fastdiv(static_cast<uint32_t>(uph));
-        const unsigned blocks = static_cast<unsigned>((a.T + tb - 1) / tb);
-        const size_t lds = static_cast<size_t>(tb) * a.half * sizeof(float2);
-        if (style == 0)
-            rope_vec_kernel<T, 0><<<dim3(blocks), dim3(kRopeThreads), lds, stream()>>>(a);
-        else
-            rope_vec_kernel<T, 1><<<dim3(blocks), dim3(kRopeThreads), lds, stream()>>>(a);
+        a.div_half = make_fastdiv(static_cast<uint32_t>(a.half));
+        // Units per thread: as many as keep at least two workgroups per CU.
+        const long long min_blocks = 2ll * device_cu_count();
+        int U = 4;
+        while (U > 1 && (units + kRopeThreads * U - 1) / (kRopeThreads * U) < min_blocks) U >>= 1;
+        const int per_block = kRopeThreads * U;
+        const unsigned blocks = static_cast<unsigned>((units + per_block - 1) / per_block);
+        const int max_tok = (per_block + a.upt - 1) / a.upt + 1;
+        const size_t lds = static_cast<size_t>(max_tok) * a.half * sizeof(float2);
+        NG_REQUIRE(lds <= 64 * 1024, "%s: head_dim=%d needs %zu bytes of LDS", name, head_dim, lds);
+        auto go = [&](auto kern) { kern<<<dim3(blocks), dim3(kRopeThreads), lds, stream()>>>(a); };
+        if (style == 0) {
+            if (U == 4) go(rope_vec_kernel<T, 0, 4>);
+            else if (U == 2) go(rope_vec_kernel<T, 0, 2>);
+            else go(rope_vec_kernel<T, 0, 1>);
+        } else {
+            if (U == 4) go(rope_vec_kernel<T, 1, 4>);
+            else if (U == 2) go(rope_vec_kernel<T, 1, 2>);
+            else go(rope_vec_kernel<T, 1, 1>);
+        }
     } else {
         const size_t npairs = static_cast<size_t>(a.T) * num_heads * a.half;
         size_t blocks = (npairs + kRopeThreads - 1) / kRopeThreads;
