@@ -13,8 +13,9 @@ Launches go through the library's C ABI on the stream set with
 ng_set_stream. The host side is Python (ctypes), which issues launches more
 slowly than a short kernel runs, so every timed sequence is captured once
 into a HIP graph and replayed: the GPU then never waits for the host.
-  * step time: one graph per rotating set holding the six launches of a
-    layer; K replays between two HIP events on the launch stream;
+  * step time: one graph holding exactly K layer steps (6 K launches, the
+    steps cycling over the rotating sets), replayed once between two HIP
+    events on the launch stream, after a W-step warm-up graph;
   * per-kernel time: one graph per kernel holding R back-to-back launches of
     that kernel over the rotating sets; the event time of a replay / R is the
     kernel's average launch duration (it includes the short dispatch gap
@@ -235,15 +236,17 @@ def run_layer(L, hip, stream, cfg, steps, warmup, kernel_launches=24, kernel_rep
                 raise RuntimeError(f"{name} failed")
     hip.sync()
 
-    step_graphs = [hip.capture(stream, lset) for lset in launches]
-    step_ms = time_graph(hip, stream, step_graphs, steps, warmup)
-    t0 = time.perf_counter()
-    for i in range(steps):
-        step_graphs[i % nsets].launch(stream)
+    # One graph of `warmup` steps, replayed once untimed, then one graph of
+    # exactly `steps` steps, replayed once between two events.
+    warm_graph = hip.capture(stream, [t for i in range(max(warmup, 1)) for t in launches[i % nsets]])
+    timed_graph = hip.capture(stream, [t for i in range(steps) for t in launches[i % nsets]])
+    warm_graph.launch(stream)
     hip.sync()
+    t0 = time.perf_counter()
+    step_ms = time_graph(hip, stream, [timed_graph], 1, 0) / steps
     wall_ms = (time.perf_counter() - t0) * 1e3 / steps
-    for g in step_graphs:
-        g.destroy()
+    warm_graph.destroy()
+    timed_graph.destroy()
 
     per = {}
     for j, n in enumerate(names):

@@ -11,7 +11,7 @@
 // the 16-bit result).
 //
 // Layout: each thread moves U 16-byte vectors per operand (8 elements each),
-// lane-contiguous so a wave covers 1 KiB per operand per step; loads and
+// lane-contiguous so a wave covers 1 KiB per operand per vector; loads and
 // stores are non-temporal because every byte is used exactly once.
 #include "ng_common.hpp"
 
@@ -39,7 +39,10 @@ struct EwArity {
 };
 
 constexpr int kEwThreads = 256;
-constexpr int kEwUnroll = 4;
+// One 16-byte vector per operand per thread: measured on MI355X, deeper
+// per-thread unrolling (2 or 4 vectors) is slower at every size from 0.5 MB
+// to 350 MB, and at decode sizes it leaves most CUs idle.
+constexpr int kEwUnroll = 1;
 
 template <typename T, int OP, int U>
 __global__ __launch_bounds__(kEwThreads) void ew_vec_kernel(void* out, const void* a, const void* b,

@@ -137,6 +137,125 @@ __device__ __forceinline__ uint16_t lane16(const u32x4 v, int i) {
 }
 
 // ---------------------------------------------------------------------------
+// Arithmetic on one 16-bit element of a packed dword (HI selects the upper
+// half), each rounded once to fp32 exactly as the plain fp32 expression
+// would be. For fp16 each is one v_fma_mix_f32, which widens its fp16
+// operands exactly inside the instruction, so no separate conversion is
+// issued; for bf16 the element is widened with a shift first.
+//   el_get  h            el_mul  RN(h * b)        el_add  RN(ha + hb)
+//   el_fma  RN(a * b + h)
+// el_mul adds -0.0 to the exact product so that a zero product keeps the
+// sign an IEEE multiply gives it.
+// ---------------------------------------------------------------------------
+template <typename T, int HI>
+__device__ __forceinline__ float el_get(uint32_t p) {
+    return to_f32<T>(static_cast<uint16_t>(HI ? p >> 16 : p & 0xffffu));
+}
+
+template <typename T, int HI>
+__device__ __forceinline__ float el_mul(uint32_t p, float b) {
+    if constexpr (__is_same(T, f16)) {
+        float d;
+        if (HI)
+            __asm__("v_fma_mix_f32 %0, %1, %2, %3 op_sel:[1,0,0] op_sel_hi:[1,0,0]" : "=v"(d) : "v"(p), "v"(b), "v"(-0.0f));
+        else
+            __asm__("v_fma_mix_f32 %0, %1, %2, %3 op_sel_hi:[1,0,0]" : "=v"(d) : "v"(p), "v"(b), "v"(-0.0f));
+        return d;
+    } else {
+        return fp32_barrier(el_get<T, HI>(p) * b);
+    }
+}
+
+template <typename T, int HI>
+__device__ __forceinline__ float el_add(uint32_t pa, uint32_t pb) {
+    if constexpr (__is_same(T, f16)) {
+        float d;
+        if (HI)
+            __asm__("v_fma_mix_f32 %0, %1, 1.0, %2 op_sel:[1,0,1] op_sel_hi:[1,0,1]" : "=v"(d) : "v"(pa), "v"(pb));
+        else
+            __asm__("v_fma_mix_f32 %0, %1, 1.0, %2 op_sel_hi:[1,0,1]" : "=v"(d) : "v"(pa), "v"(pb));
+        return d;
+    } else {
+        return fp32_barrier(el_get<T, HI>(pa) + el_get<T, HI>(pb));
+    }
+}
+
+template <typename T, int HI>
+__device__ __forceinline__ float el_fma(float a, float b, uint32_t p) {
+    if constexpr (__is_same(T, f16)) {
+        float d;
+        if (HI)
+            __asm__("v_fma_mix_f32 %0, %1, %2, %3 op_sel:[0,0,1] op_sel_hi:[0,0,1]" : "=v"(d) : "v"(a), "v"(b), "v"(p));
+        else
+            __asm__("v_fma_mix_f32 %0, %1, %2, %3 op_sel_hi:[0,0,1]" : "=v"(d) : "v"(a), "v"(b), "v"(p));
+        return d;
+    } else {
+        return __builtin_fmaf(a, b, el_get<T, HI>(p));
+    }
+}
+
+// ---------------------------------------------------------------------------
+// int8 absmax code: q = clamp(rint(RN(v / s)), -127, 127) for a row scale
+// s > 0, given inv = RN(1 / s) and ns = -s. RN(v / s) is obtained without a
+// division: z = RN(v inv) is within a few ulp of v / s, the residual
+// r = RN(v - z s) is then exact, and RN(z + r inv) is the correctly rounded
+// quotient (Markstein's correction step; checked exhaustively for every fp16
+// v against every scale RN(m / 127) of an fp16 m). Returned biased by +128,
+// ready for v_cvt_pk_u8_f32; xor 0x80 turns the byte into two's complement.
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ float qcode_biased_f32(float v, float inv, float ns) {
+    const float z = v * inv;
+    const float r = __builtin_fmaf(z, ns, v);
+    const float q = __builtin_rintf(__builtin_fmaf(r, inv, z));
+    return __builtin_amdgcn_fmed3f(q, -127.0f, 127.0f) + 128.0f;
+}
+
+template <typename T, int HI>
+__device__ __forceinline__ float qcode_biased(uint32_t p, float inv, float ns) {
+    if constexpr (__is_same(T, f16)) {
+        const float z = el_mul<T, HI>(p, inv);
+        const float r = el_fma<T, HI>(z, ns, p);
+        const float q = __builtin_rintf(__builtin_fmaf(r, inv, z));
+        return __builtin_amdgcn_fmed3f(q, -127.0f, 127.0f) + 128.0f;
+    } else {
+        return qcode_biased_f32(el_get<T, HI>(p), inv, ns);
+    }
+}
+
+// Codes of the 8 elements of a 16-byte vector, as two dwords of int8.
+template <typename T>
+__device__ __forceinline__ u32x2 qcode8(const u32x4 v, float inv, float ns) {
+    u32x2 out;
+#pragma unroll
+    for (int d = 0; d < 2; ++d) {
+        uint32_t acc = 0;
+        acc = __builtin_amdgcn_cvt_pk_u8_f32(qcode_biased<T, 0>(v[2 * d], inv, ns), 0, acc);
+        acc = __builtin_amdgcn_cvt_pk_u8_f32(qcode_biased<T, 1>(v[2 * d], inv, ns), 1, acc);
+        acc = __builtin_amdgcn_cvt_pk_u8_f32(qcode_biased<T, 0>(v[2 * d + 1], inv, ns), 2, acc);
+        acc = __builtin_amdgcn_cvt_pk_u8_f32(qcode_biased<T, 1>(v[2 * d + 1], inv, ns), 3, acc);
+        out[d] = acc ^ 0x80808080u;
+    }
+    return out;
+}
+
+// Scalar form of the same code (for element-wise fallback paths).
+__device__ __forceinline__ int qcode_int(float v, float inv, float ns) {
+    return static_cast<int>(qcode_biased_f32(v, inv, ns)) - 128;
+}
+
+// Largest |value| of the 8 elements of a 16-byte vector, as the 15-bit
+// magnitude pattern (for finite values |a| < |b| iff the patterns compare so).
+typedef uint16_t u16x2 __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ uint32_t absmax_bits8(const u32x4 v, uint32_t m) {
+    u16x2 a = __builtin_bit_cast(u16x2, v[0] & 0x7fff7fffu);
+    a = __builtin_elementwise_max(a, __builtin_bit_cast(u16x2, v[1] & 0x7fff7fffu));
+    a = __builtin_elementwise_max(a, __builtin_bit_cast(u16x2, v[2] & 0x7fff7fffu));
+    a = __builtin_elementwise_max(a, __builtin_bit_cast(u16x2, v[3] & 0x7fff7fffu));
+    const uint32_t r = a[0] > a[1] ? a[0] : a[1];
+    return r > m ? r : m;
+}
+
+// ---------------------------------------------------------------------------
 // 16-byte global memory access. Streaming variants mark the access
 // non-temporal so single-use data does not displace reused lines.
 // ---------------------------------------------------------------------------

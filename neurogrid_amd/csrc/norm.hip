@@ -11,7 +11,14 @@
 // (gpu/cuda/kernels.cu:58-95 and 196-235; bf16_utils.cu:57-93).
 // Quantisation of a row v (v = y for the fused kernels, v = x otherwise):
 //   m = max|v_i|, scale = m / 127 (1 if 0), q_i = clamp(rint(v_i / scale), +-127)
-// (reference: quantize.cu:274-316, with half-to-even rounding).
+// (reference: quantize.cu:274-316, with half-to-even rounding), where
+// v_i / scale is the IEEE quotient, obtained without a division (qcode8).
+//
+// Every element-wise step is a single fp32 rounding; for fp16 rows the steps
+// read their fp16 operands directly (v_fma_mix_f32, see el_mul / el_add), so
+// the kernels spend about 6 VALU operations per element (13 with int8 codes)
+// and stay under the HBM time. The sum of squares runs in fp64 (exact
+// squares, error-free combination across lanes and waves).
 //
 // Layout: one workgroup per row, the row held in registers. Lane l of a
 // workgroup of nthr threads owns the 16-byte vectors l, l + nthr, ...; a row
@@ -39,19 +46,6 @@ struct RowArgs {
     float eps;
 };
 
-// Quantise one element given the row scale and its reciprocal. The product
-// with the reciprocal decides rint(v / scale) unless it lies within 2^-14 of
-// a half-integer; those elements take the IEEE quotient.
-__device__ __forceinline__ int quant_code(float v, float scale, float inv) {
-    float z = v * inv;
-    const float fr = z - floorf(z);
-    const bool near_tie = fabsf(fr - 0.5f) < 0x1p-14f;
-    if (__builtin_expect(near_tie, 0)) z = v / scale;
-    float q = __builtin_rintf(z);
-    q = fminf(fmaxf(q, -127.0f), 127.0f);
-    return static_cast<int>(q);
-}
-
 template <int V>
 struct MaxThreads {
     static constexpr int value = V <= 4 ? 1024 : 256;
@@ -74,21 +68,44 @@ __global__ __launch_bounds__(MaxThreads<V>::value) void row_kernel(RowArgs a) {
     const uint16_t* rr = ADD ? static_cast<const uint16_t*>(a.res) + rowoff : nullptr;
     const uint16_t* wr = static_cast<const uint16_t*>(a.w);
 
-    // All of the row's loads are issued before any arithmetic.
+    // All of the row's loads are issued before any arithmetic, unconditionally,
+    // so that the reduction consumes each vector as it arrives. With
+    // V = ceil(nvec / nthr) only the last vector of a lane can lie past the
+    // row end: it is loaded from a clamped (valid) index, zeroed, and never
+    // stored. A clamped load may read a vector another wave of the workgroup
+    // later overwrites in place; that wave stores only after the workgroup
+    // barrier of the reduction, by which point every load has been consumed.
     u32x4 xv[V], rv[V], wv[V];
     bool act[V];
 #pragma unroll
     for (int k = 0; k < V; ++k) {
         const int vi = tid + k * nthr;
-        act[k] = vi < a.nvec;
-        xv[k] = act[k] ? ld16_stream(xr + vi * 8) : u32x4{0, 0, 0, 0};
-        if (ADD) rv[k] = act[k] ? ld16_stream(rr + vi * 8) : u32x4{0, 0, 0, 0};
+        act[k] = k < V - 1 || vi < a.nvec;
+        const int vc = act[k] ? vi : a.nvec - 1;
+        xv[k] = ld16_stream(xr + vc * 8);
+        if (ADD) rv[k] = ld16_stream(rr + vc * 8);
     }
-    if (NORM) {
+    // The weight row is the same for every row of the grid. Plain RMSNorm
+    // loads it only after the reduction: issued at kernel start by every
+    // wave at once, these loads all land on the same few L2 lines and slow
+    // the row loads behind them (measured on MI355X: 13.5 vs 10.8 us for
+    // T = H = 4096); the residual and quantising variants, which have more
+    // work after the reduction, are faster with the weights loaded early.
+    constexpr bool kWeightsLate = NORM && !ADD && !QUANT;
+    if (NORM && !kWeightsLate) {
 #pragma unroll
         for (int k = 0; k < V; ++k) {
             const int vi = tid + k * nthr;
-            wv[k] = act[k] ? ld16(wr + vi * 8) : u32x4{0, 0, 0, 0};
+            wv[k] = ld16(wr + (act[k] ? vi : a.nvec - 1) * 8);
+        }
+    }
+    // Keep the scheduler from sinking any of these loads below the arithmetic.
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int k = 0; k < V; ++k) {
+        if (!act[k]) {
+            xv[k] = u32x4{0, 0, 0, 0};
+            if (ADD) rv[k] = u32x4{0, 0, 0, 0};
         }
     }
 
@@ -99,21 +116,21 @@ __global__ __launch_bounds__(MaxThreads<V>::value) void row_kernel(RowArgs a) {
         double acc[4] = {0.0, 0.0, 0.0, 0.0};
 #pragma unroll
         for (int k = 0; k < V; ++k) {
-            float fx[8];
-            unpack8<T>(xv[k], fx);
-            if (ADD) {
-                float fr[8];
-                unpack8<T>(rv[k], fr);
 #pragma unroll
-                for (int i = 0; i < 8; ++i) fx[i] = fx[i] + fr[i];
-                ov[k] = pack8<T>(fx);
-            } else {
-                ov[k] = xv[k];
-            }
-#pragma unroll
-            for (int i = 0; i < 8; ++i) {
-                const double d = static_cast<double>(fx[i]);
-                acc[i & 3] = __builtin_fma(d, d, acc[i & 3]);
+            for (int i = 0; i < 4; ++i) {
+                float s0, s1;
+                if (ADD) {
+                    s0 = el_add<T, 0>(xv[k][i], rv[k][i]);
+                    s1 = el_add<T, 1>(xv[k][i], rv[k][i]);
+                    ov[k][i] = pack2<T>(s0, s1);
+                } else {
+                    s0 = el_get<T, 0>(xv[k][i]);
+                    s1 = el_get<T, 1>(xv[k][i]);
+                    ov[k][i] = xv[k][i];
+                }
+                const double d0 = static_cast<double>(s0), d1 = static_cast<double>(s1);
+                acc[(2 * i) & 3] = __builtin_fma(d0, d0, acc[(2 * i) & 3]);
+                acc[(2 * i + 1) & 3] = __builtin_fma(d1, d1, acc[(2 * i + 1) & 3]);
             }
         }
         // Keep only the packed row live across the reduction: the second pass
@@ -185,17 +202,24 @@ __global__ __launch_bounds__(MaxThreads<V>::value) void row_kernel(RowArgs a) {
         for (int k = 0; k < V; ++k) ov[k] = xv[k];
     }
 
-    // Second pass: y = RN_T((o * r) * w), or v = x when only quantising.
+    // Second pass: y = RN_T(RN(o * r) * w), or v = x when only quantising.
+    if (kWeightsLate) {
+#pragma unroll
+        for (int k = 0; k < V; ++k) {
+            const int vi = tid + k * nthr;
+            wv[k] = ld16(wr + (act[k] ? vi : a.nvec - 1) * 8);
+        }
+    }
     u32x4 yv[V];
     if (NORM) {
 #pragma unroll
         for (int k = 0; k < V; ++k) {
-            float fo[8], fw[8], fy[8];
-            unpack8<T>(ov[k], fo);
-            unpack8<T>(wv[k], fw);
 #pragma unroll
-            for (int i = 0; i < 8; ++i) fy[i] = (fo[i] * r) * fw[i];
-            yv[k] = pack8<T>(fy);
+            for (int i = 0; i < 4; ++i) {
+                const float y0 = el_mul<T, 0>(wv[k][i], el_mul<T, 0>(ov[k][i], r));
+                const float y1 = el_mul<T, 1>(wv[k][i], el_mul<T, 1>(ov[k][i], r));
+                yv[k][i] = pack2<T>(y0, y1);
+            }
         }
     } else {
 #pragma unroll
@@ -210,17 +234,10 @@ __global__ __launch_bounds__(MaxThreads<V>::value) void row_kernel(RowArgs a) {
         return;
     }
 
-    // Row absmax on the 16-bit patterns: for finite values |v| orders like
-    // the integer (bits & 0x7fff).
+    // Row absmax on the 16-bit patterns (inactive vectors hold zeros).
     uint32_t mx = 0;
 #pragma unroll
-    for (int k = 0; k < V; ++k) {
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            mx = umax32(mx, yv[k][i] & 0x7fffu);
-            mx = umax32(mx, (yv[k][i] >> 16) & 0x7fffu);
-        }
-    }
+    for (int k = 0; k < V; ++k) mx = absmax_bits8(act[k] ? yv[k] : u32x4{0, 0, 0, 0}, mx);
     mx = wave_max_u32_dpp(mx);
     if (nw > 1) {
         if (lane == 0) s_max[wid] = mx;
@@ -237,15 +254,8 @@ __global__ __launch_bounds__(MaxThreads<V>::value) void row_kernel(RowArgs a) {
     int8_t* qr = a.q + rowoff;
 #pragma unroll
     for (int k = 0; k < V; ++k) {
-        float fy[8];
-        unpack8<T>(yv[k], fy);
-        uint32_t c[2] = {0, 0};
-#pragma unroll
-        for (int i = 0; i < 8; ++i) {
-            const uint32_t b = static_cast<uint32_t>(quant_code(fy[i], scale, inv)) & 0xffu;
-            c[i >> 2] |= b << ((i & 3) * 8);
-        }
-        if (act[k]) __builtin_nontemporal_store(u32x2{c[0], c[1]}, reinterpret_cast<u32x2*>(qr + (tid + k * nthr) * 8));
+        const u32x2 c = qcode8<T>(yv[k], inv, -scale);
+        if (act[k]) __builtin_nontemporal_store(c, reinterpret_cast<u32x2*>(qr + (tid + k * nthr) * 8));
     }
 }
 
@@ -353,7 +363,7 @@ __global__ __launch_bounds__(256) void row_kernel_scalar(RowArgs a) {
         const uint16_t vb = vbits(i);
         const uint16_t rb = ADD ? from_f32<T>(sval(i)) : 0;
         if (ADD) ror[i] = rb;
-        qr[i] = static_cast<int8_t>(quant_code(to_f32<T>(vb), scale, inv));
+        qr[i] = static_cast<int8_t>(qcode_int(to_f32<T>(vb), inv, -scale));
     }
 }
 

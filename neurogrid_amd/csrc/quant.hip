@@ -25,13 +25,8 @@ __device__ __forceinline__ float scale_from_bits(uint32_t mbits) {
     return s == 0.0f ? 1.0f : s;
 }
 
-__device__ __forceinline__ int qcode(float v, float scale, float inv) {
-    float z = v * inv;
-    const float fr = z - floorf(z);
-    const bool near_tie = fabsf(fr - 0.5f) < 0x1p-14f;
-    if (__builtin_expect(near_tie, 0)) z = v / scale;
-    return static_cast<int>(fminf(fmaxf(__builtin_rintf(z), -127.0f), 127.0f));
-}
+// q = clamp(rint(RN(v / scale)), -127, 127) without a division (qcode_int).
+__device__ __forceinline__ int qcode(float v, float scale, float inv) { return qcode_int(v, inv, -scale); }
 
 __global__ void fill_u32_kernel(uint32_t* p, size_t n, uint32_t v) {
     const size_t stride = static_cast<size_t>(gridDim.x) * blockDim.x;
