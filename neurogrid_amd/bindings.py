@@ -4,8 +4,8 @@ The reference's Go host calls ``libgpu_engine.so`` through cgo wrappers in
 ``gpu/bindings/gpu.go``. Go is not available here, so this module restates
 those wrappers over the same C ABI with ctypes: same names, same argument
 meaning and shape derivations, same error text (a Go ``error`` becomes a
-raised :class:`GPUError`). The Go side stays unchanged in a real deployment;
-see INTEGRATION.md for the cgo binding.
+raised :class:`GPUError`). The Go side stays unchanged in a real deployment:
+its cgo wrappers link this library in place of the CUDA build.
 
 Reference wrappers restated here (gpu/bindings/gpu.go):
   InitGPU :73, ShutdownGPU :82, GetDeviceCount :87, SetDevice :97,

@@ -13,7 +13,9 @@
 // S differs from the exact sum by less than m 2^-53 S (1 + 2^-40). With
 // k = ceil(log2 m) + 1, the interval S (1 +- 2^(k-53)) contains the exact sum;
 // when both of its ends round to the same fp32 value, that value is
-// RN_f32(exact sum). Otherwise (about 2^(k-23) of rows) the slow path runs.
+// RN_f32(exact sum). Otherwise (a fraction of about 2^(k-29) of rows: the
+// interval is 2^(k-52) S wide, fp32 values are about 2^-23 S apart) the slow
+// path runs.
 //
 // Slow path. A value v on the 2^-24 grid with |v| < 2^17 (every value derived
 // from fp16 inputs) has v^2 = t 2^16 + u 2^-16 + w 2^-48 with integers
