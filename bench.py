@@ -52,7 +52,8 @@ from neurogrid_amd.device import DeviceBuffer as DB  # noqa: E402
 
 PEAK_GBPS = 8000.0  # MI355X HBM3E, AMD published
 METRIC = "fused-kernel HBM GB/s (% of peak) + µs/layer at Mistral-7B shapes"
-ROTATE_BYTES = 1536 << 20  # rotating working set, > 6x the 256 MB MALL
+ROTATE_BYTES = 1536 << 20  # layer-step rotation: > 6x the 256 MB Infinity Cache
+POOL_BYTES = 1 << 30       # per-kernel pools: bytes touched between reuses of a buffer
 TRAFFIC_FILE = ROOT / "profiles" / "traffic_mistral7b_prefill.json"
 
 
@@ -194,6 +195,68 @@ def layer_launches(L, cfg, s):
     ]
 
 
+class Pool:
+    """`n` copies of one buffer in one device allocation (slot j at offset
+    j * slot bytes), all holding the same initial data, so that a kernel can be
+    launched over many distinct buffers."""
+
+    def __init__(self, hip, slot_bytes, n, init=None):
+        self.slot = -(-int(slot_bytes) // 256) * 256
+        self.n = n
+        self.buf = DB(self.slot * n)
+        if init is not None:
+            self.buf.upload(init)
+            for j in range(1, n):
+                hip.check(hip.h.hipMemcpyAsync(self.at(j), self.at(0), int(slot_bytes), 3, None), "hipMemcpyAsync")
+            hip.sync()
+
+    def at(self, j):
+        return self.buf.offset((j % self.n) * self.slot)
+
+    def free(self):
+        self.buf.free()
+
+
+def pool_slots(footprint_bytes, min_slots=3, max_slots=512):
+    """Slots so that at least POOL_BYTES of other buffers are touched between
+    two launches on the same slot (the Infinity Cache is 256 MB)."""
+    return int(min(max_slots, max(min_slots, -(-POOL_BYTES // int(footprint_bytes)) + 1)))
+
+
+def kernel_pools_for(L, hip, cfg, d, shared):
+    """Yield (name, make) per layer kernel; make() allocates that kernel's
+    buffer pools and returns (thunks, pools), one thunk per pool slot."""
+    T, H, I, D, e = cfg.T, cfg.H, cfg.I, cfg.D, cfg.e
+    eps, theta = C.c_float(cfg.eps), C.c_float(cfg.theta)
+    bf = cfg.dtype == "bf16"
+    rms = L.cuda_bf16_rmsnorm if bf else L.cuda_rmsnorm
+    rope = L.cuda_bf16_rope_with_theta if bf else L.cuda_rope_with_theta
+    addn = L.ng_bf16_add_rmsnorm if bf else L.cuda_add_rmsnorm
+    swig = L.ng_bf16_silu_mul if bf else L.cuda_silu_mul
+    add = L.cuda_bf16_add if bf else L.cuda_add
+    th = T * H * e
+    tq, tk, ti = T * cfg.nq * D * e, T * cfg.nkv * D * e, T * I * e
+
+    def mk(name, footprint, specs, launch):
+        def make():
+            n = pool_slots(footprint)
+            pools = [Pool(hip, nbytes, n, init) for nbytes, init in specs]
+            thunks = [(name, (lambda j=j: launch(*[p.at(j) for p in pools]))) for j in range(n)]
+            return thunks, pools
+        return name, make
+
+    yield mk("rmsnorm", 2 * th, [(th, d["x"]), (th, None)],
+             lambda x, y: rms(y, x, shared["w_attn"].vp, T, H, eps))
+    yield mk("rope_q", tq, [(tq, d["q"])], lambda q: rope(q, q, shared["pos"].ip, 1, T, cfg.nq, D, 0, theta))
+    yield mk("rope_k", tk, [(tk, d["k"])], lambda k: rope(k, k, shared["pos"].ip, 1, T, cfg.nkv, D, 0, theta))
+    yield mk("add_rmsnorm", 4 * th, [(th, d["x"]), (th, d["residual"]), (th, None), (th, None)],
+             lambda x, r, ro, y: addn(y, ro, x, r, shared["w_ffn"].vp, T, H, eps))
+    yield mk("silu_mul", 3 * ti, [(ti, d["gate"]), (ti, d["up"]), (ti, None)],
+             lambda g, u, o: swig(o, g, u, T * I))
+    yield mk("add", 3 * th, [(th, d["x"]), (th, d["residual"]), (th, None)],
+             lambda a, b, o: add(o, a, b, T * H))
+
+
 def time_graph(hip, stream, graphs, reps, warmup=2):
     """Average event time (ms) of one replay of graphs[i % len(graphs)] over reps replays."""
     for i in range(warmup):
@@ -239,7 +302,7 @@ def run_layer(L, hip, stream, cfg, steps, warmup, kernel_launches=24, kernel_rep
     # One graph of `warmup` steps, replayed once untimed, then one graph of
     # exactly `steps` steps, replayed once between two events.
     warm_graph = hip.capture(stream, [t for i in range(max(warmup, 1)) for t in launches[i % nsets]])
-    timed_graph = hip.capture(stream, [t for i in range(steps) for t in launches[i % nsets]])
+    timed_graph = hip.capture(stream, [t for i in range(warmup, warmup + steps) for t in launches[i % nsets]])
     warm_graph.launch(stream)
     hip.sync()
     t0 = time.perf_counter()
@@ -248,16 +311,29 @@ def run_layer(L, hip, stream, cfg, steps, warmup, kernel_launches=24, kernel_rep
     warm_graph.destroy()
     timed_graph.destroy()
 
-    per = {}
-    for j, n in enumerate(names):
-        g = kernel_graph(hip, stream, [lset[j] for lset in launches], kernel_launches)
-        per[n] = time_graph(hip, stream, [g], kernel_reps, 1) * 1e3 / kernel_launches
-        g.destroy()
     for s in sets:
         s.free()
+
+    # Per-kernel: each kernel over its own pool of buffers (see Pool).
+    d = W.make_layer_inputs(cfg, seed=0, with_table=False)
+    per, slots = {}, {}
+    for name, make in kernel_pools_for(L, hip, cfg, d, shared):
+        thunks, pools = make()
+        for t_name, fn in thunks:
+            if fn() != 0:
+                raise RuntimeError(f"{t_name} failed")
+        hip.sync()
+        n = max(kernel_launches, len(thunks))
+        g = kernel_graph(hip, stream, thunks, n)
+        per[name] = time_graph(hip, stream, [g], kernel_reps, 1) * 1e3 / n
+        slots[name] = len(thunks)
+        g.destroy()
+        for p in pools:
+            p.free()
+    del d
     for b in shared.values():
         b.free()
-    return step_ms, wall_ms, per, nsets
+    return step_ms, wall_ms, per, nsets, slots
 
 
 # ----------------------------------------------------------------------------- other kernels
@@ -274,52 +350,73 @@ def time_kernel(hip, stream, fns, launches=24, reps=4):
     return us
 
 
+def time_pool_kernel(hip, stream, thunks, launches=24, reps=4):
+    """Average duration (us) of `thunks` (one per buffer slot) cycled back-to-back in one graph."""
+    for _, f in thunks:
+        if f() != 0:
+            raise RuntimeError("kernel failed")
+    hip.sync()
+    n = max(launches, len(thunks))
+    g = kernel_graph(hip, stream, thunks, n)
+    us = time_graph(hip, stream, [g], reps, 1) * 1e3 / n
+    g.destroy()
+    return us
+
+
 def extra_kernels(L, hip, stream):
     out = {}
-    # embedding gather at Mistral-7B prefill (per forward pass)
+    # Embedding gather at Mistral-7B prefill (per forward pass): 8 copies of
+    # the [32000, 4096] fp16 table (262 MB each) and a distinct id vector per
+    # launch, so rows come from HBM rather than the Infinity Cache.
     cfg = W.CONFIGS["mistral7b_prefill"]
     rng = np.random.Generator(np.random.PCG64(0))
     table = W.round_to(rng.standard_normal((cfg.vocab, cfg.H), dtype=np.float32) * np.float32(0.02), "f16")
-    tb = DB.from_array(table)
+    ntab, nids = 8, 24
+    tabs = Pool(hip, table.nbytes, ntab, table)
     del table
-    nb = 4
-    ids = [DB.from_array(rng.integers(0, cfg.vocab, cfg.T).astype(np.int32)) for _ in range(nb)]
-    outs = [DB(2 * cfg.T * cfg.H) for _ in range(nb)]
-    fns = [lambda i=i: L.cuda_gather_embeddings(outs[i].vp, tb.vp, ids[i].ip, cfg.H, cfg.T) for i in range(nb)]
-    us = time_kernel(hip, stream, fns)
+    ids = Pool(hip, 4 * cfg.T, nids)
+    assert ids.slot == 4 * cfg.T  # slots are contiguous, so one upload fills every slot
+    ids.buf.upload(np.stack([rng.integers(0, cfg.vocab, cfg.T).astype(np.int32) for _ in range(nids)]))
+    outs = Pool(hip, 2 * cfg.T * cfg.H, 8)
+    ipt = lambda j: C.cast(ids.at(j), C.POINTER(C.c_int))
+    thunks = [("gather", (lambda j=j: L.cuda_gather_embeddings(outs.at(j), tabs.at(j), ipt(j), cfg.H, cfg.T)))
+              for j in range(nids)]
+    us = time_pool_kernel(hip, stream, thunks)
     b = W.layer_bytes(cfg)["gather"]
     out["gather_mistral7b_prefill"] = {"us": us, "GBps": b / us / 1e3, "frac": b / us / 1e3 / PEAK_GBPS,
-                                       "bytes": b, "note": "table [32000,4096] fp16 (262 MB), uniform ids"}
-    for x in ids + outs + [tb]:
-        x.free()
+                                       "bytes": b, "buffer_sets": f"{ntab} tables, {nids} id vectors",
+                                       "note": "table [32000,4096] fp16 (262 MB), uniform ids"}
+    for p in (tabs, ids, outs):
+        p.free()
 
-    # fused RMSNorm + per-token int8, and int8 weight dequant (quant config)
+    # Fused RMSNorm + per-token int8, and int8 weight dequant (quant config).
     q = W.make_quant_inputs(seed=0)
     qb = W.quant_bytes()
-    nb = 8
-    xs = [DB.from_array(q["x"]) for _ in range(nb)]
-    wb = DB.from_array(q["w"])
-    codes = [DB(q["x"].size) for _ in range(nb)]
-    scl = [DB(4 * W.QUANT_T) for _ in range(nb)]
     eps = C.c_float(1e-5)
-    fns = [lambda i=i: L.ng_rmsnorm_quant_int8(codes[i].vp, scl[i].vp, xs[i].vp, wb.vp, W.QUANT_T, W.QUANT_H, eps)
-           for i in range(nb)]
-    us = time_kernel(hip, stream, fns)
     b = qb["rmsnorm_quant"]
-    out["rmsnorm_quant_int8"] = {"us": us, "GBps": b / us / 1e3, "frac": b / us / 1e3 / PEAK_GBPS, "bytes": b}
-    for x in xs + codes + scl + [wb]:
-        x.free()
-    nb = 3
-    wq = [DB.from_array(q["wq"]) for _ in range(nb)]
-    ws = DB.from_array(q["wscale"])
-    wo = [DB(2 * q["wq"].size) for _ in range(nb)]
-    fns = [lambda i=i: L.cuda_dequantize_weights(wo[i].vp, wq[i].vp, ws.vp, W.QUANT_WN, W.QUANT_WK, 1)
-           for i in range(nb)]
-    us = time_kernel(hip, stream, fns)
+    n = pool_slots(b)
+    xs, codes, scl = Pool(hip, q["x"].nbytes, n, q["x"]), Pool(hip, q["x"].size, n), Pool(hip, 4 * W.QUANT_T, n)
+    wb = DB.from_array(q["w"])
+    thunks = [("rmsnorm_quant", (lambda j=j: L.ng_rmsnorm_quant_int8(codes.at(j), scl.at(j), xs.at(j), wb.vp,
+                                                                     W.QUANT_T, W.QUANT_H, eps))) for j in range(n)]
+    us = time_pool_kernel(hip, stream, thunks)
+    out["rmsnorm_quant_int8"] = {"us": us, "GBps": b / us / 1e3, "frac": b / us / 1e3 / PEAK_GBPS, "bytes": b,
+                                 "buffer_sets": n}
+    for p in (xs, codes, scl):
+        p.free()
+    wb.free()
     b = qb["dequant"]
-    out["dequant_int8_weights"] = {"us": us, "GBps": b / us / 1e3, "frac": b / us / 1e3 / PEAK_GBPS, "bytes": b}
-    for x in wq + wo + [ws]:
-        x.free()
+    n = pool_slots(b)
+    wq, wo = Pool(hip, q["wq"].nbytes, n, q["wq"]), Pool(hip, 2 * q["wq"].size, n)
+    ws = DB.from_array(q["wscale"])
+    thunks = [("dequant", (lambda j=j: L.cuda_dequantize_weights(wo.at(j), wq.at(j), ws.vp, W.QUANT_WN, W.QUANT_WK,
+                                                                1))) for j in range(n)]
+    us = time_pool_kernel(hip, stream, thunks)
+    out["dequant_int8_weights"] = {"us": us, "GBps": b / us / 1e3, "frac": b / us / 1e3 / PEAK_GBPS, "bytes": b,
+                                   "buffer_sets": n}
+    for p in (wq, wo):
+        p.free()
+    ws.free()
     return out
 
 
@@ -432,13 +529,14 @@ def main():
 
     cfg = W.CONFIGS[args.config]
     log(f"layer {cfg.key}: {args.warmup} warmup + {args.steps} timed graph replays")
-    step_ms, wall_ms, per, nsets = run_layer(L, hip, stream, cfg, args.steps, args.warmup)
+    step_ms, wall_ms, per, nsets, slots = run_layer(L, hip, stream, cfg, args.steps, args.warmup)
     lb = W.layer_bytes(cfg)
     layer_bytes = sum(lb[k] for k in W.LAYER_KERNELS)
     kernels = {}
     for k in W.LAYER_KERNELS:
         us = per[k]
-        kernels[k] = {"us": us, "GBps": lb[k] / us / 1e3, "frac": lb[k] / us / 1e3 / PEAK_GBPS, "bytes": lb[k]}
+        kernels[k] = {"us": us, "GBps": lb[k] / us / 1e3, "frac": lb[k] / us / 1e3 / PEAK_GBPS, "bytes": lb[k],
+                      "buffer_sets": slots[k]}
     us_layer = sum(kernels[k]["us"] for k in W.LAYER_KERNELS)
     log(f"layer done: {us_layer:.1f} us summed kernel time, {step_ms * 1e3:.1f} us per step")
 
@@ -447,7 +545,7 @@ def main():
         for key in ("mistral7b_decode", "llama2_13b_prefill", "mistral_nemo_bf16"):
             log(f"layer {key}")
             c2 = W.CONFIGS[key]
-            s2, _, p2, _ = run_layer(L, hip, stream, c2, 20, 3)
+            s2, _, p2, _, _ = run_layer(L, hip, stream, c2, 20, 3)
             lb2 = W.layer_bytes(c2)
             b2 = sum(lb2[k] for k in W.LAYER_KERNELS)
             u2 = sum(p2.values())

@@ -11,10 +11,13 @@ namespace ng {
 
 constexpr int kGatherThreads = 256;
 constexpr int kGatherRowsPerBlock = kGatherThreads / kWave;
-constexpr int kGatherUnroll = 4;
+constexpr int kGatherChunk = 8;  // 16-byte vectors per lane loaded before any store
 
 // vocab > 0 turns on the range check: rows whose id is outside [0, vocab)
-// are zero-filled and counted in *bad.
+// are zero-filled and counted in *bad. Each chunk of up to 8 vectors per lane
+// is loaded in full before it is stored (unconditional loads from clamped
+// indices, predicated stores), so a row of up to 1024 elements is one load
+// phase and one store phase.
 __global__ __launch_bounds__(kGatherThreads) void gather_vec_kernel(void* out, const void* table, const int* ids,
                                                                    int T, int nvec, int vocab, int* bad) {
     const int lane = threadIdx.x & 63;
@@ -28,16 +31,16 @@ __global__ __launch_bounds__(kGatherThreads) void gather_vec_kernel(void* out, c
         return;
     }
     const u32x4* src = reinterpret_cast<const u32x4*>(table) + static_cast<size_t>(id) * nvec;
-    for (int v0 = lane; v0 < nvec; v0 += kWave * kGatherUnroll) {
-        u32x4 r[kGatherUnroll];
+    for (int v0 = 0; v0 < nvec; v0 += kWave * kGatherChunk) {
+        u32x4 r[kGatherChunk];
 #pragma unroll
-        for (int k = 0; k < kGatherUnroll; ++k) {
-            const int v = v0 + k * kWave;
-            if (v < nvec) r[k] = ld16(src + v);
+        for (int k = 0; k < kGatherChunk; ++k) {
+            const int v = v0 + lane + k * kWave;
+            r[k] = ld16(src + (v < nvec ? v : nvec - 1));
         }
 #pragma unroll
-        for (int k = 0; k < kGatherUnroll; ++k) {
-            const int v = v0 + k * kWave;
+        for (int k = 0; k < kGatherChunk; ++k) {
+            const int v = v0 + lane + k * kWave;
             if (v < nvec) st16_stream(dst + v, r[k]);
         }
     }

@@ -168,44 +168,44 @@ __global__ void col_scale_finalize_kernel(float* scales, int N) {
 // ---- dequantisation ----------------------------------------------------------
 enum DqMode : int { DQ_ROW = 0, DQ_COL = 1, DQ_TENSOR = 2 };
 
-// Vector path: one 16-byte int8 load -> two 16-byte fp16 stores.
-// Workgroup grid: x over the 16-code groups of a row, y over rows.
+// Vector path: one 16-byte int8 load -> two 16-byte fp16 stores, one group
+// of 16 codes per thread over a flat grid (every group of the matrix has its
+// own thread). groups_per_row = cols / 16; the row of group g is
+// g / groups_per_row (a run-time-constant division).
 template <int MODE>
 __global__ __launch_bounds__(kQThreads) void dequant_vec_kernel(uint16_t* out, const int8_t* q, const float* scales,
-                                                                int rows, int cols) {
-    const int g = blockIdx.x * kQThreads + threadIdx.x;  // group of 16 within the row
-    const int ngroups = cols / 16;
+                                                                uint32_t ngroups, FastDiv gpr) {
+    const uint32_t g = blockIdx.x * kQThreads + threadIdx.x;
     if (g >= ngroups) return;
-    const float ts = MODE == DQ_TENSOR ? scales[0] : 0.0f;
-    for (int r = blockIdx.y; r < rows; r += gridDim.y) {
-        const size_t e0 = static_cast<size_t>(r) * cols + static_cast<size_t>(g) * 16;
-        const u32x4 v = ld16_stream(q + e0);
-        float s[16];
-        if (MODE == DQ_ROW) {
-            const float rs = scales[r];
+    const size_t e0 = static_cast<size_t>(g) * 16;
+    const u32x4 v = ld16_stream(q + e0);
+    float s[16];
+    if (MODE == DQ_ROW) {
+        const float rs = scales[fdiv(g, gpr)];
 #pragma unroll
-            for (int e = 0; e < 16; ++e) s[e] = rs;
-        } else if (MODE == DQ_COL) {
+        for (int e = 0; e < 16; ++e) s[e] = rs;
+    } else if (MODE == DQ_COL) {
+        const uint32_t cg = g - fdiv(g, gpr) * gpr.d;  // group within the row
 #pragma unroll
-            for (int k = 0; k < 4; ++k) {
-                const u32x4 sv = ld16(scales + g * 16 + 4 * k);
+        for (int k = 0; k < 4; ++k) {
+            const u32x4 sv = ld16(scales + cg * 16 + 4 * k);
 #pragma unroll
-                for (int e = 0; e < 4; ++e) s[4 * k + e] = as_float(sv[e]);
-            }
-        } else {
-#pragma unroll
-            for (int e = 0; e < 16; ++e) s[e] = ts;
+            for (int e = 0; e < 4; ++e) s[4 * k + e] = as_float(sv[e]);
         }
-        float lo[8], hi[8];
+    } else {
+        const float ts = scales[0];
 #pragma unroll
-        for (int e = 0; e < 16; ++e) {
-            const int8_t c = static_cast<int8_t>((v[e >> 2] >> ((e & 3) * 8)) & 0xffu);
-            const float f = static_cast<float>(c) * s[e];
-            if (e < 8) lo[e] = f; else hi[e - 8] = f;
-        }
-        st16_stream(out + e0, pack8<f16>(lo));
-        st16_stream(out + e0 + 8, pack8<f16>(hi));
+        for (int e = 0; e < 16; ++e) s[e] = ts;
     }
+    float lo[8], hi[8];
+#pragma unroll
+    for (int e = 0; e < 16; ++e) {
+        const int8_t c = static_cast<int8_t>((v[e >> 2] >> ((e & 3) * 8)) & 0xffu);
+        const float f = static_cast<float>(c) * s[e];
+        if (e < 8) lo[e] = f; else hi[e - 8] = f;
+    }
+    st16_stream(out + e0, pack8<f16>(lo));
+    st16_stream(out + e0 + 8, pack8<f16>(hi));
 }
 
 template <int MODE>
@@ -225,13 +225,13 @@ template <int MODE>
 static int launch_dequant(const char* name, void* out, const void* q, const void* scales, size_t rows, size_t cols) {
     const size_t n = rows * cols;
     const bool vec = cols % 16 == 0 && aligned16(out) && aligned16(q) && (MODE != DQ_COL || aligned16(scales)) &&
-                     rows < (1ull << 31) && cols < (1ull << 31);
+                     n / 16 < (1ull << 32) && cols / 16 < (1ull << 31);
     if (vec) {
-        const unsigned gx = static_cast<unsigned>((cols / 16 + kQThreads - 1) / kQThreads);
-        const unsigned gy = static_cast<unsigned>(rows < 65535 ? rows : 65535);
-        dequant_vec_kernel<MODE><<<dim3(gx, gy), dim3(kQThreads), 0, stream()>>>(
-            static_cast<uint16_t*>(out), static_cast<const int8_t*>(q), static_cast<const float*>(scales),
-            static_cast<int>(rows), static_cast<int>(cols));
+        const uint32_t ngroups = static_cast<uint32_t>(n / 16);
+        const unsigned blocks = static_cast<unsigned>((ngroups + kQThreads - 1) / kQThreads);
+        dequant_vec_kernel<MODE><<<dim3(blocks), dim3(kQThreads), 0, stream()>>>(
+            static_cast<uint16_t*>(out), static_cast<const int8_t*>(q), static_cast<const float*>(scales), ngroups,
+            make_fastdiv(static_cast<uint32_t>(cols / 16)));
     } else {
         size_t blocks = (n + kQThreads - 1) / kQThreads;
         if (blocks > 65536) blocks = 65536;

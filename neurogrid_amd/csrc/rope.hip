@@ -117,6 +117,108 @@ __global__ __launch_bounds__(kRopeThreads) void rope_vec_kernel(RopeArgs a) {
     }
 }
 
+// Wave-per-token kernel, for head_dim 64, 128 or 256 (16-byte aligned).
+// A wave rotates HPL passes of heads of one token; a pass covers 64 / lph
+// heads, lph lanes per head (split-half: lane j of a head owns vector j of
+// each half, pairs 8j..8j+7; interleaved: vector j, pairs 4j..4j+3). Lane l
+// evaluates (cos, sin) of pairs l and l + 64 once; the lanes that need them
+// fetch them with cross-lane shuffles, so each (token, pair) angle is
+// evaluated once per wave, with no LDS table and no workgroup barrier. All
+// loads are issued first, from clamped indices where a pass runs past the
+// last head; those vectors are not stored. When T is small, a token's passes
+// are split over G waves so that enough waves are in flight.
+struct RopeWaveArgs {
+    void* out;
+    const void* in;
+    const int* pos;
+    int T;
+    int nh;
+    int D;
+    int lph_log2;      // log2(lanes per head)
+    int G;             // waves per token
+    FastDiv div_G;
+    float inv_freq[kRopeMaxHalf];
+};
+
+template <typename T, int STYLE, int HPL>
+__global__ __launch_bounds__(kRopeThreads) void rope_wave_kernel(RopeWaveArgs a) {
+    const int lane = threadIdx.x & 63;
+    const uint32_t w = blockIdx.x * (kRopeThreads / kWave) + (threadIdx.x >> 6);
+    const int t = static_cast<int>(fdiv(w, a.div_G));
+    if (t >= a.T) return;
+    const int g = static_cast<int>(w) - t * a.G;
+    const int lph = 1 << a.lph_log2;
+    const int hpp = kWave >> a.lph_log2;
+    const int j = lane & (lph - 1);
+    const int hl = lane >> a.lph_log2;
+    const int half = a.D >> 1;
+    const size_t base = static_cast<size_t>(t) * a.nh * a.D;
+    const uint16_t* in = static_cast<const uint16_t*>(a.in) + base;
+    uint16_t* out = static_cast<uint16_t*>(a.out) + base;
+
+    u32x4 v1[HPL], v2[HPL];
+    int off[HPL];
+    bool ok[HPL];
+#pragma unroll
+    for (int k = 0; k < HPL; ++k) {
+        const int h = (g * HPL + k) * hpp + hl;
+        ok[k] = h < a.nh;
+        off[k] = (ok[k] ? h : a.nh - 1) * a.D + 8 * j;
+        v1[k] = ld16_stream(in + off[k]);
+        if (STYLE == 0) v2[k] = ld16_stream(in + off[k] + half);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+
+    const float p = static_cast<float>(__builtin_amdgcn_readfirstlane(a.pos[t]));
+    float s0, c0, s1 = 0.0f, c1 = 0.0f;
+    sincosf(p * a.inv_freq[lane < half ? lane : 0], &s0, &c0);
+    if (half > kWave) sincosf(p * a.inv_freq[lane + kWave < half ? lane + kWave : 0], &s1, &c1);
+
+    constexpr int NP = STYLE == 0 ? 8 : 4;  // pairs per lane
+    float c[NP], sn[NP];
+#pragma unroll
+    for (int e = 0; e < NP; ++e) {
+        const int pi = NP * j + e;
+        const int src = pi & (kWave - 1);
+        const float cl = __shfl(c0, src, kWave), sl = __shfl(s0, src, kWave);
+        if (half > kWave) {
+            const float ch = __shfl(c1, src, kWave), sh = __shfl(s1, src, kWave);
+            c[e] = pi < kWave ? cl : ch;
+            sn[e] = pi < kWave ? sl : sh;
+        } else {
+            c[e] = cl;
+            sn[e] = sl;
+        }
+    }
+
+#pragma unroll
+    for (int k = 0; k < HPL; ++k) {
+        if (STYLE == 0) {
+            float x1[8], x2[8], y1[8], y2[8];
+            unpack8<T>(v1[k], x1);
+            unpack8<T>(v2[k], x2);
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                y1[e] = x1[e] * c[e] - x2[e] * sn[e];
+                y2[e] = x1[e] * sn[e] + x2[e] * c[e];
+            }
+            if (ok[k]) {
+                st16_stream(out + off[k], pack8<T>(y1));
+                st16_stream(out + off[k] + half, pack8<T>(y2));
+            }
+        } else {
+            float x[8], y[8];
+            unpack8<T>(v1[k], x);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                y[2 * e] = x[2 * e] * c[e] - x[2 * e + 1] * sn[e];
+                y[2 * e + 1] = x[2 * e] * sn[e] + x[2 * e + 1] * c[e];
+            }
+            if (ok[k]) st16_stream(out + off[k], pack8<T>(y));
+        }
+    }
+}
+
 // Any head_dim and alignment: one thread per (token, head, pair).
 template <typename T>
 __global__ __launch_bounds__(kRopeThreads) void rope_scalar_kernel(RopeArgs a, int style) {
@@ -185,7 +287,46 @@ static int launch_rope(const char* name, void* output, const void* input, const 
 
     const bool aligned = aligned16(output) && aligned16(input);
     const bool vec = aligned && ((style == 0 && head_dim % 16 == 0) || (style == 1 && head_dim % 8 == 0));
-    if (vec) {
+    if (aligned && (head_dim == 64 || head_dim == 128 || head_dim == 256)) {
+        RopeWaveArgs w{};
+        w.out = output;
+        w.in = input;
+        w.pos = positions;
+        w.T = a.T;
+        w.nh = num_heads;
+        w.D = head_dim;
+        const int lph = style == 0 ? head_dim / 16 : head_dim / 8;
+        w.lph_log2 = __builtin_ctz(static_cast<unsigned>(lph));
+        const int hpp = kWave / lph;
+        const int npass = (num_heads + hpp - 1) / hpp;
+        // Waves per token: enough waves to cover the GPU at small T, at most
+        // one per pass, and at most 8 passes per wave.
+        const long long want = 8ll * device_cu_count();
+        int G = static_cast<int>((want + a.T - 1) / a.T);
+        if (G > npass) G = npass;
+        if (G < (npass + 7) / 8) G = (npass + 7) / 8;
+        if (G < 1) G = 1;
+        const int hpl = (npass + G - 1) / G;
+        G = (npass + hpl - 1) / hpl;
+        w.G = G;
+        w.div_G = make_fastdiv(static_cast<uint32_t>(G));
+        for (int i = 0; i < a.half; ++i) w.inv_freq[i] = a.inv_freq[i];
+        const long long waves = static_cast<long long>(a.T) * G;
+        NG_REQUIRE(waves < (1ll << 31), "%s: tensor too large", name);
+        const unsigned blocks = static_cast<unsigned>((waves + 3) / 4);
+        auto go = [&](auto kern) { kern<<<dim3(blocks), dim3(kRopeThreads), 0, stream()>>>(w); };
+#define NG_ROPE_WAVE(HPL)                                                 \
+    case HPL:                                                             \
+        if (style == 0) go(rope_wave_kernel<T, 0, HPL>);                  \
+        else go(rope_wave_kernel<T, 1, HPL>);                             \
+        break;
+        switch (hpl) {
+            NG_ROPE_WAVE(1) NG_ROPE_WAVE(2) NG_ROPE_WAVE(3) NG_ROPE_WAVE(4)
+            NG_ROPE_WAVE(5) NG_ROPE_WAVE(6) NG_ROPE_WAVE(7) NG_ROPE_WAVE(8)
+            default: NG_REQUIRE(false, "%s: internal: %d passes per wave", name, hpl);
+        }
+#undef NG_ROPE_WAVE
+    } else if (vec) {
         const int uph = style == 0 ? head_dim / 16 : head_dim / 8;
         a.upt = num_heads * uph;
         const long long units = static_cast<long long>(a.T) * a.upt;

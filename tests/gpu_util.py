@@ -74,4 +74,50 @@ def assert_bits_equal(got, ref, what: str = "") -> None:
                              f"got {got[tuple(idx[0])]} want {ref[tuple(idx[0])]}")
 
 
-__all__ = ["banner", "dev", "empty", "get", "ok", "f32", "ulp", "assert_close16", "assert_bits_equal", "sync", "C"]
+__all__ = ["banner", "dev", "empty", "get", "ok", "f32", "ulp", "assert_close16", "assert_bits_equal", "sync", "C",
+           "HipRuntime"]
+
+
+class HipRuntime:
+    """The few HIP runtime calls the graph-capture test needs (ctypes)."""
+
+    def __init__(self):
+        vp = C.c_void_p
+        self.h = C.CDLL("libamdhip64.so")
+        self.h.hipStreamBeginCapture.argtypes = [vp, C.c_int]
+        self.h.hipStreamEndCapture.argtypes = [vp, C.POINTER(vp)]
+        self.h.hipGraphInstantiate.argtypes = [C.POINTER(vp), vp, vp, vp, C.c_size_t]
+        self.h.hipGraphLaunch.argtypes = [vp, vp]
+        self.h.hipGraphExecDestroy.argtypes = [vp]
+        self.h.hipGraphDestroy.argtypes = [vp]
+        self.h.hipStreamSynchronize.argtypes = [vp]
+        self.h.hipStreamDestroy.argtypes = [vp]
+
+    def check(self, rc, what):
+        assert rc == 0, f"{what} failed with hipError {rc}"
+
+    def stream(self):
+        s = C.c_void_p()
+        self.check(self.h.hipStreamCreate(C.byref(s)), "hipStreamCreate")
+        return s
+
+    def capture(self, stream, fn):
+        """Capture the launches `fn` makes on `stream` (relaxed mode); returns (graph, exec)."""
+        self.check(self.h.hipStreamBeginCapture(stream, 2), "hipStreamBeginCapture")
+        try:
+            fn()
+        finally:
+            g = C.c_void_p()
+            rc = self.h.hipStreamEndCapture(stream, C.byref(g))
+        self.check(rc, "hipStreamEndCapture")
+        ex = C.c_void_p()
+        self.check(self.h.hipGraphInstantiate(C.byref(ex), g, None, None, 0), "hipGraphInstantiate")
+        return g, ex
+
+    def launch(self, ex, stream):
+        self.check(self.h.hipGraphLaunch(ex, stream), "hipGraphLaunch")
+        self.check(self.h.hipStreamSynchronize(stream), "hipStreamSynchronize")
+
+    def destroy(self, g, ex):
+        self.h.hipGraphExecDestroy(ex)
+        self.h.hipGraphDestroy(g)
