@@ -259,6 +259,109 @@ __global__ __launch_bounds__(MaxThreads<V>::value) void row_kernel(RowArgs a) {
     }
 }
 
+// RN_f32 of the exact sum of squares of one row held by a single wave,
+// recomputed from memory with the 3-limb integer method (ng_exact.hpp): the
+// fallback of the fp64 fast path. Returns false (ss untouched) for rows with
+// a value off the 2^-24 grid.
+template <typename T, bool ADD>
+__device__ __forceinline__ bool exact_row_ss_wave(const uint16_t* xr, const uint16_t* rr, int nvec, int lane, float& ss) {
+    Limbs Lm{0.0, 0.0, 0.0, 0};
+    for (int vi = lane; vi < nvec; vi += kWave) {
+        float fx[8];
+        unpack8<T>(ld16(xr + vi * 8), fx);
+        if (ADD) {
+            float fr[8];
+            unpack8<T>(ld16(rr + vi * 8), fr);
+#pragma unroll
+            for (int i = 0; i < 8; ++i) fx[i] = fx[i] + fr[i];
+        }
+#pragma unroll
+        for (int i = 0; i < 8; ++i) limbs_add(Lm, fx[i]);
+    }
+    const double t = wave_sum_f64_dpp(Lm.t), u = wave_sum_f64_dpp(Lm.u), w = wave_sum_f64_dpp(Lm.w);
+    if (wave_max_u32_dpp(static_cast<uint32_t>(Lm.bad))) return false;
+    ss = limbs_to_f32(t, u, w);
+    return true;
+}
+
+// Residual add + RMSNorm for rows that fit one wave (nvec <= 64 V), R rows
+// per wave: the loads of all R rows are issued first, then each row is
+// reduced, normalised and stored in turn, so the stores of the first rows
+// overlap the arrival of the later ones. Same arithmetic as row_kernel.
+// Rows past the last one are loaded from the last row and never stored.
+template <typename T, int V, int R>
+__global__ __launch_bounds__(64) void add_rms_rows_kernel(RowArgs a, int rows) {
+    const int lane = threadIdx.x;
+    const int row0 = blockIdx.x * R;
+    const uint16_t* X = static_cast<const uint16_t*>(a.x);
+    const uint16_t* RS = static_cast<const uint16_t*>(a.res);
+    const uint16_t* wr = static_cast<const uint16_t*>(a.w);
+    bool act[V];
+    int vc[V];
+#pragma unroll
+    for (int k = 0; k < V; ++k) {
+        const int vi = lane + k * kWave;
+        act[k] = k < V - 1 || vi < a.nvec;
+        vc[k] = act[k] ? vi : a.nvec - 1;
+    }
+    u32x4 xv[R][V], rv[R][V], wv[V];
+#pragma unroll
+    for (int j = 0; j < R; ++j) {
+        const size_t off = static_cast<size_t>(min(row0 + j, rows - 1)) * a.H;
+#pragma unroll
+        for (int k = 0; k < V; ++k) {
+            xv[j][k] = ld16_stream(X + off + vc[k] * 8);
+            rv[j][k] = ld16_stream(RS + off + vc[k] * 8);
+        }
+    }
+#pragma unroll
+    for (int k = 0; k < V; ++k) wv[k] = ld16(wr + vc[k] * 8);
+    __builtin_amdgcn_sched_barrier(0);
+
+#pragma unroll
+    for (int j = 0; j < R; ++j) {
+        if (row0 + j >= rows) break;
+        const size_t off = static_cast<size_t>(row0 + j) * a.H;
+        u32x4 ov[V];
+        double acc[4] = {0.0, 0.0, 0.0, 0.0};
+#pragma unroll
+        for (int k = 0; k < V; ++k) {
+            if (!act[k]) {
+                xv[j][k] = u32x4{0, 0, 0, 0};
+                rv[j][k] = u32x4{0, 0, 0, 0};
+            }
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const float s0 = el_add<T, 0>(xv[j][k][i], rv[j][k][i]);
+                const float s1 = el_add<T, 1>(xv[j][k][i], rv[j][k][i]);
+                ov[k][i] = pack2<T>(s0, s1);
+                const double d0 = static_cast<double>(s0), d1 = static_cast<double>(s1);
+                acc[(2 * i) & 3] = __builtin_fma(d0, d0, acc[(2 * i) & 3]);
+                acc[(2 * i + 1) & 3] = __builtin_fma(d1, d1, acc[(2 * i + 1) & 3]);
+            }
+        }
+        DD S = dd_add(two_sum(acc[0], acc[1]), two_sum(acc[2], acc[3]));
+        S = wave_sum_dd(S);
+        float ss;
+        if (!ss_fast_resolve(S.hi, 2 * V, ss)) exact_row_ss_wave<T, true>(X + off, RS + off, a.nvec, lane, ss);
+        const float r = 1.0f / __builtin_sqrtf(ss / static_cast<float>(a.H) + a.eps);
+        uint16_t* ro = static_cast<uint16_t*>(a.res_out) + off;
+        uint16_t* yr = static_cast<uint16_t*>(a.y) + off;
+#pragma unroll
+        for (int k = 0; k < V; ++k)
+            if (act[k]) st16_stream(ro + (lane + k * kWave) * 8, ov[k]);
+#pragma unroll
+        for (int k = 0; k < V; ++k) {
+            u32x4 y;
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+                y[i] = pack2<T>(el_mul<T, 0>(wv[k][i], el_mul<T, 0>(ov[k][i], r)),
+                                el_mul<T, 1>(wv[k][i], el_mul<T, 1>(ov[k][i], r)));
+            if (act[k]) st16_stream(yr + (lane + k * kWave) * 8, y);
+        }
+    }
+}
+
 // Element-wise fallback for any H and any alignment: one workgroup per row,
 // the row re-read from memory for each pass. Same arithmetic as row_kernel.
 template <typename T, bool NORM, bool ADD, bool QUANT>
@@ -417,6 +520,18 @@ static int launch_rows(const char* name, int rows, const RowArgs& a0) {
                   (QUANT || !NORM || aligned16(a.y)) && (!QUANT || aligned8(a.q));
     int nw = 0, V = 0;
     if (vec_ok && pick_row_shape(a.nvec, rows, nw, V)) {
+        if constexpr (NORM && ADD && !QUANT) {
+            // Residual add + RMSNorm on single-wave rows at prefill sizes: four
+            // rows per wave (measured on MI355X at T = H = 4096: 22.8 vs 24.0 us).
+            // The in-place aliasing of the engine (layer.cu:1038) is safe: a row's
+            // stores come after that row's loads, and rows never share a wave
+            // with another wave's rows.
+            if (nw == 1 && V == 8 && rows >= 4096) {
+                add_rms_rows_kernel<T, 8, 4><<<dim3((rows + 3) / 4), dim3(64), 0, stream()>>>(a, rows);
+                NG_CHECK_LAUNCH(name);
+                return 0;
+            }
+        }
         RowDispatch<T, NORM, ADD, QUANT>::launch(V, dim3(rows), dim3(nw * 64), a);
     } else {
         row_kernel_scalar<T, NORM, ADD, QUANT><<<dim3(rows), dim3(256), 0, stream()>>>(a);

@@ -101,7 +101,8 @@ def run_add_rmsnorm(lib, x, r, w, eps, dtype, inplace=False):
 
 
 @pytest.mark.parametrize("dtype", ["f16", "bf16"])
-@pytest.mark.parametrize("T,H", [(1, 4096), (64, 4096), (257, 5120), (5, 4100), (2, 65536), (1030, 2048)])
+@pytest.mark.parametrize("T,H", [(1, 4096), (64, 4096), (257, 5120), (5, 4100), (2, 65536), (1030, 2048),
+                                 (4096, 4096), (4099, 4096)])
 @pytest.mark.parametrize("inplace", [False, True])
 def test_add_rmsnorm_bit_exact(lib, ora, dtype, T, H, inplace):
     banner(f"add_rmsnorm {dtype} T={T} H={H} inplace={inplace}")
@@ -114,10 +115,20 @@ def test_add_rmsnorm_bit_exact(lib, ora, dtype, T, H, inplace):
     assert_bits_equal(y, y_want, "normed")
 
 
-def test_add_rmsnorm_exact_path_rows(lib, ora):
-    banner("add_rmsnorm exact-path rows")
+@pytest.mark.parametrize("T", [None, 4101])
+def test_add_rmsnorm_exact_path_rows(lib, ora, T):
+    """Rows that force the exact (integer-limb) reduction; T=4101 runs them
+    through the several-rows-per-wave kernel of large prefill batches, with the
+    adversarial rows scattered among ordinary ones and a partial last wave."""
+    banner(f"add_rmsnorm exact-path rows T={T}")
     H = 4096
-    x = bits(adversarial_rows(H), "f16")
+    adv = bits(adversarial_rows(H), "f16")
+    if T is None:
+        x = adv
+    else:
+        x = bits(RNG.standard_normal((T, H)), "f16")
+        at = np.sort(RNG.choice(T, adv.shape[0], replace=False))
+        x[at] = adv
     r = np.zeros_like(x)
     w = bits(np.ones(H), "f16")
     y, ro = run_add_rmsnorm(lib, x, r, w, 0.0, "f16")
