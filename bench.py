@@ -217,7 +217,7 @@ class Pool:
         self.buf.free()
 
 
-def pool_slots(footprint_bytes, min_slots=3, max_slots=512):
+def pool_slots(footprint_bytes, min_slots=3, max_slots=64):
     """Slots so that at least POOL_BYTES of other buffers are touched between
     two launches on the same slot (the Infinity Cache is 256 MB)."""
     return int(min(max_slots, max(min_slots, -(-POOL_BYTES // int(footprint_bytes)) + 1)))
@@ -286,7 +286,7 @@ def run_layer(L, hip, stream, cfg, steps, warmup, kernel_launches=24, kernel_rep
     shared = {"w_attn": DB.from_array(d["w_attn"]), "w_ffn": DB.from_array(d["w_ffn"]),
               "pos": DB.from_array(d["pos"])}
     if nsets is None:
-        nsets = max(2, -(-ROTATE_BYTES // LayerSet.nbytes(cfg)))
+        nsets = min(32, max(2, -(-ROTATE_BYTES // LayerSet.nbytes(cfg))))
     sets = [LayerSet(d, cfg, shared) for _ in range(nsets)]
     del d
     launches = [layer_launches(L, cfg, s) for s in sets]
