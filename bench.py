@@ -234,6 +234,7 @@ def kernel_pools_for(L, hip, cfg, d, shared):
     addn = L.ng_bf16_add_rmsnorm if bf else L.cuda_add_rmsnorm
     swig = L.ng_bf16_silu_mul if bf else L.cuda_silu_mul
     add = L.cuda_bf16_add if bf else L.cuda_add
+    rope_qk = L.ng_bf16_rope_qk_with_theta if bf else L.ng_rope_qk_with_theta
     th = T * H * e
     tq, tk, ti = T * cfg.nq * D * e, T * cfg.nkv * D * e, T * I * e
 
@@ -255,6 +256,9 @@ def kernel_pools_for(L, hip, cfg, d, shared):
              lambda g, u, o: swig(o, g, u, T * I))
     yield mk("add", 3 * th, [(th, d["x"]), (th, d["residual"]), (th, None)],
              lambda a, b, o: add(o, a, b, T * H))
+    # not in the engine's sequence: Q and K in one launch (ng_rope_qk_with_theta)
+    yield mk("rope_qk", tq + tk, [(tq, d["q"]), (tk, d["k"])],
+             lambda q, k: rope_qk(q, q, k, k, shared["pos"].ip, 1, T, cfg.nq, cfg.nkv, D, 0, theta))
 
 
 def time_graph(hip, stream, graphs, reps, warmup=2):
@@ -539,6 +543,12 @@ def main():
                       "buffer_sets": slots[k]}
     us_layer = sum(kernels[k]["us"] for k in W.LAYER_KERNELS)
     log(f"layer done: {us_layer:.1f} us summed kernel time, {step_ms * 1e3:.1f} us per step")
+    qk_bytes = lb["rope_q"] + lb["rope_k"] - 4 * cfg.T
+    fused_qk = {"entry_point": "ng_rope_qk_with_theta", "rope_qk_us": per["rope_qk"],
+                "rope_qk_GBps": qk_bytes / per["rope_qk"] / 1e3,
+                "us_per_layer": us_layer - per["rope_q"] - per["rope_k"] + per["rope_qk"],
+                "note": "Q and K rotated in one launch; the engine's own sequence (the headline) calls "
+                        "cuda_rope_with_theta twice"}
 
     extra = {}
     if not args.no_extra:
@@ -548,7 +558,7 @@ def main():
             s2, _, p2, _, _ = run_layer(L, hip, stream, c2, 20, 3)
             lb2 = W.layer_bytes(c2)
             b2 = sum(lb2[k] for k in W.LAYER_KERNELS)
-            u2 = sum(p2.values())
+            u2 = sum(p2[k] for k in W.LAYER_KERNELS)
             extra[key] = {"us_per_layer": u2, "us_per_step": s2 * 1e3, "GBps": b2 / u2 / 1e3,
                           "frac": b2 / u2 / 1e3 / PEAK_GBPS, "layer_bytes": b2, "per_kernel_us": p2}
         log("gather / rmsnorm+int8 / dequant")
@@ -583,6 +593,7 @@ def main():
                    "intermediate": cfg.I, "q_heads": cfg.nq, "kv_heads": cfg.nkv, "head_dim": cfg.D,
                    "rope_theta": cfg.theta, "eps": cfg.eps, "rotating_sets": nsets},
         "us_per_layer": us_layer,
+        "fused_qk_variant": fused_qk,
         "pct_of_peak": layer_bytes / us_layer / 1e3 / PEAK_GBPS * 100,
         "host_wall_ms_per_step": wall_ms,
         "layer_bytes": layer_bytes,

@@ -43,6 +43,19 @@ int ng_bf16_add_rmsnorm(void* normed_output, void* residual_output, const void* 
  * engine's cuda_bf16_silu + cuda_bf16_mul (gpu/engine/layer.cu:1603-1607). */
 int ng_bf16_silu_mul(void* output, const void* gate, const void* up, size_t num_elements);
 
+/* RoPE on Q [B, S, num_q_heads, D] and K [B, S, num_kv_heads, D] of the same
+ * tokens in one launch, with the semantics of two cuda_rope_with_theta calls
+ * sharing `positions` (the pair at gpu/engine/layer.cu:1016,1018). Each
+ * token's angles are evaluated once for both tensors. q_out may alias q_in
+ * and k_out may alias k_in. The bf16 variant fuses the pair of
+ * cuda_bf16_rope_with_theta calls the same way. */
+int ng_rope_qk_with_theta(void* q_out, const void* q_in, void* k_out, const void* k_in, const int* positions,
+                          int batch_size, int seq_len, int num_q_heads, int num_kv_heads, int head_dim,
+                          int rope_style, float rope_theta);
+int ng_bf16_rope_qk_with_theta(void* q_out, const void* q_in, void* k_out, const void* k_in, const int* positions,
+                               int batch_size, int seq_len, int num_q_heads, int num_kv_heads, int head_dim,
+                               int rope_style, float rope_theta);
+
 /* fp32 <-> fp16 on the device (round to nearest even / exact widening): the
  * converters behind gpu/cuda/memory.cu:130-143, exported. */
 int ng_fp32_to_fp16(void* output, const void* input, size_t num_elements);

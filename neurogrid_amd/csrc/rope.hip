@@ -128,11 +128,15 @@ __global__ __launch_bounds__(kRopeThreads) void rope_vec_kernel(RopeArgs a) {
 // last head; those vectors are not stored. When T is small, a token's passes
 // are split over G waves so that enough waves are in flight.
 struct RopeWaveArgs {
-    void* out;
+    void* out;         // first tensor [T, nh, D]
     const void* in;
+    void* out2;        // optional second tensor [T, nh2, D], same positions (nh2 = 0: none)
+    const void* in2;
     const int* pos;
     int T;
     int nh;
+    int nh2;
+    int npass1;        // head passes of the first tensor; passes beyond it cover the second
     int D;
     int lph_log2;      // log2(lanes per head)
     int G;             // waves per token
@@ -152,20 +156,28 @@ __global__ __launch_bounds__(kRopeThreads) void rope_wave_kernel(RopeWaveArgs a)
     const int j = lane & (lph - 1);
     const int hl = lane >> a.lph_log2;
     const int half = a.D >> 1;
-    const size_t base = static_cast<size_t>(t) * a.nh * a.D;
-    const uint16_t* in = static_cast<const uint16_t*>(a.in) + base;
-    uint16_t* out = static_cast<uint16_t*>(a.out) + base;
+    const uint16_t* in1 = static_cast<const uint16_t*>(a.in) + static_cast<size_t>(t) * a.nh * a.D;
+    uint16_t* out1 = static_cast<uint16_t*>(a.out) + static_cast<size_t>(t) * a.nh * a.D;
+    const uint16_t* in2 = static_cast<const uint16_t*>(a.in2) + static_cast<size_t>(t) * a.nh2 * a.D;
+    uint16_t* out2 = static_cast<uint16_t*>(a.out2) + static_cast<size_t>(t) * a.nh2 * a.D;
 
+    // Pass k of this wave is head pass g * HPL + k of the token: passes
+    // [0, npass1) cover the first tensor, the rest the second. A pass (or a
+    // lane) past the last head loads the first tensor's last head, and does
+    // not store.
     u32x4 v1[HPL], v2[HPL];
     int off[HPL];
-    bool ok[HPL];
+    bool ok[HPL], sec[HPL];
 #pragma unroll
     for (int k = 0; k < HPL; ++k) {
-        const int h = (g * HPL + k) * hpp + hl;
-        ok[k] = h < a.nh;
+        const int pi = g * HPL + k;
+        sec[k] = pi >= a.npass1;
+        const int h = (sec[k] ? pi - a.npass1 : pi) * hpp + hl;
+        ok[k] = h < (sec[k] ? a.nh2 : a.nh);
+        const uint16_t* src = ok[k] && sec[k] ? in2 : in1;
         off[k] = (ok[k] ? h : a.nh - 1) * a.D + 8 * j;
-        v1[k] = ld16_stream(in + off[k]);
-        if (STYLE == 0) v2[k] = ld16_stream(in + off[k] + half);
+        v1[k] = ld16_stream(src + off[k]);
+        if (STYLE == 0) v2[k] = ld16_stream(src + off[k] + half);
     }
     __builtin_amdgcn_sched_barrier(0);
 
@@ -203,8 +215,9 @@ __global__ __launch_bounds__(kRopeThreads) void rope_wave_kernel(RopeWaveArgs a)
                 y2[e] = x1[e] * sn[e] + x2[e] * c[e];
             }
             if (ok[k]) {
-                st16_stream(out + off[k], pack8<T>(y1));
-                st16_stream(out + off[k] + half, pack8<T>(y2));
+                uint16_t* dst = sec[k] ? out2 : out1;
+                st16_stream(dst + off[k], pack8<T>(y1));
+                st16_stream(dst + off[k] + half, pack8<T>(y2));
             }
         } else {
             float x[8], y[8];
@@ -214,7 +227,7 @@ __global__ __launch_bounds__(kRopeThreads) void rope_wave_kernel(RopeWaveArgs a)
                 y[2 * e] = x[2 * e] * c[e] - x[2 * e + 1] * sn[e];
                 y[2 * e + 1] = x[2 * e] * sn[e] + x[2 * e + 1] * c[e];
             }
-            if (ok[k]) st16_stream(out + off[k], pack8<T>(y));
+            if (ok[k]) st16_stream((sec[k] ? out2 : out1) + off[k], pack8<T>(y));
         }
     }
 }
@@ -262,6 +275,59 @@ static void fill_inv_freq(float theta, int D, float* dst) {
     for (int i = 0; i < D / 2; ++i) dst[i] = it->second[i];
 }
 
+static bool wave_rope_ok(int head_dim) { return head_dim == 64 || head_dim == 128 || head_dim == 256; }
+
+// Launch rope_wave_kernel over one tensor [T, nh, D], or two tensors of the
+// same tokens ([T, nh, D] and [T, nh2, D], nh2 > 0) that share positions.
+template <typename T>
+static int launch_rope_wave(const char* name, void* out, const void* in, void* out2, const void* in2,
+                            const int* positions, int tokens, int nh, int nh2, int head_dim, int style,
+                            const float* inv_freq) {
+    RopeWaveArgs w{};
+    w.out = out;
+    w.in = in;
+    w.out2 = out2;
+    w.in2 = in2;
+    w.pos = positions;
+    w.T = tokens;
+    w.nh = nh;
+    w.nh2 = nh2;
+    w.D = head_dim;
+    const int lph = style == 0 ? head_dim / 16 : head_dim / 8;
+    w.lph_log2 = __builtin_ctz(static_cast<unsigned>(lph));
+    const int hpp = kWave / lph;
+    w.npass1 = (nh + hpp - 1) / hpp;
+    const int npass = w.npass1 + (nh2 + hpp - 1) / hpp;
+    // Waves per token: enough waves to cover the GPU at small T, at most
+    // one per pass, and at most 8 passes per wave.
+    const long long want = 8ll * device_cu_count();
+    int G = static_cast<int>((want + tokens - 1) / tokens);
+    if (G > npass) G = npass;
+    if (G < (npass + 7) / 8) G = (npass + 7) / 8;
+    if (G < 1) G = 1;
+    const int hpl = (npass + G - 1) / G;
+    G = (npass + hpl - 1) / hpl;
+    w.G = G;
+    w.div_G = make_fastdiv(static_cast<uint32_t>(G));
+    for (int i = 0; i < head_dim / 2; ++i) w.inv_freq[i] = inv_freq[i];
+    const long long waves = static_cast<long long>(tokens) * G;
+    NG_REQUIRE(waves < (1ll << 31), "%s: tensor too large", name);
+    const unsigned blocks = static_cast<unsigned>((waves + 3) / 4);
+    auto go = [&](auto kern) { kern<<<dim3(blocks), dim3(kRopeThreads), 0, stream()>>>(w); };
+#define NG_ROPE_WAVE(HPL)                                                 \
+    case HPL:                                                             \
+        if (style == 0) go(rope_wave_kernel<T, 0, HPL>);                  \
+        else go(rope_wave_kernel<T, 1, HPL>);                             \
+        break;
+    switch (hpl) {
+        NG_ROPE_WAVE(1) NG_ROPE_WAVE(2) NG_ROPE_WAVE(3) NG_ROPE_WAVE(4)
+        NG_ROPE_WAVE(5) NG_ROPE_WAVE(6) NG_ROPE_WAVE(7) NG_ROPE_WAVE(8)
+        default: NG_REQUIRE(false, "%s: internal: %d passes per wave", name, hpl);
+    }
+#undef NG_ROPE_WAVE
+    return 0;
+}
+
 template <typename T>
 static int launch_rope(const char* name, void* output, const void* input, const int* positions,
                        int batch_size, int seq_len, int num_heads, int head_dim, int style, float theta) {
@@ -287,45 +353,10 @@ static int launch_rope(const char* name, void* output, const void* input, const 
 
     const bool aligned = aligned16(output) && aligned16(input);
     const bool vec = aligned && ((style == 0 && head_dim % 16 == 0) || (style == 1 && head_dim % 8 == 0));
-    if (aligned && (head_dim == 64 || head_dim == 128 || head_dim == 256)) {
-        RopeWaveArgs w{};
-        w.out = output;
-        w.in = input;
-        w.pos = positions;
-        w.T = a.T;
-        w.nh = num_heads;
-        w.D = head_dim;
-        const int lph = style == 0 ? head_dim / 16 : head_dim / 8;
-        w.lph_log2 = __builtin_ctz(static_cast<unsigned>(lph));
-        const int hpp = kWave / lph;
-        const int npass = (num_heads + hpp - 1) / hpp;
-        // Waves per token: enough waves to cover the GPU at small T, at most
-        // one per pass, and at most 8 passes per wave.
-        const long long want = 8ll * device_cu_count();
-        int G = static_cast<int>((want + a.T - 1) / a.T);
-        if (G > npass) G = npass;
-        if (G < (npass + 7) / 8) G = (npass + 7) / 8;
-        if (G < 1) G = 1;
-        const int hpl = (npass + G - 1) / G;
-        G = (npass + hpl - 1) / hpl;
-        w.G = G;
-        w.div_G = make_fastdiv(static_cast<uint32_t>(G));
-        for (int i = 0; i < a.half; ++i) w.inv_freq[i] = a.inv_freq[i];
-        const long long waves = static_cast<long long>(a.T) * G;
-        NG_REQUIRE(waves < (1ll << 31), "%s: tensor too large", name);
-        const unsigned blocks = static_cast<unsigned>((waves + 3) / 4);
-        auto go = [&](auto kern) { kern<<<dim3(blocks), dim3(kRopeThreads), 0, stream()>>>(w); };
-#define NG_ROPE_WAVE(HPL)                                                 \
-    case HPL:                                                             \
-        if (style == 0) go(rope_wave_kernel<T, 0, HPL>);                  \
-        else go(rope_wave_kernel<T, 1, HPL>);                             \
-        break;
-        switch (hpl) {
-            NG_ROPE_WAVE(1) NG_ROPE_WAVE(2) NG_ROPE_WAVE(3) NG_ROPE_WAVE(4)
-            NG_ROPE_WAVE(5) NG_ROPE_WAVE(6) NG_ROPE_WAVE(7) NG_ROPE_WAVE(8)
-            default: NG_REQUIRE(false, "%s: internal: %d passes per wave", name, hpl);
-        }
-#undef NG_ROPE_WAVE
+    if (aligned && wave_rope_ok(head_dim)) {
+        const int rc = launch_rope_wave<T>(name, output, input, output, input, positions, a.T, num_heads, 0,
+                                           head_dim, style, a.inv_freq);
+        if (rc != 0) return rc;
     } else if (vec) {
         const int uph = style == 0 ? head_dim / 16 : head_dim / 8;
         a.upt = num_heads * uph;
@@ -391,4 +422,53 @@ extern "C" int cuda_bf16_rope_with_theta(void* output, const void* input, const 
                                          float rope_theta) {
     return launch_rope<bf16>("cuda_bf16_rope_with_theta", output, input, positions, batch_size, seq_len,
                              num_heads, head_dim, rope_style, rope_theta);
+}
+
+// Q and K of the same tokens in one launch (the pair of calls at
+// gpu/engine/layer.cu:1016,1018, fused): each token's angles are evaluated
+// once for both tensors. Falls back to two launches for head_dim outside
+// {64, 128, 256} or unaligned buffers.
+template <typename T>
+static int launch_rope_qk(const char* name, void* q_out, const void* q_in, void* k_out, const void* k_in,
+                          const int* positions, int batch_size, int seq_len, int num_q_heads, int num_kv_heads,
+                          int head_dim, int style, float theta,
+                          int (*single)(void*, const void*, const int*, int, int, int, int, int, float)) {
+    NG_REQUIRE(q_out && q_in && k_out && k_in && positions, "%s: null pointer", name);
+    NG_REQUIRE(batch_size > 0 && seq_len > 0 && num_q_heads > 0 && num_kv_heads > 0,
+               "%s: batch=%d seq=%d q_heads=%d kv_heads=%d must be > 0", name, batch_size, seq_len, num_q_heads,
+               num_kv_heads);
+    NG_REQUIRE(head_dim >= 2 && head_dim % 2 == 0 && head_dim <= 2 * kRopeMaxHalf,
+               "%s: head_dim=%d must be even and in [2, %d]", name, head_dim, 2 * kRopeMaxHalf);
+    style = style == 1 ? 1 : 0;
+    const long long T64 = static_cast<long long>(batch_size) * seq_len;
+    NG_REQUIRE(T64 * num_q_heads * head_dim < (1ll << 31) && T64 * num_kv_heads * head_dim < (1ll << 31),
+               "%s: tensor too large", name);
+    const bool aligned = aligned16(q_out) && aligned16(q_in) && aligned16(k_out) && aligned16(k_in);
+    if (!(aligned && wave_rope_ok(head_dim))) {
+        const int rc = single(q_out, q_in, positions, batch_size, seq_len, num_q_heads, head_dim, style, theta);
+        if (rc != 0) return rc;
+        return single(k_out, k_in, positions, batch_size, seq_len, num_kv_heads, head_dim, style, theta);
+    }
+    float inv[kRopeMaxHalf];
+    fill_inv_freq(theta, head_dim, inv);
+    const int rc = launch_rope_wave<T>(name, q_out, q_in, k_out, k_in, positions, static_cast<int>(T64), num_q_heads,
+                                       num_kv_heads, head_dim, style, inv);
+    if (rc != 0) return rc;
+    NG_CHECK_LAUNCH(name);
+    return 0;
+}
+
+extern "C" int ng_rope_qk_with_theta(void* q_out, const void* q_in, void* k_out, const void* k_in,
+                                     const int* positions, int batch_size, int seq_len, int num_q_heads,
+                                     int num_kv_heads, int head_dim, int rope_style, float rope_theta) {
+    return launch_rope_qk<f16>("ng_rope_qk_with_theta", q_out, q_in, k_out, k_in, positions, batch_size, seq_len,
+                               num_q_heads, num_kv_heads, head_dim, rope_style, rope_theta, cuda_rope_with_theta);
+}
+
+extern "C" int ng_bf16_rope_qk_with_theta(void* q_out, const void* q_in, void* k_out, const void* k_in,
+                                          const int* positions, int batch_size, int seq_len, int num_q_heads,
+                                          int num_kv_heads, int head_dim, int rope_style, float rope_theta) {
+    return launch_rope_qk<bf16>("ng_bf16_rope_qk_with_theta", q_out, q_in, k_out, k_in, positions, batch_size,
+                                seq_len, num_q_heads, num_kv_heads, head_dim, rope_style, rope_theta,
+                                cuda_bf16_rope_with_theta);
 }

@@ -120,3 +120,36 @@ def test_gather_checked_zero_fills_bad_ids(lib):
     for i, t in enumerate(ids):
         want = table[t] if 0 <= t < V else np.zeros(H, np.uint16)
         assert_bits_equal(got[i], want, f"row {i}")
+
+
+QK_CASES = [
+    # (T, nq, nkv, D, theta, maxpos)
+    (4096, 32, 8, 128, 1e6, 4096),     # Mistral-7B prefill
+    (64, 32, 8, 128, 1e6, 4096),       # Mistral-7B decode: passes split over several waves
+    (300, 40, 40, 128, 1e4, 8192),     # Llama-2-13B heads
+    (50, 32, 4, 64, 1e4, 128),         # TinyLlama
+    (20, 6, 3, 256, 5e5, 32768),
+    (20, 5, 2, 80, 1e4, 1000),         # head_dim 80: two single launches
+]
+
+
+@pytest.mark.parametrize("dtype", ["f16", "bf16"])
+@pytest.mark.parametrize("style", [0, 1])
+@pytest.mark.parametrize("inplace", [False, True])
+@pytest.mark.parametrize("T,nq,nkv,D,theta,maxpos", QK_CASES)
+def test_rope_qk_fused(lib, ora, dtype, style, inplace, T, nq, nkv, D, theta, maxpos):
+    """ng_rope_qk_with_theta == the two cuda_rope_with_theta calls it fuses, and the oracle."""
+    banner(f"rope_qk {dtype} style={style} inplace={inplace} T={T} nq={nq} nkv={nkv} D={D}")
+    q = bits(RNG.standard_normal((T, nq, D)), dtype)
+    k = bits(RNG.standard_normal((T, nkv, D)), dtype)
+    pos = RNG.integers(0, maxpos, T).astype(np.int32)
+    qb, kb, pb = dev(q), dev(k), dev(pos)
+    qo = qb if inplace else empty(q.nbytes)
+    ko = kb if inplace else empty(k.nbytes)
+    fn = lib.ng_bf16_rope_qk_with_theta if dtype == "bf16" else lib.ng_rope_qk_with_theta
+    ok(fn(qo.vp, qb.vp, ko.vp, kb.vp, pb.ip, 1, T, nq, nkv, D, style, C.c_float(theta)), "rope_qk")
+    gq, gk = get(qo, np.uint16, q.shape), get(ko, np.uint16, k.shape)
+    assert_bits_equal(gq, run_rope(lib, q, pos, style, theta, dtype), "fused Q vs single launch")
+    assert_bits_equal(gk, run_rope(lib, k, pos, style, theta, dtype), "fused K vs single launch")
+    assert_close16(gq, ora.rope(q, pos, style, theta, dtype), dtype, "Q vs oracle")
+    assert_close16(gk, ora.rope(k, pos, style, theta, dtype), dtype, "K vs oracle")
