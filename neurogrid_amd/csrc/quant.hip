@@ -208,6 +208,56 @@ __global__ __launch_bounds__(kQThreads) void dequant_vec_kernel(uint16_t* out, c
     st16_stream(out + e0 + 8, pack8<f16>(hi));
 }
 
+// Chunked path for rows that are a multiple of 512 codes. A chunk is 512
+// consecutive codes of one row; lane l of a wave owns codes [8l, 8l + 8) of
+// each of its DQ_CHUNKS chunks: one 8-byte load and one 16-byte store per
+// chunk, so every load instruction reads 512 contiguous bytes and every store
+// instruction writes 1 KiB of whole cache lines. (Writing 16 codes per lane,
+// i.e. two 16-byte stores 32 bytes apart, leaves every line half-written by
+// each instruction; measured on MI355X that costs 27% at [14336, 4096].)
+constexpr int kDqChunks = 2;
+
+template <int MODE>
+__global__ __launch_bounds__(kQThreads) void dequant_chunk_kernel(uint16_t* out, const int8_t* q, const float* scales,
+                                                                  uint32_t nchunks, FastDiv chunks_per_row) {
+    const int lane = threadIdx.x & 63;
+    const uint32_t wv = blockIdx.x * (kQThreads / kWave) + (threadIdx.x >> 6);
+    u32x2 v[kDqChunks];
+    uint32_t ch[kDqChunks];
+#pragma unroll
+    for (int c = 0; c < kDqChunks; ++c) {
+        ch[c] = wv * kDqChunks + c;
+        const uint32_t cc = ch[c] < nchunks ? ch[c] : nchunks - 1;
+        v[c] = __builtin_nontemporal_load(reinterpret_cast<const u32x2*>(q + static_cast<size_t>(cc) * 512 + 8 * lane));
+    }
+#pragma unroll
+    for (int c = 0; c < kDqChunks; ++c) {
+        if (ch[c] >= nchunks) break;
+        float s[8];
+        if (MODE == DQ_ROW) {
+            const float rs = scales[fdiv(ch[c], chunks_per_row)];
+#pragma unroll
+            for (int e = 0; e < 8; ++e) s[e] = rs;
+        } else if (MODE == DQ_COL) {
+            const uint32_t col = (ch[c] - fdiv(ch[c], chunks_per_row) * chunks_per_row.d) * 512 + 8 * lane;
+            const u32x4 s0 = ld16(scales + col), s1 = ld16(scales + col + 4);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                s[e] = as_float(s0[e]);
+                s[4 + e] = as_float(s1[e]);
+            }
+        } else {
+            const float ts = scales[0];
+#pragma unroll
+            for (int e = 0; e < 8; ++e) s[e] = ts;
+        }
+        float f[8];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) f[e] = static_cast<float>(static_cast<int8_t>((v[c][e >> 2] >> ((e & 3) * 8)) & 0xffu)) * s[e];
+        st16_stream(out + static_cast<size_t>(ch[c]) * 512 + 8 * lane, pack8<f16>(f));
+    }
+}
+
 template <int MODE>
 __global__ __launch_bounds__(kQThreads) void dequant_scalar_kernel(uint16_t* out, const int8_t* q,
                                                                    const float* scales, size_t n, int cols) {
@@ -226,7 +276,14 @@ static int launch_dequant(const char* name, void* out, const void* q, const void
     const size_t n = rows * cols;
     const bool vec = cols % 16 == 0 && aligned16(out) && aligned16(q) && (MODE != DQ_COL || aligned16(scales)) &&
                      n / 16 < (1ull << 32) && cols / 16 < (1ull << 31);
-    if (vec) {
+    if (vec && cols % 512 == 0 && aligned8(q) && n / 512 < (1ull << 32)) {
+        const uint32_t nchunks = static_cast<uint32_t>(n / 512);
+        const uint32_t waves = (nchunks + kDqChunks - 1) / kDqChunks;
+        const unsigned blocks = (waves + kQThreads / kWave - 1) / (kQThreads / kWave);
+        dequant_chunk_kernel<MODE><<<dim3(blocks), dim3(kQThreads), 0, stream()>>>(
+            static_cast<uint16_t*>(out), static_cast<const int8_t*>(q), static_cast<const float*>(scales), nchunks,
+            make_fastdiv(static_cast<uint32_t>(cols / 512)));
+    } else if (vec) {
         const uint32_t ngroups = static_cast<uint32_t>(n / 16);
         const unsigned blocks = static_cast<unsigned>((ngroups + kQThreads - 1) / kQThreads);
         dequant_vec_kernel<MODE><<<dim3(blocks), dim3(kQThreads), 0, stream()>>>(

@@ -131,7 +131,7 @@ def test_per_column_quant_bit_exact(lib, ora, K, N):
     assert_bits_equal(get(qb, np.int8, (K, N)), qw, "codes")
 
 
-@pytest.mark.parametrize("rows,cols", [(256, 4096), (7, 100), (3, 16), (14336, 4096)])
+@pytest.mark.parametrize("rows,cols", [(256, 4096), (7, 100), (3, 16), (14336, 4096), (7, 1536), (1, 512), (5, 528)])
 @pytest.mark.parametrize("per_row", [1, 0])
 def test_dequant_weights_bit_exact(lib, ora, rows, cols, per_row):
     banner(f"dequant {rows}x{cols} per_row={per_row}")
@@ -144,7 +144,7 @@ def test_dequant_weights_bit_exact(lib, ora, rows, cols, per_row):
     assert_bits_equal(get(ob, np.uint16, (rows, cols)), want, "dequant")
 
 
-@pytest.mark.parametrize("n", [4096, 4099, 1 << 20])
+@pytest.mark.parametrize("n", [4096, 4099, 1 << 20, 512 * 7])
 def test_dequant_per_tensor_bit_exact(lib, ora, n):
     banner(f"dequant per-tensor n={n}")
     q = RNG.integers(-128, 128, n).astype(np.int8)
