@@ -238,9 +238,29 @@ __device__ __forceinline__ u32x2 qcode8(const u32x4 v, float inv, float ns) {
     return out;
 }
 
-// Scalar form of the same code (for element-wise fallback paths).
-__device__ __forceinline__ int qcode_int(float v, float inv, float ns) {
-    return static_cast<int>(qcode_biased_f32(v, inv, ns)) - 128;
+// Codes of a row whose scale is not finite (the row holds an infinity or a
+// NaN): the IEEE quotient itself, clamped. Finite values of a row with an
+// infinite scale get code 0, as v / inf = 0; the correction step above would
+// form 0 * inf = NaN instead. Codes of infinite or NaN elements are not
+// specified (the quotient is NaN).
+template <typename T>
+__device__ __forceinline__ u32x2 qcode8_div(const u32x4 v, float scale) {
+    u32x2 out = {0, 0};
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+        const float q = __builtin_rintf(to_f32<T>(lane16(v, e)) / scale);
+        const int c = static_cast<int>(fminf(fmaxf(q, -127.0f), 127.0f));
+        out[e >> 2] |= (static_cast<uint32_t>(c) & 0xffu) << ((e & 3) * 8);
+    }
+    return out;
+}
+
+// Scalar form of the code (for element-wise fallback paths); handles a
+// non-finite scale like qcode8_div.
+__device__ __forceinline__ int qcode_int(float v, float scale, float inv) {
+    if (!__builtin_isfinite(scale))
+        return static_cast<int>(fminf(fmaxf(__builtin_rintf(v / scale), -127.0f), 127.0f));
+    return static_cast<int>(qcode_biased_f32(v, inv, -scale)) - 128;
 }
 
 // Largest |value| of the 8 elements of a 16-byte vector, as the 15-bit

@@ -252,9 +252,10 @@ __global__ __launch_bounds__(MaxThreads<V>::value) void row_kernel(RowArgs a) {
     if (tid == 0) a.scales[blockIdx.x] = scale;
 
     int8_t* qr = a.q + rowoff;
+    const bool finite_scale = __builtin_isfinite(scale);  // uniform over the row
 #pragma unroll
     for (int k = 0; k < V; ++k) {
-        const u32x2 c = qcode8<T>(yv[k], inv, -scale);
+        const u32x2 c = finite_scale ? qcode8<T>(yv[k], inv, -scale) : qcode8_div<T>(yv[k], scale);
         if (act[k]) __builtin_nontemporal_store(c, reinterpret_cast<u32x2*>(qr + (tid + k * nthr) * 8));
     }
 }
@@ -466,7 +467,7 @@ __global__ __launch_bounds__(256) void row_kernel_scalar(RowArgs a) {
         const uint16_t vb = vbits(i);
         const uint16_t rb = ADD ? from_f32<T>(sval(i)) : 0;
         if (ADD) ror[i] = rb;
-        qr[i] = static_cast<int8_t>(qcode_int(to_f32<T>(vb), inv, -scale));
+        qr[i] = static_cast<int8_t>(qcode_int(to_f32<T>(vb), scale, inv));
     }
 }
 

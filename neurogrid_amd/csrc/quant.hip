@@ -26,7 +26,7 @@ __device__ __forceinline__ float scale_from_bits(uint32_t mbits) {
 }
 
 // q = clamp(rint(RN(v / scale)), -127, 127) without a division (qcode_int).
-__device__ __forceinline__ int qcode(float v, float scale, float inv) { return qcode_int(v, inv, -scale); }
+__device__ __forceinline__ int qcode(float v, float scale, float inv) { return qcode_int(v, scale, inv); }
 
 __global__ void fill_u32_kernel(uint32_t* p, size_t n, uint32_t v) {
     const size_t stride = static_cast<size_t>(gridDim.x) * blockDim.x;

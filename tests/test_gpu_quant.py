@@ -57,6 +57,24 @@ def test_per_row_quant_zero_rows_and_ties(lib, ora):
     assert q[1, 1:9].tolist() == [0, 2, 2, 0, -2, -2, 126, -126]
 
 
+@pytest.mark.parametrize("cols", [4096, 1000])
+def test_per_row_quant_rows_with_infinities(lib, ora, cols):
+    """A row holding +-inf has scale inf; its finite values get code 0 (v / inf = 0),
+    as in the oracle. Codes of the infinite elements themselves are unspecified."""
+    banner(f"per-row quant rows with infinities cols={cols}")
+    x = f16(RNG.standard_normal((6, cols)))
+    x[1, 5] = 0x7C00          # +inf
+    x[3, cols - 1] = 0xFC00   # -inf
+    x[4, 0], x[4, 7] = 0x7C00, 0xFC00
+    q, s = run_rows(lib, x)
+    qw, sw = ora.quant_rows(x)
+    assert_bits_equal(s.view(np.uint32), sw.view(np.uint32), "scales")
+    assert np.isinf(s[[1, 3, 4]]).all()
+    finite = (x & 0x7C00) != 0x7C00
+    assert_bits_equal(q[finite], qw[finite], "codes of finite elements")
+    assert (q[[1, 3, 4]][finite[[1, 3, 4]]] == 0).all()
+
+
 def run_norm_quant(lib, x, w, eps, residual=None):
     T, H = x.shape
     xb, wb, qb, sb = dev(x), dev(w), empty(x.size), empty(4 * T)
