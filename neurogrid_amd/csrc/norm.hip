@@ -522,13 +522,20 @@ static int launch_rows(const char* name, int rows, const RowArgs& a0) {
     int nw = 0, V = 0;
     if (vec_ok && pick_row_shape(a.nvec, rows, nw, V)) {
         if constexpr (NORM && ADD && !QUANT) {
-            // Residual add + RMSNorm on single-wave rows at prefill sizes: four
-            // rows per wave (measured on MI355X at T = H = 4096: 22.8 vs 24.0 us).
-            // The in-place aliasing of the engine (layer.cu:1038) is safe: a row's
-            // stores come after that row's loads, and rows never share a wave
-            // with another wave's rows.
-            if (nw == 1 && V == 8 && rows >= 4096) {
+            // Residual add + RMSNorm at prefill sizes, shapes measured on MI355X.
+            // Several rows per wave pays when it leaves about 1024 waves (one per
+            // SIMD), each with many bytes in flight:
+            //   H = 4096, T >= 4096: 4 rows per wave      (T = 4096: 22.8 vs 24.0 us)
+            //   H = 5120, T in [1536, 4096): 2 rows/wave  (T = 2048: 14.5 vs 15.9 us)
+            // The engine's in-place aliasing (layer.cu:1038) is safe: a row's
+            // stores come after that row's loads, and no two waves share a row.
+            if (a.nvec == 512 && rows >= 4096) {
                 add_rms_rows_kernel<T, 8, 4><<<dim3((rows + 3) / 4), dim3(64), 0, stream()>>>(a, rows);
+                NG_CHECK_LAUNCH(name);
+                return 0;
+            }
+            if (a.nvec == 640 && rows >= 1536 && rows < 4096) {
+                add_rms_rows_kernel<T, 10, 2><<<dim3((rows + 1) / 2), dim3(64), 0, stream()>>>(a, rows);
                 NG_CHECK_LAUNCH(name);
                 return 0;
             }

@@ -102,7 +102,7 @@ def run_add_rmsnorm(lib, x, r, w, eps, dtype, inplace=False):
 
 @pytest.mark.parametrize("dtype", ["f16", "bf16"])
 @pytest.mark.parametrize("T,H", [(1, 4096), (64, 4096), (257, 5120), (5, 4100), (2, 65536), (1030, 2048),
-                                 (4096, 4096), (4099, 4096)])
+                                 (4096, 4096), (4099, 4096), (1537, 5120), (2048, 5120), (6200, 5120)])
 @pytest.mark.parametrize("inplace", [False, True])
 def test_add_rmsnorm_bit_exact(lib, ora, dtype, T, H, inplace):
     banner(f"add_rmsnorm {dtype} T={T} H={H} inplace={inplace}")
