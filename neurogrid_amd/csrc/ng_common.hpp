@@ -196,30 +196,32 @@ __device__ __forceinline__ float el_fma(float a, float b, uint32_t p) {
 
 // ---------------------------------------------------------------------------
 // int8 absmax code: q = clamp(rint(RN(v / s)), -127, 127) for a row scale
-// s > 0, given inv = RN(1 / s) and ns = -s. RN(v / s) is obtained without a
-// division: z = RN(v inv) is within a few ulp of v / s, the residual
-// r = RN(v - z s) is then exact, and RN(z + r inv) is the correctly rounded
-// quotient (Markstein's correction step; checked exhaustively for every fp16
-// v against every scale RN(m / 127) of an fp16 m). Returned biased by +128,
-// ready for v_cvt_pk_u8_f32; xor 0x80 turns the byte into two's complement.
+// s = RN(m / 127) > 0 of the row's absmax m, given inv = RN(1 / s) and
+// ns = -s. RN(v / s) is obtained without a division: z = RN(v inv) is within
+// a few ulp of v / s, the residual r = RN(v - z s) is then exact, and
+// z1 = RN(z + r inv) is the correctly rounded quotient (Markstein's correction
+// step). Adding 1.5 * 2^23 to z1 rounds it to an integer, ties to even, and
+// leaves that integer in the low bits of the sum, so its low byte is the
+// two's-complement code. No clamp is needed: |v| <= m gives
+// |v / s| <= 127 (1 + 2^-24). The whole sequence is checked exhaustively
+// against clamp(rint(v / s)) with IEEE division, for every fp16 m and every
+// fp16 v with |v| <= m.
 // ---------------------------------------------------------------------------
-__device__ __forceinline__ float qcode_biased_f32(float v, float inv, float ns) {
-    const float z = v * inv;
-    const float r = __builtin_fmaf(z, ns, v);
-    const float q = __builtin_rintf(__builtin_fmaf(r, inv, z));
-    return __builtin_amdgcn_fmed3f(q, -127.0f, 127.0f) + 128.0f;
-}
+constexpr float kRoundMagic = 12582912.0f;  // 1.5 * 2^23
 
 template <typename T, int HI>
-__device__ __forceinline__ float qcode_biased(uint32_t p, float inv, float ns) {
+__device__ __forceinline__ uint32_t qcode_bits(uint32_t p, float inv, float ns) {
+    float z1;
     if constexpr (__is_same(T, f16)) {
         const float z = el_mul<T, HI>(p, inv);
         const float r = el_fma<T, HI>(z, ns, p);
-        const float q = __builtin_rintf(__builtin_fmaf(r, inv, z));
-        return __builtin_amdgcn_fmed3f(q, -127.0f, 127.0f) + 128.0f;
+        z1 = __builtin_fmaf(r, inv, z);
     } else {
-        return qcode_biased_f32(el_get<T, HI>(p), inv, ns);
+        const float v = el_get<T, HI>(p);
+        const float z = v * inv;
+        z1 = __builtin_fmaf(__builtin_fmaf(z, ns, v), inv, z);
     }
+    return __builtin_bit_cast(uint32_t, fp32_barrier(z1) + kRoundMagic);
 }
 
 // Codes of the 8 elements of a 16-byte vector, as two dwords of int8.
@@ -228,12 +230,11 @@ __device__ __forceinline__ u32x2 qcode8(const u32x4 v, float inv, float ns) {
     u32x2 out;
 #pragma unroll
     for (int d = 0; d < 2; ++d) {
-        uint32_t acc = 0;
-        acc = __builtin_amdgcn_cvt_pk_u8_f32(qcode_biased<T, 0>(v[2 * d], inv, ns), 0, acc);
-        acc = __builtin_amdgcn_cvt_pk_u8_f32(qcode_biased<T, 1>(v[2 * d], inv, ns), 1, acc);
-        acc = __builtin_amdgcn_cvt_pk_u8_f32(qcode_biased<T, 0>(v[2 * d + 1], inv, ns), 2, acc);
-        acc = __builtin_amdgcn_cvt_pk_u8_f32(qcode_biased<T, 1>(v[2 * d + 1], inv, ns), 3, acc);
-        out[d] = acc ^ 0x80808080u;
+        const uint32_t b0 = qcode_bits<T, 0>(v[2 * d], inv, ns), b1 = qcode_bits<T, 1>(v[2 * d], inv, ns);
+        const uint32_t b2 = qcode_bits<T, 0>(v[2 * d + 1], inv, ns), b3 = qcode_bits<T, 1>(v[2 * d + 1], inv, ns);
+        const uint32_t lo = __builtin_amdgcn_perm(b1, b0, 0x0c0c0400u);  // bytes b0.0, b1.0, 0, 0
+        const uint32_t hi = __builtin_amdgcn_perm(b3, b2, 0x0c0c0400u);  // bytes b2.0, b3.0, 0, 0
+        out[d] = __builtin_amdgcn_perm(hi, lo, 0x05040100u);            // lo.0, lo.1, hi.0, hi.1
     }
     return out;
 }
@@ -260,7 +261,9 @@ __device__ __forceinline__ u32x2 qcode8_div(const u32x4 v, float scale) {
 __device__ __forceinline__ int qcode_int(float v, float scale, float inv) {
     if (!__builtin_isfinite(scale))
         return static_cast<int>(fminf(fmaxf(__builtin_rintf(v / scale), -127.0f), 127.0f));
-    return static_cast<int>(qcode_biased_f32(v, inv, -scale)) - 128;
+    const float z = v * inv;
+    const float z1 = __builtin_fmaf(__builtin_fmaf(z, -scale, v), inv, z);
+    return static_cast<int8_t>(__builtin_bit_cast(uint32_t, fp32_barrier(z1) + kRoundMagic) & 0xffu);
 }
 
 // Largest |value| of the 8 elements of a 16-byte vector, as the 15-bit
