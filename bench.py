@@ -421,6 +421,41 @@ def extra_kernels(L, hip, stream):
     for p in (wq, wo):
         p.free()
     ws.free()
+
+    # QK LayerNorm + RoPE at Mistral-7B prefill shapes (not part of the Mistral
+    # layer; the engine runs it for models with per-head norms, layer.cu:998-1018):
+    # the fused entry point vs the four launches it replaces.
+    d = W.make_layer_inputs(cfg, seed=0, with_table=False)
+    T, D, nq, nkv = cfg.T, cfg.D, cfg.nq, cfg.nkv
+    tq, tk = T * nq * D * 2, T * nkv * D * 2
+    n = pool_slots(2 * (tq + tk))
+    qp, kp = Pool(hip, tq, n, d["q"]), Pool(hip, tk, n, d["k"])
+    wq, wk, pos = DB.from_array(d["w_attn"][:D]), DB.from_array(d["w_ffn"][:D]), DB.from_array(d["pos"])
+    eps, th = C.c_float(1e-5), C.c_float(cfg.theta)
+    fused = [("qkn_rope", (lambda j=j: L.ng_qk_rmsnorm_rope_with_theta(
+        qp.at(j), qp.at(j), kp.at(j), kp.at(j), wq.vp, wk.vp, pos.ip, 1, T, nq, nkv, D, eps, 0, th)))
+        for j in range(n)]
+    us_f = time_pool_kernel(hip, stream, fused)
+
+    def composed(j):
+        for rc in (L.ng_per_head_rmsnorm(qp.at(j), qp.at(j), wq.vp, T, nq, D, eps),
+                   L.ng_per_head_rmsnorm(kp.at(j), kp.at(j), wk.vp, T, nkv, D, eps),
+                   L.cuda_rope_with_theta(qp.at(j), qp.at(j), pos.ip, 1, T, nq, D, 0, th),
+                   L.cuda_rope_with_theta(kp.at(j), kp.at(j), pos.ip, 1, T, nkv, D, 0, th)):
+            if rc != 0:
+                return rc
+        return 0
+
+    us_c = time_pool_kernel(hip, stream, [("qkn_composed", (lambda j=j: composed(j))) for j in range(n)])
+    b = 2 * (tq + tk) + 4 * T + 4 * D
+    out["qk_rmsnorm_rope_mistral7b_prefill"] = {
+        "us": us_f, "GBps": b / us_f / 1e3, "frac": b / us_f / 1e3 / PEAK_GBPS, "bytes": b,
+        "composed_us": us_c, "note": "fused ng_qk_rmsnorm_rope_with_theta vs ng_per_head_rmsnorm x2 + "
+                                             "cuda_rope_with_theta x2 (composed_us: the four launches)"}
+    for p in (qp, kp):
+        p.free()
+    for x in (wq, wk, pos):
+        x.free()
     return out
 
 

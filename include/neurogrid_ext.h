@@ -56,6 +56,30 @@ int ng_bf16_rope_qk_with_theta(void* q_out, const void* q_in, void* k_out, const
                                int batch_size, int seq_len, int num_q_heads, int num_kv_heads, int head_dim,
                                int rope_style, float rope_theta);
 
+/* Per-head RMSNorm (QK LayerNorm): x [tokens, heads, head_dim], weight
+ * [head_dim] shared by every head; each head's head_dim slice is normalised
+ * like a cuda_rmsnorm row. Replaces the engine's static per_head_rmsnorm
+ * kernels (gpu/engine/layer.cu:657-701, bf16 1323-1366). output may alias
+ * input. */
+int ng_per_head_rmsnorm(void* output, const void* input, const void* weight, int num_tokens, int num_heads,
+                        int head_dim, float eps);
+int ng_bf16_per_head_rmsnorm(void* output, const void* input, const void* weight, int num_tokens,
+                             int num_heads, int head_dim, float eps);
+
+/* Per-head RMSNorm of Q and K (weights q_norm_weight, k_norm_weight [head_dim])
+ * followed by RoPE on both, in one launch: the same results as
+ * ng_per_head_rmsnorm on each tensor and then ng_rope_qk_with_theta. Fuses
+ * gpu/engine/layer.cu:998-1018 (QK LayerNorm, then RoPE on Q and K). Outputs
+ * may alias their inputs. */
+int ng_qk_rmsnorm_rope_with_theta(void* q_out, const void* q_in, void* k_out, const void* k_in,
+                                  const void* q_norm_weight, const void* k_norm_weight, const int* positions,
+                                  int batch_size, int seq_len, int num_q_heads, int num_kv_heads, int head_dim,
+                                  float eps, int rope_style, float rope_theta);
+int ng_bf16_qk_rmsnorm_rope_with_theta(void* q_out, const void* q_in, void* k_out, const void* k_in,
+                                       const void* q_norm_weight, const void* k_norm_weight, const int* positions,
+                                       int batch_size, int seq_len, int num_q_heads, int num_kv_heads,
+                                       int head_dim, float eps, int rope_style, float rope_theta);
+
 /* fp32 <-> fp16 on the device (round to nearest even / exact widening): the
  * converters behind gpu/cuda/memory.cu:130-143, exported. */
 int ng_fp32_to_fp16(void* output, const void* input, size_t num_elements);

@@ -82,6 +82,11 @@ SIGNATURES: dict[str, tuple] = {
     "ng_gather_embeddings_checked": (_i, [_vp, _cvp, _ip, _i, _i, _i, _ip]),
     "ng_rope_qk_with_theta": (_i, [_vp, _cvp, _vp, _cvp, _ip, _i, _i, _i, _i, _i, _i, _f]),
     "ng_bf16_rope_qk_with_theta": (_i, [_vp, _cvp, _vp, _cvp, _ip, _i, _i, _i, _i, _i, _i, _f]),
+    "ng_per_head_rmsnorm": (_i, [_vp, _cvp, _cvp, _i, _i, _i, _f]),
+    "ng_bf16_per_head_rmsnorm": (_i, [_vp, _cvp, _cvp, _i, _i, _i, _f]),
+    "ng_qk_rmsnorm_rope_with_theta": (_i, [_vp, _cvp, _vp, _cvp, _cvp, _cvp, _ip, _i, _i, _i, _i, _i, _f, _i, _f]),
+    "ng_bf16_qk_rmsnorm_rope_with_theta": (_i, [_vp, _cvp, _vp, _cvp, _cvp, _cvp, _ip, _i, _i, _i, _i, _i, _f, _i,
+                                                _f]),
 }
 
 _LIB = None

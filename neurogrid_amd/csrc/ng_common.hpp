@@ -64,6 +64,12 @@ inline hipStream_t stream() { return ng_get_stream(); }
 // Number of compute units of the current device (cached per device id).
 int device_cu_count();
 
+// RMSNorm of `rows` rows of H 16-bit elements through the row kernels
+// (norm.hip); launches on stream(), returns 0 or -1.
+template <typename T>
+__attribute__((visibility("hidden"))) int rows_rmsnorm(const char* name, void* output, const void* input,
+                                                      const void* weight, int rows, int H, float eps);
+
 // ---------------------------------------------------------------------------
 // Element conversions.
 // ---------------------------------------------------------------------------

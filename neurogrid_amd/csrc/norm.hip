@@ -636,3 +636,20 @@ extern "C" int cuda_quantize_weights_per_row(void* output, void* scales, const v
     a.x = input; a.H = cols;
     return launch_rows<f16, false, false, true>("cuda_quantize_weights_per_row", rows, a);
 }
+
+namespace ng {
+
+// RMSNorm of `rows` rows of H elements through the row kernels, for the
+// per-head RMSNorm's fallback (rope.hip).
+template <typename T>
+int rows_rmsnorm(const char* name, void* output, const void* input, const void* weight, int rows, int H,
+                 float eps) {
+    RowArgs a{};
+    a.y = output; a.x = input; a.w = weight; a.H = H; a.eps = eps;
+    return launch_rows<T, true, false, false>(name, rows, a);
+}
+
+template int rows_rmsnorm<f16>(const char*, void*, const void*, const void*, int, int, float);
+template int rows_rmsnorm<bf16>(const char*, void*, const void*, const void*, int, int, float);
+
+}  // namespace ng

@@ -12,6 +12,8 @@
 // rotates every head of those tokens with 16-byte vector accesses; the
 // reference evaluates powf/sincos again for every head.
 #include "ng_common.hpp"
+#include "ng_exact.hpp"
+#include "../../include/neurogrid_ext.h"
 
 #include <math.h>
 
@@ -141,10 +143,75 @@ struct RopeWaveArgs {
     int lph_log2;      // log2(lanes per head)
     int G;             // waves per token
     FastDiv div_G;
+    const void* w1;    // per-head RMSNorm weights [D] of the first / second tensor (QKNORM)
+    const void* w2;
+    float eps;
     float inv_freq[kRopeMaxHalf];
 };
 
-template <typename T, int STYLE, int HPL>
+// Sums over the lph consecutive lanes that hold one head (lph a power of two
+// up to 32). Each step adds the value of a partner lane in the complementary
+// half of the current group, so every lane of the group ends with the same
+// bits (dd_add is commutative bit for bit).
+__device__ __forceinline__ DD group_sum_dd(DD v, int lph) {
+    if (lph > 1) v = dd_add(v, dpp_dd<kDppQuadSwap1>(v));
+    if (lph > 2) v = dd_add(v, dpp_dd<kDppQuadSwap2>(v));
+    if (lph > 4) v = dd_add(v, dpp_dd<kDppRowHalfMirror>(v));
+    if (lph > 8) v = dd_add(v, dpp_dd<kDppRowMirror>(v));
+    if (lph > 16) v = dd_add(v, DD{__shfl_xor(v.hi, 16, kWave), __shfl_xor(v.lo, 16, kWave)});
+    return v;
+}
+
+__device__ __forceinline__ double group_sum_f64(double v, int lph) {
+    if (lph > 1) v += dpp_f64<kDppQuadSwap1>(v);
+    if (lph > 2) v += dpp_f64<kDppQuadSwap2>(v);
+    if (lph > 4) v += dpp_f64<kDppRowHalfMirror>(v);
+    if (lph > 8) v += dpp_f64<kDppRowMirror>(v);
+    if (lph > 16) v += __shfl_xor(v, 16, kWave);
+    return v;
+}
+
+// Per-head RMSNorm of the NV 16-byte vectors a lane holds of one head (the
+// head spread over lph lanes), in place: y = RN_T(RN(x * r) * w),
+// r = 1 / sqrt(RN_f32(exact sum x^2) / D + eps), as the row kernels compute it.
+template <typename T, int NV>
+__device__ __forceinline__ void head_rmsnorm(u32x4 (&x)[NV], const u32x4 (&w)[NV], int lph, int D, float eps) {
+    double acc[4] = {0.0, 0.0, 0.0, 0.0};
+#pragma unroll
+    for (int n = 0; n < NV; ++n)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const double d0 = static_cast<double>(el_get<T, 0>(x[n][i]));
+            const double d1 = static_cast<double>(el_get<T, 1>(x[n][i]));
+            acc[(2 * i) & 3] = __builtin_fma(d0, d0, acc[(2 * i) & 3]);
+            acc[(2 * i + 1) & 3] = __builtin_fma(d1, d1, acc[(2 * i + 1) & 3]);
+        }
+    const DD S = group_sum_dd(dd_add(two_sum(acc[0], acc[1]), two_sum(acc[2], acc[3])), lph);
+    float ss;
+    if (!ss_fast_resolve(S.hi, 2 * NV, ss)) {
+        // Exact path for this head (the whole lane group takes it together).
+        Limbs Lm{0.0, 0.0, 0.0, 0};
+#pragma unroll
+        for (int n = 0; n < NV; ++n)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                limbs_add(Lm, el_get<T, 0>(x[n][i]));
+                limbs_add(Lm, el_get<T, 1>(x[n][i]));
+            }
+        const double t = group_sum_f64(Lm.t, lph), u = group_sum_f64(Lm.u, lph), wl = group_sum_f64(Lm.w, lph);
+        const double bad = group_sum_f64(static_cast<double>(Lm.bad), lph);
+        if (bad == 0.0) ss = limbs_to_f32(t, u, wl);
+    }
+    const float r = 1.0f / __builtin_sqrtf(ss / static_cast<float>(D) + eps);
+#pragma unroll
+    for (int n = 0; n < NV; ++n)
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+            x[n][i] = pack2<T>(el_mul<T, 0>(w[n][i], el_mul<T, 0>(x[n][i], r)),
+                               el_mul<T, 1>(w[n][i], el_mul<T, 1>(x[n][i], r)));
+}
+
+template <typename T, int STYLE, int HPL, bool QKNORM, bool ROT = true>
 __global__ __launch_bounds__(kRopeThreads) void rope_wave_kernel(RopeWaveArgs a) {
     const int lane = threadIdx.x & 63;
     const uint32_t w = blockIdx.x * (kRopeThreads / kWave) + (threadIdx.x >> 6);
@@ -180,6 +247,46 @@ __global__ __launch_bounds__(kRopeThreads) void rope_wave_kernel(RopeWaveArgs a)
         if (STYLE == 0) v2[k] = ld16_stream(src + off[k] + half);
     }
     __builtin_amdgcn_sched_barrier(0);
+
+    if (QKNORM) {
+        // Per-head RMSNorm of each pass before it is rotated (weights of the
+        // tensor the pass belongs to; the same vectors of the weight row for
+        // every head).
+        const uint16_t* wt1 = static_cast<const uint16_t*>(a.w1);
+        const uint16_t* wt2 = a.nh2 > 0 ? static_cast<const uint16_t*>(a.w2) : wt1;
+        u32x4 wa1 = ld16(wt1 + 8 * j), wa2 = ld16(wt2 + 8 * j), wb1 = wa1, wb2 = wa2;
+        if (STYLE == 0) {
+            wb1 = ld16(wt1 + half + 8 * j);
+            wb2 = ld16(wt2 + half + 8 * j);
+        }
+#pragma unroll
+        for (int k = 0; k < HPL; ++k) {
+            if (STYLE == 0) {
+                u32x4 xs[2] = {v1[k], v2[k]};
+                const u32x4 ws[2] = {sec[k] ? wa2 : wa1, sec[k] ? wb2 : wb1};
+                head_rmsnorm<T, 2>(xs, ws, lph, a.D, a.eps);
+                v1[k] = xs[0];
+                v2[k] = xs[1];
+            } else {
+                u32x4 xs[1] = {v1[k]};
+                const u32x4 ws[1] = {sec[k] ? wa2 : wa1};
+                head_rmsnorm<T, 1>(xs, ws, lph, a.D, a.eps);
+                v1[k] = xs[0];
+            }
+        }
+    }
+
+    if (!ROT) {
+        // Per-head RMSNorm alone (ng_per_head_rmsnorm): store the normalised heads.
+#pragma unroll
+        for (int k = 0; k < HPL; ++k) {
+            if (!ok[k]) continue;
+            uint16_t* dst = sec[k] ? out2 : out1;
+            st16_stream(dst + off[k], v1[k]);
+            if (STYLE == 0) st16_stream(dst + off[k] + half, v2[k]);
+        }
+        return;
+    }
 
     const float p = static_cast<float>(__builtin_amdgcn_readfirstlane(a.pos[t]));
     float s0, c0, s1 = 0.0f, c1 = 0.0f;
@@ -282,8 +389,13 @@ static bool wave_rope_ok(int head_dim) { return head_dim == 64 || head_dim == 12
 template <typename T>
 static int launch_rope_wave(const char* name, void* out, const void* in, void* out2, const void* in2,
                             const int* positions, int tokens, int nh, int nh2, int head_dim, int style,
-                            const float* inv_freq) {
+                            const float* inv_freq, const void* w1 = nullptr, const void* w2 = nullptr,
+                            float eps = 0.0f, bool rotate = true) {
     RopeWaveArgs w{};
+    w.w1 = w1;
+    w.w2 = w2;
+    w.eps = eps;
+    const bool qknorm = w1 != nullptr;
     w.out = out;
     w.in = in;
     w.out2 = out2;
@@ -309,15 +421,23 @@ static int launch_rope_wave(const char* name, void* out, const void* in, void* o
     G = (npass + hpl - 1) / hpl;
     w.G = G;
     w.div_G = make_fastdiv(static_cast<uint32_t>(G));
-    for (int i = 0; i < head_dim / 2; ++i) w.inv_freq[i] = inv_freq[i];
+    if (inv_freq)
+        for (int i = 0; i < head_dim / 2; ++i) w.inv_freq[i] = inv_freq[i];
     const long long waves = static_cast<long long>(tokens) * G;
     NG_REQUIRE(waves < (1ll << 31), "%s: tensor too large", name);
     const unsigned blocks = static_cast<unsigned>((waves + 3) / 4);
     auto go = [&](auto kern) { kern<<<dim3(blocks), dim3(kRopeThreads), 0, stream()>>>(w); };
-#define NG_ROPE_WAVE(HPL)                                                 \
-    case HPL:                                                             \
-        if (style == 0) go(rope_wave_kernel<T, 0, HPL>);                  \
-        else go(rope_wave_kernel<T, 1, HPL>);                             \
+#define NG_ROPE_WAVE(HPL)                                                                   \
+    case HPL:                                                                               \
+        if (!rotate) {                                                                      \
+            go(rope_wave_kernel<T, 0, HPL, true, false>);                                   \
+        } else if (qknorm) {                                                                \
+            if (style == 0) go(rope_wave_kernel<T, 0, HPL, true>);                          \
+            else go(rope_wave_kernel<T, 1, HPL, true>);                                     \
+        } else {                                                                            \
+            if (style == 0) go(rope_wave_kernel<T, 0, HPL, false>);                         \
+            else go(rope_wave_kernel<T, 1, HPL, false>);                                    \
+        }                                                                                   \
         break;
     switch (hpl) {
         NG_ROPE_WAVE(1) NG_ROPE_WAVE(2) NG_ROPE_WAVE(3) NG_ROPE_WAVE(4)
@@ -471,4 +591,102 @@ extern "C" int ng_bf16_rope_qk_with_theta(void* q_out, const void* q_in, void* k
     return launch_rope_qk<bf16>("ng_bf16_rope_qk_with_theta", q_out, q_in, k_out, k_in, positions, batch_size,
                                 seq_len, num_q_heads, num_kv_heads, head_dim, rope_style, rope_theta,
                                 cuda_bf16_rope_with_theta);
+}
+
+// Per-head RMSNorm of Q and K followed by RoPE, in one launch (the QK
+// LayerNorm of gpu/engine/layer.cu:998-1013 and the RoPE pair of :1016-1018).
+// The normalisation is exactly ng_per_head_rmsnorm's, rounded to the element
+// type, and the rotation is cuda_rope_with_theta's applied to that result.
+// head_dim outside {64, 128, 256} or unaligned buffers take the two steps as
+// separate launches.
+template <typename T>
+static int launch_qk_norm_rope(const char* name, void* q_out, const void* q_in, void* k_out, const void* k_in,
+                               const void* q_weight, const void* k_weight, const int* positions, int batch_size,
+                               int seq_len, int num_q_heads, int num_kv_heads, int head_dim, float eps, int style,
+                               float theta,
+                               int (*norm)(void*, const void*, const void*, int, int, int, float),
+                               int (*rope)(void*, const void*, const int*, int, int, int, int, int, float)) {
+    NG_REQUIRE(q_out && q_in && k_out && k_in && q_weight && k_weight && positions, "%s: null pointer", name);
+    NG_REQUIRE(batch_size > 0 && seq_len > 0 && num_q_heads > 0 && num_kv_heads > 0,
+               "%s: batch=%d seq=%d q_heads=%d kv_heads=%d must be > 0", name, batch_size, seq_len, num_q_heads,
+               num_kv_heads);
+    NG_REQUIRE(head_dim >= 2 && head_dim % 2 == 0 && head_dim <= 2 * kRopeMaxHalf,
+               "%s: head_dim=%d must be even and in [2, %d]", name, head_dim, 2 * kRopeMaxHalf);
+    style = style == 1 ? 1 : 0;
+    const long long T64 = static_cast<long long>(batch_size) * seq_len;
+    NG_REQUIRE(T64 * num_q_heads * head_dim < (1ll << 31) && T64 * num_kv_heads * head_dim < (1ll << 31),
+               "%s: tensor too large", name);
+    const bool aligned = aligned16(q_out) && aligned16(q_in) && aligned16(k_out) && aligned16(k_in) &&
+                         aligned16(q_weight) && aligned16(k_weight);
+    if (!(aligned && wave_rope_ok(head_dim))) {
+        const int T32 = static_cast<int>(T64);
+        int rc = norm(q_out, q_in, q_weight, T32, num_q_heads, head_dim, eps);
+        if (rc == 0) rc = norm(k_out, k_in, k_weight, T32, num_kv_heads, head_dim, eps);
+        if (rc == 0) rc = rope(q_out, q_out, positions, batch_size, seq_len, num_q_heads, head_dim, style, theta);
+        if (rc == 0) rc = rope(k_out, k_out, positions, batch_size, seq_len, num_kv_heads, head_dim, style, theta);
+        return rc;
+    }
+    float inv[kRopeMaxHalf];
+    fill_inv_freq(theta, head_dim, inv);
+    const int rc = launch_rope_wave<T>(name, q_out, q_in, k_out, k_in, positions, static_cast<int>(T64), num_q_heads,
+                                       num_kv_heads, head_dim, style, inv, q_weight, k_weight, eps);
+    if (rc != 0) return rc;
+    NG_CHECK_LAUNCH(name);
+    return 0;
+}
+
+extern "C" int ng_qk_rmsnorm_rope_with_theta(void* q_out, const void* q_in, void* k_out, const void* k_in,
+                                             const void* q_norm_weight, const void* k_norm_weight,
+                                             const int* positions, int batch_size, int seq_len, int num_q_heads,
+                                             int num_kv_heads, int head_dim, float eps, int rope_style,
+                                             float rope_theta) {
+    return launch_qk_norm_rope<f16>("ng_qk_rmsnorm_rope_with_theta", q_out, q_in, k_out, k_in, q_norm_weight,
+                                    k_norm_weight, positions, batch_size, seq_len, num_q_heads, num_kv_heads,
+                                    head_dim, eps, rope_style, rope_theta, ng_per_head_rmsnorm,
+                                    cuda_rope_with_theta);
+}
+
+extern "C" int ng_bf16_qk_rmsnorm_rope_with_theta(void* q_out, const void* q_in, void* k_out, const void* k_in,
+                                                  const void* q_norm_weight, const void* k_norm_weight,
+                                                  const int* positions, int batch_size, int seq_len,
+                                                  int num_q_heads, int num_kv_heads, int head_dim, float eps,
+                                                  int rope_style, float rope_theta) {
+    return launch_qk_norm_rope<bf16>("ng_bf16_qk_rmsnorm_rope_with_theta", q_out, q_in, k_out, k_in, q_norm_weight,
+                                     k_norm_weight, positions, batch_size, seq_len, num_q_heads, num_kv_heads,
+                                     head_dim, eps, rope_style, rope_theta, ng_bf16_per_head_rmsnorm,
+                                     cuda_bf16_rope_with_theta);
+}
+
+// Per-head RMSNorm alone: the wave kernel without the rotation for head_dim
+// 64, 128 or 256 (a head is spread over head_dim / 16 lanes, every lane busy);
+// other head_dim or unaligned buffers use the row kernel over tokens * heads
+// rows of head_dim.
+template <typename T>
+static int launch_per_head_rmsnorm(const char* name, void* output, const void* input, const void* weight,
+                                   int num_tokens, int num_heads, int head_dim, float eps) {
+    NG_REQUIRE(output && input && weight, "%s: null pointer", name);
+    NG_REQUIRE(num_tokens > 0 && num_heads > 0 && head_dim > 0, "%s: tokens=%d heads=%d head_dim=%d must be > 0",
+               name, num_tokens, num_heads, head_dim);
+    NG_REQUIRE(static_cast<long long>(num_tokens) * num_heads * head_dim < (1ll << 31), "%s: tensor too large",
+               name);
+    if (aligned16(output) && aligned16(input) && aligned16(weight) && wave_rope_ok(head_dim)) {
+        const int rc = launch_rope_wave<T>(name, output, input, output, input, nullptr, num_tokens, num_heads, 0,
+                                           head_dim, 0, nullptr, weight, weight, eps, false);
+        if (rc != 0) return rc;
+        NG_CHECK_LAUNCH(name);
+        return 0;
+    }
+    return rows_rmsnorm<T>(name, output, input, weight, num_tokens * num_heads, head_dim, eps);
+}
+
+extern "C" int ng_per_head_rmsnorm(void* output, const void* input, const void* weight, int num_tokens,
+                                   int num_heads, int head_dim, float eps) {
+    return launch_per_head_rmsnorm<f16>("ng_per_head_rmsnorm", output, input, weight, num_tokens, num_heads,
+                                        head_dim, eps);
+}
+
+extern "C" int ng_bf16_per_head_rmsnorm(void* output, const void* input, const void* weight, int num_tokens,
+                                        int num_heads, int head_dim, float eps) {
+    return launch_per_head_rmsnorm<bf16>("ng_bf16_per_head_rmsnorm", output, input, weight, num_tokens, num_heads,
+                                         head_dim, eps);
 }
