@@ -456,6 +456,64 @@ def extra_kernels(L, hip, stream):
         p.free()
     for x in (wq, wk, pos):
         x.free()
+    out["gemm_int8"] = gemm_extras(L, hip, stream)
+    return out
+
+
+def gemm_extras(L, hip, stream):
+    """cuda_gemm_int8 at the INT8 projections of one Mistral-7B layer
+    (layer.cu:487-501,551,575: B int8 [N, K] with per-row scales), for M = 1
+    and 64 tokens, against the reference's composition without its cudaMalloc /
+    cudaFree (cuda_dequantize_weights into an fp16 buffer, then
+    cuda_gemm_fp16). Weight pools keep the codes cache-cold. Also q_proj at
+    prefill (M = 4096), where cuda_gemm_int8 dequantizes and calls hipBLASLt."""
+    rng = np.random.Generator(np.random.PCG64(0))
+    H, I = 4096, 14336
+    shapes = {"q_proj": (H, H), "k_proj": (H, 1024), "gate_proj": (H, I), "down_proj": (I, H)}
+    per_layer = {"q_proj": 2, "k_proj": 2, "gate_proj": 2, "down_proj": 1}   # q+o, k+v, gate+up, down
+    out, layer = {}, {1: [0.0, 0.0], 64: [0.0, 0.0]}
+    for name, (K, N) in shapes.items():
+        wq = rng.integers(-128, 128, (N, K)).astype(np.int8)
+        n = pool_slots(N * K)
+        wp = Pool(hip, wq.nbytes, n, wq)
+        del wq
+        sc = DB.from_array(rng.uniform(1e-3, 1e-2, N).astype(np.float32))
+        deq = DB(2 * N * K)
+        for M in (1, 64):
+            ab = DB.from_array(W.round_to(rng.standard_normal((M, K), dtype=np.float32), "f16"))
+            cp = Pool(hip, 2 * M * N, n)
+            th = [("gemm_int8", (lambda j=j: L.cuda_gemm_int8(cp.at(j), ab.vp, wp.at(j), sc.vp, M, K, N, True)))
+                  for j in range(n)]
+            us = time_pool_kernel(hip, stream, th)
+
+            def comp(j, M=M, ab=ab, cp=cp):
+                rc = L.cuda_dequantize_weights(deq.vp, wp.at(j), sc.vp, N, K, 1)
+                return rc or L.cuda_gemm_fp16(cp.at(j), ab.vp, deq.vp, M, K, N, False, True)
+
+            usc = time_pool_kernel(hip, stream, [("composed", (lambda j=j: comp(j))) for j in range(n)])
+            b = N * K + 2 * M * K + 2 * M * N + 4 * N
+            out[f"{name}_M{M}"] = {"us": us, "GBps": b / us / 1e3, "frac": b / us / 1e3 / PEAK_GBPS, "bytes": b,
+                                   "composed_us": usc, "buffer_sets": n}
+            layer[M][0] += per_layer[name] * us
+            layer[M][1] += per_layer[name] * usc
+            cp.free()
+            ab.free()
+        if name == "q_proj":
+            M = 4096
+            ab = DB.from_array(W.round_to(rng.standard_normal((M, K), dtype=np.float32), "f16"))
+            cb = DB(2 * M * N)
+            us = time_kernel(hip, stream, [lambda: L.cuda_gemm_int8(cb.vp, ab.vp, wp.at(0), sc.vp, M, K, N, True)],
+                             launches=8, reps=2)
+            out["q_proj_M4096"] = {"us": us, "TFLOPs": 2 * M * N * K / us / 1e6,
+                                   "note": "dequantize to fp16 + hipBLASLt fp16 GEMM"}
+            ab.free()
+            cb.free()
+        wp.free()
+        sc.free()
+        deq.free()
+    for M, (u, c) in layer.items():
+        out[f"mistral7b_layer_M{M}"] = {"us": u, "composed_us": c,
+                                        "note": "q, k, v, o, gate, up, down projections of one layer"}
     return out
 
 

@@ -1,0 +1,52 @@
+/* matmul.h - fp16 GEMM and int8-weight GEMM of libgpu_engine.so (gfx950 build).
+ *
+ * Drop-in replacement for the two GEMM entry points of the reference's
+ * gpu/cuda/matmul.h (lines 16-38) that the INT8 layer path calls
+ * (gpu/engine/layer.cu:487-501,551,575). All matrices are row-major.
+ *
+ * cuda_gemm_int8 computes C[M,N] = A[M,K] @ (B * scale)^T when transpose_b
+ * (B int8 [N,K], scale[n] per row of B, the engine's layout), or
+ * A @ (B * scale) when not (B int8 [K,N], scale[n] per column). Two paths:
+ *   - transpose_b, K % 64 == 0, M <= 64 (and N >= 2048 when M > 32),
+ *     16-byte aligned A and B: one fused kernel that streams the int8
+ *     weights once, converts them to fp16 exactly in registers, accumulates
+ *     A @ B^T on the matrix cores in fp32 and applies scale[n] to the sum.
+ *     No temporary, nothing allocated.
+ *   - otherwise: the weights are dequantized to fp16 (fp16(q * scale), as the
+ *     reference) into a per-stream buffer that grows on demand and is reused,
+ *     then multiplied by hipBLASLt with fp32 accumulation.
+ * The reference dequantizes into a fresh cudaMalloc'd copy on every call and
+ * multiplies with cublasHgemm (matmul.cu:189-244).
+ *
+ * cuda_gemm_fp16 is C = op(A) @ op(B) through hipBLASLt, fp32 accumulation.
+ *
+ * Both return 0, or -1 with one line on stderr. They launch on ng_get_stream().
+ * The first call for a (device, stream) allocates that pair's buffers (and, on
+ * the library path, a larger call grows them after synchronising the stream);
+ * a call that would allocate while the stream is being captured fails instead.
+ */
+#ifndef NG_MATMUL_H
+#define NG_MATMUL_H
+
+#include <stdbool.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* C[M,N] = op(A) @ op(B), fp16 in and out. A is [M,K] ([K,M] if transpose_a),
+ * B is [K,N] ([N,K] if transpose_b). Replaces matmul.h:16-25 (matmul.cu:75-156). */
+int cuda_gemm_fp16(void* c, const void* a, const void* b, int M, int K, int N,
+                   bool transpose_a, bool transpose_b);
+
+/* C[M,N] = A[M,K] @ (B * scale): A fp16, B int8 [K,N] (or [N,K] when
+ * transpose_b), scale fp32 [N], C fp16. Replaces matmul.h:27-38
+ * (matmul.cu:189-244). */
+int cuda_gemm_int8(void* c, const void* a, const void* b, const void* scale, int M,
+                   int K, int N, bool transpose_b);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* NG_MATMUL_H */

@@ -87,6 +87,9 @@ SIGNATURES: dict[str, tuple] = {
     "ng_qk_rmsnorm_rope_with_theta": (_i, [_vp, _cvp, _vp, _cvp, _cvp, _cvp, _ip, _i, _i, _i, _i, _i, _f, _i, _f]),
     "ng_bf16_qk_rmsnorm_rope_with_theta": (_i, [_vp, _cvp, _vp, _cvp, _cvp, _cvp, _ip, _i, _i, _i, _i, _i, _f, _i,
                                                 _f]),
+    # matmul.h
+    "cuda_gemm_fp16": (_i, [_vp, _cvp, _cvp, _i, _i, _i, C.c_bool, C.c_bool]),
+    "cuda_gemm_int8": (_i, [_vp, _cvp, _cvp, _cvp, _i, _i, _i, C.c_bool]),
 }
 
 _LIB = None

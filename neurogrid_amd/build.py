@@ -50,6 +50,11 @@ COMMON_FLAGS = [
 ]
 
 
+# hipBLASLt carries the GEMM half of cuda_gemm_fp16 / cuda_gemm_int8 (matmul.hip).
+ROCM_LIB = os.environ.get("ROCM_PATH", "/opt/rocm") + "/lib"
+LINK_FLAGS = [f"-L{ROCM_LIB}", "-lhipblaslt", f"-Wl,-rpath,{ROCM_LIB}"]
+
+
 def _run(cmd: list[str]) -> None:
     proc = subprocess.run(cmd, capture_output=True, text=True)
     # hipcc's host pass does not know the packed-fp32 feature and says so;
@@ -90,7 +95,7 @@ def build_library(jobs: int | None = None, verbose: bool = False) -> Path:
 
     out = LIBDIR / LIBNAME
     tmp = LIBDIR / (LIBNAME + ".tmp")
-    cmd = [HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", str(tmp), *map(str, objs)]
+    cmd = [HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", str(tmp), *map(str, objs), *LINK_FLAGS]
     if verbose:
         print(" ".join(cmd), flush=True)
     _run(cmd)

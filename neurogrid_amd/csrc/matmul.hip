@@ -1,0 +1,378 @@
+// matmul.hip - cuda_gemm_int8 and cuda_gemm_fp16 for gfx950.
+//
+// Reference: gpu/cuda/matmul.cu:75-156 (cuda_gemm_fp16: cublasHgemm with the
+// row-major -> column-major operand swap) and :169-244 (cuda_gemm_int8:
+// cudaMalloc a K*N fp16 copy, dequantize_and_copy, cuda_gemm_fp16, cudaFree).
+//
+// Weight-streaming path (transpose_b, small M). The engine's INT8 layers call
+// cuda_gemm_int8 with B stored [N, K] and one scale per row of B
+// (layer.cu:487-501,551,575). For a few tokens the product is bound by reading
+// B once, 1 byte per weight; the reference moves 5 (read int8, write fp16,
+// read fp16). Here one kernel reads the codes, turns them into exact fp16
+// integers in registers and feeds the matrix cores:
+//   C[m, n] = fp16( scale[n] * sum_k A[m, k] * q[n, k] )
+// with the sum in fp32 (every product of an fp16 activation and an integer
+// code in [-128, 127] is exact in fp32). The reference rounds q * scale to
+// fp16 first and sums those; the two differ by at most 2^-11 of
+// sum_k |A[m, k] * q[n, k] * scale[n]| plus the accumulation error.
+//
+// Layout of one wave's work: v_mfma_f32_16x16x32_f16 multiplies a 16 x 32
+// tile of A (rows m) by a 32 x 16 tile of B^T (columns n). Lane l supplies
+// row (l % 16) of each operand and 8 consecutive k starting at 8 * (l / 16);
+// the accumulator lane l holds rows 4 * (l / 16) + i, column l % 16. One
+// 16-byte load per lane covers 64 k of 16 rows of B (64 bytes per row per
+// instruction) and feeds two MFMAs; A is read from L2 at the same k.
+// A block's waves split K between them (chunk c goes to wave c % WAVES) and
+// add their partial sums through LDS in a fixed order, so results do not
+// depend on timing.
+#include "ng_common.hpp"
+#include "../../include/matmul.h"
+#include "../../include/neurogrid_ext.h"
+
+#include <hipblaslt/hipblaslt.h>
+
+#include <map>
+#include <mutex>
+#include <tuple>
+#include <utility>
+
+namespace ng {
+namespace {
+
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+constexpr int kChunk = 64;          // k per wave step
+constexpr int kMaxFusedM = 64;      // rows of A the weight-streaming path takes
+
+// Two int8 codes (bytes SEL0 and SEL1 of one dword) -> two exact fp16 values.
+// The bytes are biased to u = q + 128, placed under an fp16 exponent of 2^10
+// with v_perm (fp16 bits 0x6400 | u = 1024 + u), and 1152 is subtracted in
+// fp16: every step is exact.
+template <uint32_t SEL>
+__device__ __forceinline__ uint32_t codes_to_f16x2(uint32_t w) {
+    const f16x2 bias = {static_cast<f16>(-1152.0f), static_cast<f16>(-1152.0f)};
+    const f16x2 v = __builtin_bit_cast(f16x2, __builtin_amdgcn_perm(0x64646464u, w ^ 0x80808080u, SEL)) + bias;
+    return __builtin_bit_cast(uint32_t, v);
+}
+
+// 16 codes of one row of B -> the B operands of two MFMAs (codes 0-7, 8-15).
+__device__ __forceinline__ void codes16_to_operands(const u32x4 v, f16x8& b0, f16x8& b1) {
+    const u32x4 x = {codes_to_f16x2<0x04010400u>(v[0]), codes_to_f16x2<0x04030402u>(v[0]),
+                     codes_to_f16x2<0x04010400u>(v[1]), codes_to_f16x2<0x04030402u>(v[1])};
+    const u32x4 y = {codes_to_f16x2<0x04010400u>(v[2]), codes_to_f16x2<0x04030402u>(v[2]),
+                     codes_to_f16x2<0x04010400u>(v[3]), codes_to_f16x2<0x04030402u>(v[3])};
+    b0 = __builtin_bit_cast(f16x8, x);
+    b1 = __builtin_bit_cast(f16x8, y);
+}
+
+// MT tiles of 16 rows of A x NT tiles of 16 rows of B per block; WAVES waves
+// split K; each wave loads U chunks, then multiplies them.
+template <int MT, int NT, int WAVES, int U>
+__global__ __launch_bounds__(WAVES * kWave) void gemm_i8w_kernel(uint16_t* __restrict__ c,
+                                                                  const uint16_t* __restrict__ a,
+                                                                  const int8_t* __restrict__ b,
+                                                                  const float* __restrict__ scale, int M, int N,
+                                                                  int K) {
+    __shared__ f32x4 partial[WAVES - 1][MT * NT][kWave];
+    const int lane = threadIdx.x & (kWave - 1);
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
+    const int col = lane & 15;
+    const int grp = lane >> 4;
+    const int n0 = blockIdx.x * (16 * NT);
+
+    // Rows past N (M) are clamped to the last row: they are loaded and
+    // multiplied like the others, and their outputs are never stored.
+    const int8_t* bp[NT];
+#pragma unroll
+    for (int t = 0; t < NT; ++t) {
+        const int n = min(n0 + 16 * t + col, N - 1);
+        bp[t] = b + static_cast<size_t>(n) * K + 16 * grp;
+    }
+    const uint16_t* ap[MT];
+#pragma unroll
+    for (int t = 0; t < MT; ++t) {
+        const int m = min(16 * t + col, M - 1);
+        ap[t] = a + static_cast<size_t>(m) * K + 16 * grp;
+    }
+
+    f32x4 acc[MT][NT];
+#pragma unroll
+    for (int i = 0; i < MT; ++i)
+#pragma unroll
+        for (int j = 0; j < NT; ++j) acc[i][j] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+
+    // This wave's chunks are wave, wave + WAVES, ...
+    const int nchunks = K / kChunk;
+    const int cnt = wave < nchunks ? (nchunks - wave + WAVES - 1) / WAVES : 0;
+    if (cnt > 0) {
+        const int last = wave + (cnt - 1) * WAVES;
+        u32x4 bv[U][NT];
+        u32x4 av[U][MT][2];
+        auto load = [&](int slot, int i) {
+            // Chunks past this wave's last are clamped to it (and multiply zero codes).
+            const size_t k = static_cast<size_t>(min(wave + i * WAVES, last)) * kChunk;
+#pragma unroll
+            for (int t = 0; t < NT; ++t) bv[slot][t] = ld16_stream(bp[t] + k);
+#pragma unroll
+            for (int t = 0; t < MT; ++t) {
+                av[slot][t][0] = ld16(ap[t] + k);
+                av[slot][t][1] = ld16(ap[t] + k + 8);
+            }
+        };
+        auto multiply = [&](int u, bool valid) {
+            if (!valid) {
+#pragma unroll
+                for (int t = 0; t < NT; ++t) bv[u][t] = u32x4{0u, 0u, 0u, 0u};
+            }
+#pragma unroll
+            for (int t = 0; t < NT; ++t) {
+                f16x8 b0, b1;
+                codes16_to_operands(bv[u][t], b0, b1);
+#pragma unroll
+                for (int s = 0; s < MT; ++s) {
+                    acc[s][t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, av[u][s][0]), b0,
+                                                                       acc[s][t], 0, 0, 0);
+                    acc[s][t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, av[u][s][1]), b1,
+                                                                       acc[s][t], 0, 0, 0);
+                }
+            }
+        };
+        // U chunks are loaded, then multiplied. (Refilling each slot as soon as it
+        // is multiplied measured slower: the compiler then waits for all but the
+        // newest chunk at the top of every iteration.)
+        for (int i = 0; i < cnt; i += U) {
+#pragma unroll
+            for (int u = 0; u < U; ++u) load(u, i + u);
+            __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+            for (int u = 0; u < U; ++u) multiply(u, i + u < cnt);
+        }
+    }
+
+    if (wave > 0) {
+#pragma unroll
+        for (int i = 0; i < MT; ++i)
+#pragma unroll
+            for (int j = 0; j < NT; ++j) partial[wave - 1][i * NT + j][lane] = acc[i][j];
+    }
+    __syncthreads();
+    if (wave != 0) return;
+#pragma unroll
+    for (int j = 0; j < NT; ++j) {
+        const int n = n0 + 16 * j + col;
+        const float s = scale[min(n, N - 1)];
+#pragma unroll
+        for (int i = 0; i < MT; ++i) {
+            f32x4 v = acc[i][j];
+#pragma unroll
+            for (int w = 0; w < WAVES - 1; ++w) v += partial[w][i * NT + j][lane];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const int m = 16 * i + 4 * grp + e;
+                if (m < M && n < N) c[static_cast<size_t>(m) * N + n] = from_f32<f16>(v[e] * s);
+            }
+        }
+    }
+}
+
+template <int MT, int NT, int WAVES, int U>
+int launch_i8w(uint16_t* c, const uint16_t* a, const int8_t* b, const float* scale, int M, int N, int K) {
+    const unsigned blocks = static_cast<unsigned>((N + 16 * NT - 1) / (16 * NT));
+    gemm_i8w_kernel<MT, NT, WAVES, U>
+        <<<dim3(blocks), dim3(WAVES * kWave), 0, stream()>>>(c, a, b, scale, M, N, K);
+    NG_CHECK_LAUNCH("cuda_gemm_int8");
+    return 0;
+}
+
+// Tile shapes (NT, WAVES, U) by M and N, from a sweep on MI355X over
+// K x N in {4096 x 4096, 4096 x 1024, 4096 x 14336, 14336 x 4096}. Wide
+// weights (N >= 8192) have enough rows to give every block two row tiles,
+// which halves the reads of A per weight byte.
+int gemm_i8w(void* c, const void* a, const void* b, const void* scale, int M, int K, int N) {
+    auto* cp = static_cast<uint16_t*>(c);
+    auto* ap = static_cast<const uint16_t*>(a);
+    auto* bp = static_cast<const int8_t*>(b);
+    auto* sp = static_cast<const float*>(scale);
+    const bool wide = N >= 8192;
+    if (M <= 16) {
+        if (wide && M > 2) return launch_i8w<1, 2, 16, 4>(cp, ap, bp, sp, M, N, K);
+        return launch_i8w<1, 1, 8, 8>(cp, ap, bp, sp, M, N, K);
+    }
+    if (M <= 32) {
+        if (wide) return launch_i8w<2, 2, 8, 4>(cp, ap, bp, sp, M, N, K);
+        return launch_i8w<2, 1, 8, 4>(cp, ap, bp, sp, M, N, K);
+    }
+    if (wide) return launch_i8w<4, 2, 8, 2>(cp, ap, bp, sp, M, N, K);
+    return launch_i8w<4, 1, 8, 2>(cp, ap, bp, sp, M, N, K);
+}
+
+// The weight-streaming path takes transpose_b, M <= 64 and K % 64 == 0, except
+// 32 < M with narrow weights (N < 2048), where dequantize + hipBLASLt measured
+// faster (13.3 vs 19.8 us at M = 64, K = 4096, N = 1024).
+bool use_i8w(const void* a, const void* b, int M, int K, int N, bool transpose_b) {
+    if (!transpose_b || M > kMaxFusedM || K % kChunk != 0 || !aligned16(a) || !aligned16(b)) return false;
+    return M <= 32 || N >= 2048;
+}
+
+// ---- hipBLASLt path ----------------------------------------------------------
+constexpr size_t kLtWorkspace = size_t(32) << 20;
+
+#define NG_LT_CHECK(call)                                                                      \
+    do {                                                                                       \
+        hipblasStatus_t ng_st_ = (call);                                                       \
+        if (ng_st_ != HIPBLAS_STATUS_SUCCESS) {                                                \
+            fprintf(stderr, "neurogrid-amd: %s:%d: hipBLASLt status %d\n", __FILE__, __LINE__, \
+                    static_cast<int>(ng_st_));                                                 \
+            return -1;                                                                         \
+        }                                                                                      \
+    } while (0)
+
+struct Plan {
+    hipblasLtMatmulDesc_t desc = nullptr;
+    hipblasLtMatrixLayout_t lw = nullptr, lx = nullptr, ly = nullptr;
+    hipblasLtMatmulAlgo_t algo{};
+    size_t ws = 0;
+};
+
+// Buffers of one (device, stream) pair: the library workspace and the fp16
+// copy of the weights. Work on one stream is ordered, so reusing them from
+// call to call on that stream is safe; another stream gets its own.
+struct StreamBuffers {
+    void* ws = nullptr;
+    void* deq = nullptr;
+    size_t deq_bytes = 0;
+};
+
+using PlanKey = std::tuple<int, int, int, int, bool, bool>;  // device, M, K, N, transpose_a, transpose_b
+
+std::mutex g_mu;
+std::map<int, hipblasLtHandle_t> g_handles;
+std::map<PlanKey, Plan> g_plans;
+std::map<std::pair<int, hipStream_t>, StreamBuffers> g_buffers;
+
+int capturing(hipStream_t s, bool* out) {
+    hipStreamCaptureStatus st = hipStreamCaptureStatusNone;
+    NG_HIP_CHECK(hipStreamIsCapturing(s, &st));
+    *out = st != hipStreamCaptureStatusNone;
+    return 0;
+}
+
+// Buffers for (current device, stream), with the fp16 copy at least
+// deq_bytes long. Caller holds g_mu.
+int stream_buffers(int dev, hipStream_t s, size_t deq_bytes, StreamBuffers** out) {
+    StreamBuffers& sb = g_buffers[{dev, s}];
+    const bool need_ws = sb.ws == nullptr;
+    const bool need_deq = deq_bytes > sb.deq_bytes;
+    if (need_ws || need_deq) {
+        bool cap = false;
+        if (capturing(s, &cap) != 0) return -1;
+        NG_REQUIRE(!cap, "cuda_gemm: the stream is being captured and its buffers must be allocated or grown first; "
+                         "make one call of at least this size (%zu bytes) before capture", deq_bytes);
+    }
+    if (need_ws) NG_HIP_CHECK(hipMalloc(&sb.ws, kLtWorkspace));
+    if (need_deq) {
+        if (sb.deq != nullptr) {
+            // Earlier calls on this stream may still read the old copy.
+            NG_HIP_CHECK(hipStreamSynchronize(s));
+            NG_HIP_CHECK(hipFree(sb.deq));
+            sb.deq = nullptr;
+            sb.deq_bytes = 0;
+        }
+        NG_HIP_CHECK(hipMalloc(&sb.deq, deq_bytes));
+        sb.deq_bytes = deq_bytes;
+    }
+    *out = &sb;
+    return 0;
+}
+
+// Plan for row-major C[M,N] = op(A) @ op(B). hipBLASLt is column-major: the
+// row-major matrices are their transposes, so it computes C^T = op(B)^T op(A)^T
+// with B as its first operand (the same swap as matmul.cu:90-147).
+int get_plan(int dev, int M, int K, int N, bool ta, bool tb, const Plan** out) {
+    const PlanKey key{dev, M, K, N, ta, tb};
+    auto it = g_plans.find(key);
+    if (it != g_plans.end()) {
+        *out = &it->second;
+        return 0;
+    }
+    auto h = g_handles.find(dev);
+    if (h == g_handles.end()) {
+        hipblasLtHandle_t handle = nullptr;
+        NG_LT_CHECK(hipblasLtCreate(&handle));
+        h = g_handles.emplace(dev, handle).first;
+    }
+    Plan p;
+    NG_LT_CHECK(hipblasLtMatmulDescCreate(&p.desc, HIPBLAS_COMPUTE_32F, HIP_R_32F));
+    const int32_t op_w = tb ? HIPBLAS_OP_T : HIPBLAS_OP_N;
+    const int32_t op_x = ta ? HIPBLAS_OP_T : HIPBLAS_OP_N;
+    NG_LT_CHECK(hipblasLtMatmulDescSetAttribute(p.desc, HIPBLASLT_MATMUL_DESC_TRANSA, &op_w, sizeof(op_w)));
+    NG_LT_CHECK(hipblasLtMatmulDescSetAttribute(p.desc, HIPBLASLT_MATMUL_DESC_TRANSB, &op_x, sizeof(op_x)));
+    if (tb) NG_LT_CHECK(hipblasLtMatrixLayoutCreate(&p.lw, HIP_R_16F, K, N, K));
+    else NG_LT_CHECK(hipblasLtMatrixLayoutCreate(&p.lw, HIP_R_16F, N, K, N));
+    if (ta) NG_LT_CHECK(hipblasLtMatrixLayoutCreate(&p.lx, HIP_R_16F, M, K, M));
+    else NG_LT_CHECK(hipblasLtMatrixLayoutCreate(&p.lx, HIP_R_16F, K, M, K));
+    NG_LT_CHECK(hipblasLtMatrixLayoutCreate(&p.ly, HIP_R_16F, N, M, N));
+    hipblasLtMatmulPreference_t pref = nullptr;
+    NG_LT_CHECK(hipblasLtMatmulPreferenceCreate(&pref));
+    const uint64_t ws = kLtWorkspace;
+    NG_LT_CHECK(hipblasLtMatmulPreferenceSetAttribute(pref, HIPBLASLT_MATMUL_PREF_MAX_WORKSPACE_BYTES, &ws,
+                                                      sizeof(ws)));
+    hipblasLtMatmulHeuristicResult_t res{};
+    int found = 0;
+    const hipblasStatus_t st =
+        hipblasLtMatmulAlgoGetHeuristic(h->second, p.desc, p.lw, p.lx, p.ly, p.ly, pref, 1, &res, &found);
+    hipblasLtMatmulPreferenceDestroy(pref);
+    NG_LT_CHECK(st);
+    NG_REQUIRE(found > 0, "cuda_gemm: hipBLASLt has no kernel for M=%d K=%d N=%d", M, K, N);
+    p.algo = res.algo;
+    p.ws = res.workspaceSize;
+    *out = &g_plans.emplace(key, p).first->second;
+    return 0;
+}
+
+// C = op(A) @ op(B) through hipBLASLt. With q != nullptr, B is first
+// dequantized from the int8 codes q and their scales into this stream's fp16
+// copy (matmul.cu:205-236), and the copy is the B of the product.
+int gemm_lt(void* c, const void* a, const void* b, const void* q, const void* scale, int M, int K, int N, bool ta,
+            bool tb) {
+    int dev = 0;
+    NG_HIP_CHECK(hipGetDevice(&dev));
+    const hipStream_t s = stream();
+    std::lock_guard<std::mutex> lock(g_mu);
+    const Plan* p = nullptr;
+    if (get_plan(dev, M, K, N, ta, tb, &p) != 0) return -1;
+    StreamBuffers* sb = nullptr;
+    const size_t deq_bytes = q != nullptr ? static_cast<size_t>(K) * static_cast<size_t>(N) * 2 : 0;
+    if (stream_buffers(dev, s, deq_bytes, &sb) != 0) return -1;
+    if (q != nullptr) {
+        const int r = tb ? cuda_dequantize_weights(sb->deq, q, scale, N, K, 1)
+                         : cuda_dequantize_weights(sb->deq, q, scale, K, N, 0);
+        if (r != 0) return r;
+        b = sb->deq;
+    }
+    const float alpha = 1.0f, beta = 0.0f;
+    NG_LT_CHECK(hipblasLtMatmul(g_handles[dev], p->desc, &alpha, b, p->lw, a, p->lx, &beta, c, p->ly, c, p->ly,
+                                &p->algo, sb->ws, p->ws, s));
+    return 0;
+}
+
+}  // namespace
+}  // namespace ng
+
+using namespace ng;
+
+extern "C" int cuda_gemm_fp16(void* c, const void* a, const void* b, int M, int K, int N, bool transpose_a,
+                              bool transpose_b) {
+    NG_REQUIRE(c && a && b, "cuda_gemm_fp16: null pointer");
+    NG_REQUIRE(M > 0 && K > 0 && N > 0, "cuda_gemm_fp16: M=%d K=%d N=%d must be > 0", M, K, N);
+    return gemm_lt(c, a, b, nullptr, nullptr, M, K, N, transpose_a, transpose_b);
+}
+
+extern "C" int cuda_gemm_int8(void* c, const void* a, const void* b, const void* scale, int M, int K, int N,
+                              bool transpose_b) {
+    NG_REQUIRE(c && a && b && scale, "cuda_gemm_int8: null pointer");
+    NG_REQUIRE(M > 0 && K > 0 && N > 0, "cuda_gemm_int8: M=%d K=%d N=%d must be > 0", M, K, N);
+    if (use_i8w(a, b, M, K, N, transpose_b)) return gemm_i8w(c, a, b, scale, M, K, N);
+    return gemm_lt(c, a, nullptr, b, scale, M, K, N, false, transpose_b);
+}

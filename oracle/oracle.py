@@ -227,6 +227,32 @@ def dequant(q, scales, mode: str):
     return out
 
 
+def gemm_int8(a, q, scale, transpose_b: bool) -> np.ndarray:
+    """C = A @ (B * scale) as the reference composes it (gpu/cuda/matmul.cu:189-244).
+
+    The int8 weights are first dequantized to fp16 by dequantize_and_copy
+    (matmul.cu:169-186: fp16(float(q) * scale), scale per row of B when
+    transpose_b, per column otherwise; the same rule as ``dequant``), then
+    multiplied with the fp16 activations (cuda_gemm_fp16, matmul.cu:75-156).
+    a: fp16 bits [M, K]; q: int8 [N, K] if transpose_b else [K, N]; scale:
+    fp32 [N]. Returns the product of the two fp16 operands in float64, not
+    rounded: the reference's own GEMM rounding belongs to cuBLAS and is not
+    specified, so tests bound the distance to this value.
+    """
+    x = f16_bits_to_f32(_u16(a)).astype(np.float64)
+    w = f16_bits_to_f32(dequant(q, scale, "row" if transpose_b else "col")).astype(np.float64)
+    return x @ (w.T if transpose_b else w)
+
+
+def gemm_fp16(a, b, transpose_a: bool, transpose_b: bool) -> np.ndarray:
+    """C = op(A) @ op(B) of fp16 operands (gpu/cuda/matmul.cu:75-156), in
+    float64, not rounded. A is [M, K] ([K, M] if transpose_a), B is [K, N]
+    ([N, K] if transpose_b)."""
+    x = f16_bits_to_f32(_u16(a)).astype(np.float64)
+    w = f16_bits_to_f32(_u16(b)).astype(np.float64)
+    return (x.T if transpose_a else x) @ (w.T if transpose_b else w)
+
+
 def elementwise(op: str, a, b=None, s: float = 0.0, dtype: str = "f16") -> np.ndarray:
     a = _u16(a)
     b = _u16(b) if b is not None else a

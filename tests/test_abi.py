@@ -40,7 +40,7 @@ def test_headers_declare_the_reference_boundary():
         "ng_get_stream", "ng_set_stream", "cuda_init", "cuda_shutdown", "cuda_get_device_count",
         "cuda_set_device", "cuda_get_device_info", "cuda_sync_device", "cuda_get_memory_used",
         "cuda_malloc", "cuda_free", "cuda_copy_to_device", "cuda_copy_to_host",
-        "cuda_copy_int8_to_device", "cuda_copy_int8_to_host",
+        "cuda_copy_int8_to_device", "cuda_copy_int8_to_host", "cuda_gemm_int8",
     ]:
         assert sym in names, sym
 
@@ -92,6 +92,9 @@ def test_argument_errors_return_minus_one_without_touching_the_gpu(capfd):
     assert L.ng_rmsnorm_quant_int8(p, None, p, p, 1, 8, 1e-5) == -1
     assert L.cuda_dequantize_weights(p, p, p, 4, 0, 1) == -1
     assert L.cuda_copy_to_device(p, p, 4, 7) == -1               # unknown dtype code
+    assert L.cuda_gemm_int8(p, p, None, p, 4, 64, 16, True) == -1
+    assert L.cuda_gemm_int8(p, p, p, p, 4, 0, 16, True) == -1
+    assert L.cuda_gemm_fp16(p, None, p, 4, 64, 16, False, False) == -1
     err = capfd.readouterr().err
     assert "neurogrid-amd:" in err and "null pointer" in err
 

@@ -1,0 +1,253 @@
+"""cuda_gemm_int8 and cuda_gemm_fp16 on the GPU.
+
+Bars:
+  * exact inputs (activations on a grid 2^-e with |a| <= 1, so every partial
+    sum of A @ q is exact in fp32 whatever the summation order) give
+    bit-exact results: fp16(fp32(S) * scale[n]) on the weight-streaming path,
+    where S = sum_k a_k q_k; fp16(S') on the dequantize + hipBLASLt path with
+    power-of-two scales (fp16(q * s) exact, S' = sum_k a_k w_k exact);
+  * random inputs stay within ulp16(ref) + 2^-9 * sum_k |a_k w_k| of the
+    reference's composition (oracle.gemm_int8: fp16 weights fp16(q * s), then
+    the product), which covers the reference's rounding of w to fp16 (2^-11),
+    fp32 accumulation over K <= 16384 (K * 2^-24 < 2^-10) and the output
+    rounding;
+  * the reference's own tests (tests/matmul_test.go:19-255): the same shapes,
+    distributions and absolute tolerances.
+"""
+from __future__ import annotations
+
+import math
+
+import numpy as np
+import pytest
+
+from gpu_util import C, assert_bits_equal, banner, dev, empty, get, ok
+
+pytestmark = pytest.mark.gpu
+
+RNG = np.random.Generator(np.random.PCG64(31))
+
+
+def f16bits(x) -> np.ndarray:
+    return np.asarray(x, np.float32).astype(np.float16).view(np.uint16)
+
+
+def f16val(bits) -> np.ndarray:
+    return np.asarray(bits, np.uint16).view(np.float16).astype(np.float64)
+
+
+def exact_activations(M: int, K: int) -> np.ndarray:
+    """Values j * 2^-e in [-1, 1] with K * 128 * 2^e <= 2^23: every partial
+    sum of A @ q (|q| <= 128) is a multiple of 2^-e below 2^23 * 2^-e."""
+    e = min(6, 16 - math.ceil(math.log2(K)))
+    j = RNG.integers(-(2 ** e), 2 ** e + 1, size=(M, K))
+    return f16bits(j * 2.0 ** -e)
+
+
+def codes(shape) -> np.ndarray:
+    return RNG.integers(-128, 128, size=shape).astype(np.int8)
+
+
+def gemm_int8(lib, a, q, scale, M, K, N, tb: bool) -> np.ndarray:
+    ab, qb, sb = dev(a), dev(q), dev(np.asarray(scale, np.float32))
+    cb = empty(M * N * 2)
+    ok(lib.cuda_gemm_int8(cb.vp, ab.vp, qb.vp, sb.vp, M, K, N, tb), "cuda_gemm_int8")
+    return get(cb, np.uint16, (M, N))
+
+
+def gemm_fp16(lib, a, b, M, K, N, ta: bool, tb: bool) -> np.ndarray:
+    ab, bb = dev(a), dev(b)
+    cb = empty(M * N * 2)
+    ok(lib.cuda_gemm_fp16(cb.vp, ab.vp, bb.vp, M, K, N, ta, tb), "cuda_gemm_fp16")
+    return get(cb, np.uint16, (M, N))
+
+
+def ulp16(v) -> np.ndarray:
+    v = np.abs(np.asarray(v, np.float64))
+    return 2.0 ** (np.floor(np.log2(np.maximum(v, 2.0 ** -14))) - 10)
+
+
+def assert_within_bound(got_bits, a, q, scale, tb: bool, what: str, ora) -> None:
+    ref = ora.gemm_int8(a, q, scale, tb)
+    x = np.abs(f16val(a))
+    w = np.abs(f16val(ora.dequant(q, scale, "row" if tb else "col")))
+    mag = x @ (w.T if tb else w)
+    d = np.abs(f16val(got_bits) - ref)
+    bound = ulp16(ref) + 2.0 ** -9 * mag
+    bad = d > bound
+    assert not bad.any(), f"{what}: {bad.sum()} outside the bound; max |d| {d.max():.3g}, " \
+                          f"max |d|/bound {(d / bound).max():.3g}"
+
+
+# M, K, N: the weight-streaming path takes transpose_b, M <= 64 and K % 64 == 0
+# (and N >= 2048 when M > 32); N >= 8192 selects two row tiles per block.
+FUSED = [
+    (1, 4096, 4096), (3, 4096, 1024), (16, 4096, 4096), (17, 4096, 1000), (32, 1024, 512), (33, 4096, 4096),
+    (64, 4096, 4096), (64, 4096, 2048), (8, 14336, 4096), (64, 14336, 4096), (5, 64, 16), (2, 128, 7),
+    (64, 4096, 14336), (1, 4096, 14336), (5, 4096, 8192), (20, 1024, 8200), (40, 512, 8208), (2, 256, 9000),
+]
+
+
+@pytest.mark.parametrize("M,K,N", FUSED)
+def test_int8_weight_streaming_bit_exact(lib, M, K, N):
+    banner(f"gemm_int8 streaming exact M={M} K={K} N={N}")
+    a = exact_activations(M, K)
+    q = codes((N, K))
+    scale = RNG.uniform(1e-3, 1e-2, N).astype(np.float16).astype(np.float32)
+    got = gemm_int8(lib, a, q, scale, M, K, N, True)
+    S = f16val(a) @ q.astype(np.float64).T
+    want = (S.astype(np.float32) * scale[None, :]).astype(np.float16).view(np.uint16)
+    assert_bits_equal(got, want, "C")
+
+
+@pytest.mark.parametrize("M,K,N", [(1, 4096, 4096), (64, 4096, 2048), (16, 14336, 512), (30, 2048, 300),
+                                   (12, 4096, 14336)])
+def test_int8_weight_streaming_random(lib, ora, M, K, N):
+    banner(f"gemm_int8 streaming random M={M} K={K} N={N}")
+    a = f16bits(RNG.standard_normal((M, K)))
+    q = codes((N, K))
+    scale = RNG.uniform(1e-3, 1e-2, N).astype(np.float32)
+    got = gemm_int8(lib, a, q, scale, M, K, N, True)
+    assert_within_bound(got, a, q, scale, True, "C", ora)
+
+
+# The dequantize + hipBLASLt path: B [K, N] with per-column scales, M > 64,
+# K not a multiple of 64, or 32 < M with N < 2048.
+LIBRARY = [
+    (4, 256, 128, False), (65, 4096, 1024, True), (256, 1024, 512, False), (7, 200, 96, True),
+    (512, 4096, 4096, True), (33, 1024, 4096, False), (48, 4096, 1024, True),
+]
+
+
+@pytest.mark.parametrize("M,K,N,tb", LIBRARY)
+def test_int8_dequant_library_bit_exact(lib, M, K, N, tb):
+    banner(f"gemm_int8 library exact M={M} K={K} N={N} tb={tb}")
+    a = exact_activations(M, K)
+    q = codes((N, K) if tb else (K, N))
+    p = RNG.integers(6, 10, N)
+    scale = (2.0 ** -p).astype(np.float32)
+    got = gemm_int8(lib, a, q, scale, M, K, N, tb)
+    w = q.astype(np.float64) * scale[:, None] if tb else q.astype(np.float64) * scale[None, :]
+    S = f16val(a) @ (w.T if tb else w)
+    assert_bits_equal(got, S.astype(np.float16).view(np.uint16), "C")
+
+
+@pytest.mark.parametrize("M,K,N,tb", [(65, 4096, 1024, True), (16, 1024, 512, False), (100, 960, 200, True)])
+def test_int8_dequant_library_random(lib, ora, M, K, N, tb):
+    banner(f"gemm_int8 library random M={M} K={K} N={N} tb={tb}")
+    a = f16bits(RNG.standard_normal((M, K)))
+    q = codes((N, K) if tb else (K, N))
+    scale = RNG.uniform(1e-3, 1e-2, N).astype(np.float32)
+    got = gemm_int8(lib, a, q, scale, M, K, N, tb)
+    assert_within_bound(got, a, q, scale, tb, "C", ora)
+
+
+def test_int8_paths_agree(lib, ora):
+    """The same product through both paths (M <= 64 streams, M = 65 goes
+    through the library): rows shared by the two calls agree to the bound."""
+    banner("gemm_int8 both paths")
+    K, N = 4096, 2048
+    a = f16bits(RNG.standard_normal((65, K)))
+    q = codes((N, K))
+    scale = RNG.uniform(1e-3, 1e-2, N).astype(np.float32)
+    big = gemm_int8(lib, a, q, scale, 65, K, N, True)
+    small = gemm_int8(lib, a[:64], q, scale, 64, K, N, True)
+    assert_within_bound(big[:64], a[:64], q, scale, True, "library", ora)
+    assert_within_bound(small, a[:64], q, scale, True, "streaming", ora)
+
+
+def test_int8_streaming_is_deterministic(lib):
+    banner("gemm_int8 streaming repeat")
+    M, K, N = 16, 4096, 4096
+    a = f16bits(RNG.standard_normal((M, K)))
+    q = codes((N, K))
+    scale = RNG.uniform(1e-3, 1e-2, N).astype(np.float32)
+    ab, qb, sb = dev(a), dev(q), dev(scale)
+    outs = []
+    for _ in range(3):
+        cb = empty(M * N * 2)
+        ok(lib.cuda_gemm_int8(cb.vp, ab.vp, qb.vp, sb.vp, M, K, N, True))
+        outs.append(get(cb, np.uint16, (M, N)))
+    assert_bits_equal(outs[1], outs[0], "repeat 1")
+    assert_bits_equal(outs[2], outs[0], "repeat 2")
+
+
+def test_int8_library_buffer_grows(lib):
+    """The per-stream fp16 weight copy grows from a small call to a larger one
+    and is reused by a smaller one after that."""
+    banner("gemm_int8 library buffer growth")
+    for (M, K, N) in [(70, 128, 64), (70, 2048, 2048), (70, 256, 64)]:
+        a = exact_activations(M, K)
+        q = codes((K, N))
+        scale = np.full(N, 2.0 ** -7, np.float32)
+        got = gemm_int8(lib, a, q, scale, M, K, N, False)
+        S = f16val(a) @ (q.astype(np.float64) * 2.0 ** -7)
+        assert_bits_equal(got, S.astype(np.float16).view(np.uint16), f"C {M}x{K}x{N}")
+
+
+@pytest.mark.parametrize("ta", [False, True])
+@pytest.mark.parametrize("tb", [False, True])
+@pytest.mark.parametrize("M,K,N", [(32, 128, 64), (5, 96, 40), (256, 1024, 384)])
+def test_fp16_gemm_bit_exact(lib, M, K, N, ta, tb):
+    banner(f"gemm_fp16 exact M={M} K={K} N={N} ta={ta} tb={tb}")
+    # A on a 2^-3 grid in [-1, 1], B on a 2^-3 grid in [-1, 1]: sums exact in fp32.
+    a = f16bits(RNG.integers(-8, 9, (K, M) if ta else (M, K)) / 8.0)
+    b = f16bits(RNG.integers(-8, 9, (N, K) if tb else (K, N)) / 8.0)
+    got = gemm_fp16(lib, a, b, M, K, N, ta, tb)
+    x, w = f16val(a), f16val(b)
+    S = (x.T if ta else x) @ (w.T if tb else w)
+    assert_bits_equal(got, S.astype(np.float16).view(np.uint16), "C")
+
+
+# ---- the reference's own tests (tests/matmul_test.go) -------------------------
+
+def _ref_uniform(n):
+    return RNG.random(n, dtype=np.float32) * 2 - 1
+
+
+def _cpu_matmul(a, b):
+    return (a.astype(np.float32) @ b.astype(np.float32)).astype(np.float32)
+
+
+def test_reference_kat_gemm_fp16(lib):
+    """TestGEMMFP16 (matmul_test.go:19-92): [32,128] x [128,64], U(-1,1), max |d| < 0.1."""
+    banner("reference TestGEMMFP16")
+    M, K, N = 32, 128, 64
+    A = _ref_uniform(M * K).reshape(M, K)
+    B = _ref_uniform(K * N).reshape(K, N)
+    got = f16val(gemm_fp16(lib, f16bits(A), f16bits(B), M, K, N, False, False))
+    assert np.abs(got - _cpu_matmul(A, B)).max() < 0.1
+
+
+def test_reference_kat_gemm_int8(lib):
+    """TestGEMMINT8 (matmul_test.go:98-179): A [32,128] U(-1,1), B int8 [128,64]
+    uniform over [-128,127], scales 0.01, transpose_b false, max |d| < 5e-2."""
+    banner("reference TestGEMMINT8")
+    M, K, N = 32, 128, 64
+    A = _ref_uniform(M * K).reshape(M, K)
+    q = codes((K, N))
+    scale = np.full(N, 0.01, np.float32)
+    got = f16val(gemm_int8(lib, f16bits(A), q, scale, M, K, N, False))
+    assert np.abs(got - _cpu_matmul(A, q.astype(np.float32) * scale[None, :])).max() < 5e-2
+
+
+def test_reference_kat_gemm_int8_engine_layout(lib):
+    """TestGEMMINT8's data in the engine's layout (B [N, K], transpose_b), which
+    takes the weight-streaming path."""
+    banner("reference TestGEMMINT8, transpose_b")
+    M, K, N = 32, 128, 64
+    A = _ref_uniform(M * K).reshape(M, K)
+    q = codes((N, K))
+    scale = np.full(N, 0.01, np.float32)
+    got = f16val(gemm_int8(lib, f16bits(A), q, scale, M, K, N, True))
+    assert np.abs(got - _cpu_matmul(A, (q.astype(np.float32) * scale[:, None]).T)).max() < 5e-2
+
+
+def test_reference_kat_gemm_transpose(lib):
+    """TestGEMMTranspose (matmul_test.go:183-255): A stored [K, M], C = A^T @ B, max |d| < 0.1."""
+    banner("reference TestGEMMTranspose")
+    M, K, N = 32, 128, 64
+    A = _ref_uniform(K * M).reshape(K, M)
+    B = _ref_uniform(K * N).reshape(K, N)
+    got = f16val(gemm_fp16(lib, f16bits(A), f16bits(B), M, K, N, True, False))
+    assert np.abs(got - _cpu_matmul(A.T, B)).max() < 0.1

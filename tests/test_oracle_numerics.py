@@ -435,6 +435,78 @@ def test_dequant_reference_kat(ora):
     assert (np.abs(out - codes * np.float32(0.01)) > 1e-3).sum() < 10
 
 
+# --------------------------------------------------------------- int8-weight GEMM
+
+def _gemm_int8_loops(a_bits, q, scale, transpose_b):
+    """matmul.cu:169-244 written out element by element: w = fp16(float(q) *
+    scale) in the stored layout, then C[m, n] = sum_k A[m, k] * w(k, n)."""
+    a = a_bits.view(np.float16)
+    M, K = a.shape
+    N = q.shape[0] if transpose_b else q.shape[1]
+    C = np.zeros((M, N))
+    for m in range(M):
+        for n in range(N):
+            acc = Fraction(0)
+            for k in range(K):
+                code = int(q[n, k] if transpose_b else q[k, n])
+                w = np.float16(np.float32(code) * np.float32(scale[n]))
+                acc += Fraction(float(a[m, k])) * Fraction(float(w))
+            C[m, n] = float(acc)
+    return C
+
+
+@pytest.mark.parametrize("transpose_b", [False, True])
+def test_gemm_int8_oracle_matches_loops(ora, transpose_b):
+    M, K, N = 3, 7, 5
+    a = RNG.standard_normal((M, K)).astype(np.float16).view(np.uint16)
+    q = RNG.integers(-128, 128, (N, K) if transpose_b else (K, N)).astype(np.int8)
+    scale = RNG.uniform(1e-3, 1e-2, N).astype(np.float32)
+    got = ora.gemm_int8(a, q, scale, transpose_b)
+    want = _gemm_int8_loops(a, q, scale, transpose_b)
+    assert np.allclose(got, want, rtol=1e-12, atol=1e-15)
+
+
+def test_gemm_int8_oracle_identity_rows_are_the_fp16_weights(ora):
+    """A = I picks out the dequantized weights: C[m, n] = fp16(q[n, m] * s[n])
+    (transpose_b), which is exact, so the scale index per row of B is pinned."""
+    K = N = 16
+    a = np.eye(K, dtype=np.float16).view(np.uint16)
+    q = RNG.integers(-128, 128, (N, K)).astype(np.int8)
+    scale = RNG.uniform(1e-3, 1e-2, N).astype(np.float32)
+    C = ora.gemm_int8(a, q, scale, True)
+    w = (q.astype(np.float32) * scale[:, None]).astype(np.float16).astype(np.float64)
+    assert (C == w.T).all()
+    Ccol = ora.gemm_int8(a, q.T.copy(), scale, False)
+    assert (Ccol == w.T).all()
+
+
+def test_gemm_int8_oracle_reference_kat(ora):
+    """TestGEMMINT8 (tests/matmul_test.go:98-179): [32,128] x [128,64], A U(-1,1),
+    codes U{-128..127}, scales 0.01: the oracle (fp16 A and w) stays within the
+    test's 5e-2 of the fp32 CPU matmul of the unrounded data."""
+    M, K, N = 32, 128, 64
+    A = RNG.random((M, K), dtype=np.float32) * 2 - 1
+    q = RNG.integers(-128, 128, (K, N)).astype(np.int8)
+    scale = np.full(N, 0.01, np.float32)
+    C = ora.gemm_int8(A.astype(np.float16).view(np.uint16), q, scale, False)
+    ref = A @ (q.astype(np.float32) * scale[None, :])
+    assert np.abs(C - ref).max() < 5e-2
+
+
+@pytest.mark.parametrize("ta", [False, True])
+@pytest.mark.parametrize("tb", [False, True])
+def test_gemm_fp16_oracle_transposes(ora, ta, tb):
+    M, K, N = 4, 6, 3
+    a = RNG.standard_normal((K, M) if ta else (M, K)).astype(np.float16)
+    b = RNG.standard_normal((N, K) if tb else (K, N)).astype(np.float16)
+    got = ora.gemm_fp16(a.view(np.uint16), b.view(np.uint16), ta, tb)
+    for m in range(M):
+        for n in range(N):
+            s = sum(Fraction(float(a[k, m] if ta else a[m, k])) * Fraction(float(b[n, k] if tb else b[k, n]))
+                    for k in range(K))
+            assert got[m, n] == pytest.approx(float(s), rel=1e-12, abs=1e-15)
+
+
 # --------------------------------------------------------------- gather, softmax
 
 def test_gather_reference_byte_pattern_kat(ora):
