@@ -7,11 +7,12 @@
  * cuda_gemm_int8 computes C[M,N] = A[M,K] @ (B * scale)^T when transpose_b
  * (B int8 [N,K], scale[n] per row of B, the engine's layout), or
  * A @ (B * scale) when not (B int8 [K,N], scale[n] per column). Two paths:
- *   - transpose_b, K % 64 == 0, M <= 64 (and N >= 2048 when M > 32),
- *     16-byte aligned A and B: one fused kernel that streams the int8
- *     weights once, converts them to fp16 exactly in registers, accumulates
- *     A @ B^T on the matrix cores in fp32 and applies scale[n] to the sum.
- *     No temporary, nothing allocated.
+ *   - transpose_b, K % 64 == 0, M <= 128, 16-byte aligned A and B: the int8
+ *     weights are read once, converted to fp16 exactly in registers and
+ *     multiplied on the matrix cores with fp32 sums; scale[n] is applied to
+ *     the sum. No fp16 copy of the weights. For M > 4 the sum over K may be
+ *     split into up to 8 slices whose fp32 partial sums (a per-stream buffer
+ *     of S * M * N floats) a second kernel adds in a fixed order.
  *   - otherwise: the weights are dequantized to fp16 (fp16(q * scale), as the
  *     reference) into a per-stream buffer that grows on demand and is reused,
  *     then multiplied by hipBLASLt with fp32 accumulation.
@@ -21,9 +22,11 @@
  * cuda_gemm_fp16 is C = op(A) @ op(B) through hipBLASLt, fp32 accumulation.
  *
  * Both return 0, or -1 with one line on stderr. They launch on ng_get_stream().
- * The first call for a (device, stream) allocates that pair's buffers (and, on
- * the library path, a larger call grows them after synchronising the stream);
- * a call that would allocate while the stream is being captured fails instead.
+ * Buffers (library workspace, fp16 weight copy, partial sums) belong to a
+ * (device, stream) pair; the first call that needs one allocates it and a
+ * larger call grows it after synchronising the stream. A call that would
+ * allocate while the stream is being captured fails instead: make one call
+ * of each shape before capture.
  */
 #ifndef NG_MATMUL_H
 #define NG_MATMUL_H

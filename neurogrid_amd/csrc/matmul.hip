@@ -4,12 +4,12 @@
 // row-major -> column-major operand swap) and :169-244 (cuda_gemm_int8:
 // cudaMalloc a K*N fp16 copy, dequantize_and_copy, cuda_gemm_fp16, cudaFree).
 //
-// Weight-streaming path (transpose_b, small M). The engine's INT8 layers call
+// Weight-streaming path (transpose_b, M <= 128). The engine's INT8 layers call
 // cuda_gemm_int8 with B stored [N, K] and one scale per row of B
-// (layer.cu:487-501,551,575). For a few tokens the product is bound by reading
-// B once, 1 byte per weight; the reference moves 5 (read int8, write fp16,
-// read fp16). Here one kernel reads the codes, turns them into exact fp16
-// integers in registers and feeds the matrix cores:
+// (layer.cu:487-501,551,575). For up to a few hundred tokens the product is
+// bound by reading B once, 1 byte per weight; the reference moves 5 (read
+// int8, write fp16, read fp16). Here the kernel reads the codes, turns them
+// into exact fp16 integers in registers and feeds the matrix cores:
 //   C[m, n] = fp16( scale[n] * sum_k A[m, k] * q[n, k] )
 // with the sum in fp32 (every product of an fp16 activation and an integer
 // code in [-128, 127] is exact in fp32). The reference rounds q * scale to
@@ -18,10 +18,11 @@
 //
 // Layout of one wave's work: v_mfma_f32_16x16x32_f16 multiplies a 16 x 32
 // tile of A (rows m) by a 32 x 16 tile of B^T (columns n). Lane l supplies
-// row (l % 16) of each operand and 8 consecutive k starting at 8 * (l / 16);
-// the accumulator lane l holds rows 4 * (l / 16) + i, column l % 16. One
-// 16-byte load per lane covers 64 k of 16 rows of B (64 bytes per row per
-// instruction) and feeds two MFMAs; A is read from L2 at the same k.
+// row (l % 16) of each operand and 8 values of k; the accumulator lane l holds
+// rows 4 * (l / 16) + i, column l % 16. In a chunk of 64 k, lane group
+// g = l / 16 loads k = 16g .. 16g + 15 of its row of B with one 16-byte load
+// (64 bytes per row per instruction); the first 8 feed one MFMA and the last
+// 8 another, and A's lanes take the same k, so each MFMA sums matching k.
 // A block's waves split K between them (chunk c goes to wave c % WAVES) and
 // add their partial sums through LDS in a fixed order, so results do not
 // depend on timing.
@@ -43,7 +44,10 @@ typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 
 constexpr int kChunk = 64;          // k per wave step
-constexpr int kMaxFusedM = 64;      // rows of A the weight-streaming path takes
+#ifndef NG_I8W_MAX_M
+#define NG_I8W_MAX_M 128
+#endif
+constexpr int kMaxFusedM = NG_I8W_MAX_M;  // rows of A the weight-streaming path takes
 
 // Two int8 codes (bytes SEL0 and SEL1 of one dword) -> two exact fp16 values.
 // The bytes are biased to u = q + 128, placed under an fp16 exponent of 2^10
@@ -185,35 +189,123 @@ int launch_i8w(uint16_t* c, const uint16_t* a, const int8_t* b, const float* sca
     return 0;
 }
 
-// Tile shapes (NT, WAVES, U) by M and N, from a sweep on MI355X over
-// K x N in {4096 x 4096, 4096 x 1024, 4096 x 14336, 14336 x 4096}. Wide
-// weights (N >= 8192) have enough rows to give every block two row tiles,
-// which halves the reads of A per weight byte.
-int gemm_i8w(void* c, const void* a, const void* b, const void* scale, int M, int K, int N) {
-    auto* cp = static_cast<uint16_t*>(c);
-    auto* ap = static_cast<const uint16_t*>(a);
-    auto* bp = static_cast<const int8_t*>(b);
-    auto* sp = static_cast<const float*>(scale);
-    const bool wide = N >= 8192;
-    if (M <= 16) {
-        if (wide && M > 2) return launch_i8w<1, 2, 16, 4>(cp, ap, bp, sp, M, N, K);
-        return launch_i8w<1, 1, 8, 8>(cp, ap, bp, sp, M, N, K);
+// ---- split-K variant --------------------------------------------------------
+// For more than a few rows of A the kernel above reads A from L2 once per
+// 16 rows of B: at M = 64 that is 8 bytes of A per weight byte. Here a block
+// of kSplitWaves waves owns 16 * kSplitWaves rows of B and one of S slices of
+// K; the A columns of each batch of U chunks are staged once in LDS and shared
+// by the block's waves (2M / (16 * kSplitWaves) bytes of A per weight byte).
+// With S > 1 each block stores its fp32 partial sums in `part` [S][M][N] and a
+// second kernel adds the S slices in slice order, so the result does not
+// depend on timing. (Having the last block of each tile add them instead needs
+// an agent-scope release and acquire per block, which on MI355X write back and
+// invalidate the whole L2: measured 3-5x slower.)
+constexpr int kSplitWaves = 4;
+constexpr int kSplitU = 4;
+
+template <int MT, int U>
+__global__ __launch_bounds__(kSplitWaves * kWave) void gemm_i8w_split_kernel(
+    uint16_t* __restrict__ c, const uint16_t* __restrict__ a, const int8_t* __restrict__ b,
+    const float* __restrict__ scale, float* __restrict__ part, int M, int N, int K, int S, int tiles, int cps) {
+    constexpr int kRowBytes = U * kChunk * 2 + 16;  // one row of a batch of A in LDS, padded by 16 bytes
+    constexpr int kPieces = 16 * MT * U * 8;        // 16-byte pieces of A per batch
+    constexpr int kThreads = kSplitWaves * kWave;
+    static_assert(kPieces % kThreads == 0, "A pieces must divide among the threads");
+    __shared__ __align__(16) uint8_t lds_a[16 * MT * kRowBytes];
+
+    const int sl = blockIdx.x % S;
+    const int tile = blockIdx.x / S;
+
+    const int tid = threadIdx.x;
+    const int lane = tid & (kWave - 1);
+    const int wave = __builtin_amdgcn_readfirstlane(tid / kWave);
+    const int col = lane & 15;
+    const int grp = lane >> 4;
+    const int nchunks = K / kChunk;
+    const int c0 = sl * cps;
+    const int c1 = min(c0 + cps, nchunks);
+    const int n = tile * (16 * kSplitWaves) + 16 * wave + col;
+    const int8_t* brow = b + static_cast<size_t>(min(n, N - 1)) * K + 16 * grp;
+
+    f32x4 acc[MT];
+#pragma unroll
+    for (int i = 0; i < MT; ++i) acc[i] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+
+    for (int cb = c0; cb < c1; cb += U) {
+        u32x4 bv[U];
+#pragma unroll
+        for (int u = 0; u < U; ++u) bv[u] = ld16_stream(brow + static_cast<size_t>(min(cb + u, c1 - 1)) * kChunk);
+        u32x4 ar[kPieces / kThreads];
+#pragma unroll
+        for (int j = 0; j < kPieces / kThreads; ++j) {
+            const int pc = j * kThreads + tid;
+            const int row = pc / (U * 8);
+            const int q = pc % (U * 8);
+            const int ch = min(cb + q / 8, c1 - 1);
+            ar[j] = ld16(a + static_cast<size_t>(min(row, M - 1)) * K + ch * kChunk + 8 * (q % 8));
+        }
+        __syncthreads();  // the previous batch has been read from LDS
+#pragma unroll
+        for (int j = 0; j < kPieces / kThreads; ++j) {
+            const int pc = j * kThreads + tid;
+            const int row = pc / (U * 8);
+            const int q = pc % (U * 8);
+            *reinterpret_cast<u32x4*>(lds_a + row * kRowBytes + (q / 8) * (kChunk * 2) + 16 * (q % 8)) = ar[j];
+        }
+        __syncthreads();
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            if (cb + u >= c1) bv[u] = u32x4{0u, 0u, 0u, 0u};  // a clamped chunk multiplies zero codes
+            f16x8 b0, b1;
+            codes16_to_operands(bv[u], b0, b1);
+#pragma unroll
+            for (int t = 0; t < MT; ++t) {
+                const uint8_t* ap = lds_a + (16 * t + col) * kRowBytes + u * (kChunk * 2) + 32 * grp;
+                const u32x4 a0 = *reinterpret_cast<const u32x4*>(ap);
+                const u32x4 a1 = *reinterpret_cast<const u32x4*>(ap + 16);
+                acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, a0), b0, acc[t], 0, 0, 0);
+                acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, a1), b1, acc[t], 0, 0, 0);
+            }
+        }
     }
-    if (M <= 32) {
-        if (wide) return launch_i8w<2, 2, 8, 4>(cp, ap, bp, sp, M, N, K);
-        return launch_i8w<2, 1, 8, 4>(cp, ap, bp, sp, M, N, K);
+
+    if (S == 1) {
+        if (n < N) {
+            const float sc = scale[n];
+#pragma unroll
+            for (int t = 0; t < MT; ++t)
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    const int m = 16 * t + 4 * grp + e;
+                    if (m < M) c[static_cast<size_t>(m) * N + n] = from_f32<f16>(acc[t][e] * sc);
+                }
+        }
+        return;
     }
-    if (wide) return launch_i8w<4, 2, 8, 2>(cp, ap, bp, sp, M, N, K);
-    return launch_i8w<4, 1, 8, 2>(cp, ap, bp, sp, M, N, K);
+    if (n < N) {
+        float* mine = part + static_cast<size_t>(sl) * M * N;
+#pragma unroll
+        for (int t = 0; t < MT; ++t)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const int m = 16 * t + 4 * grp + e;
+                if (m < M) mine[static_cast<size_t>(m) * N + n] = acc[t][e];
+            }
+    }
 }
 
-// The weight-streaming path takes transpose_b, M <= 64 and K % 64 == 0, except
-// 32 < M with narrow weights (N < 2048), where dequantize + hipBLASLt measured
-// faster (13.3 vs 19.8 us at M = 64, K = 4096, N = 1024).
-bool use_i8w(const void* a, const void* b, int M, int K, int N, bool transpose_b) {
-    if (!transpose_b || M > kMaxFusedM || K % kChunk != 0 || !aligned16(a) || !aligned16(b)) return false;
-    return M <= 32 || N >= 2048;
+// C[m, n] = fp16(scale[n] * sum over slices q = 0 .. S-1, in that order, of
+// part[q][m][n]). One thread per element.
+__global__ __launch_bounds__(256) void split_reduce_kernel(uint16_t* __restrict__ c, const float* __restrict__ part,
+                                                           const float* __restrict__ scale, int M, int N, int S) {
+    const size_t i = static_cast<size_t>(blockIdx.x) * 256 + threadIdx.x;
+    const size_t mn = static_cast<size_t>(M) * N;
+    if (i >= mn) return;
+    float v = part[i];
+    for (int q = 1; q < S; ++q) v += part[static_cast<size_t>(q) * mn + i];
+    c[i] = from_f32<f16>(v * scale[i % N]);
 }
+
 
 // ---- hipBLASLt path ----------------------------------------------------------
 constexpr size_t kLtWorkspace = size_t(32) << 20;
@@ -235,13 +327,17 @@ struct Plan {
     size_t ws = 0;
 };
 
-// Buffers of one (device, stream) pair: the library workspace and the fp16
-// copy of the weights. Work on one stream is ordered, so reusing them from
-// call to call on that stream is safe; another stream gets its own.
+// Buffers of one (device, stream) pair: the library workspace, the fp16 copy
+// of the weights, and the split-K partial sums. Work on one
+// stream is ordered, so reusing them from call to call on that stream is safe;
+// another stream gets its own.
 struct StreamBuffers {
     void* ws = nullptr;
+    size_t ws_bytes = 0;
     void* deq = nullptr;
     size_t deq_bytes = 0;
+    void* part = nullptr;
+    size_t part_bytes = 0;
 };
 
 using PlanKey = std::tuple<int, int, int, int, bool, bool>;  // device, M, K, N, transpose_a, transpose_b
@@ -258,31 +354,25 @@ int capturing(hipStream_t s, bool* out) {
     return 0;
 }
 
-// Buffers for (current device, stream), with the fp16 copy at least
-// deq_bytes long. Caller holds g_mu.
-int stream_buffers(int dev, hipStream_t s, size_t deq_bytes, StreamBuffers** out) {
-    StreamBuffers& sb = g_buffers[{dev, s}];
-    const bool need_ws = sb.ws == nullptr;
-    const bool need_deq = deq_bytes > sb.deq_bytes;
-    if (need_ws || need_deq) {
-        bool cap = false;
-        if (capturing(s, &cap) != 0) return -1;
-        NG_REQUIRE(!cap, "cuda_gemm: the stream is being captured and its buffers must be allocated or grown first; "
-                         "make one call of at least this size (%zu bytes) before capture", deq_bytes);
+// Make *p hold at least `need` bytes (zeroed if `zero`). Growing while the
+// stream is being captured is refused: allocation cannot be captured. Caller
+// holds g_mu.
+int grow(hipStream_t s, void** p, size_t* have, size_t need, bool zero) {
+    if (need <= *have) return 0;
+    bool cap = false;
+    if (capturing(s, &cap) != 0) return -1;
+    NG_REQUIRE(!cap, "cuda_gemm: the stream is being captured and a buffer of %zu bytes must be allocated first; "
+                     "make one call of this shape on the stream before capture", need);
+    if (*p != nullptr) {
+        // Earlier calls on this stream may still use the old buffer.
+        NG_HIP_CHECK(hipStreamSynchronize(s));
+        NG_HIP_CHECK(hipFree(*p));
+        *p = nullptr;
+        *have = 0;
     }
-    if (need_ws) NG_HIP_CHECK(hipMalloc(&sb.ws, kLtWorkspace));
-    if (need_deq) {
-        if (sb.deq != nullptr) {
-            // Earlier calls on this stream may still read the old copy.
-            NG_HIP_CHECK(hipStreamSynchronize(s));
-            NG_HIP_CHECK(hipFree(sb.deq));
-            sb.deq = nullptr;
-            sb.deq_bytes = 0;
-        }
-        NG_HIP_CHECK(hipMalloc(&sb.deq, deq_bytes));
-        sb.deq_bytes = deq_bytes;
-    }
-    *out = &sb;
+    NG_HIP_CHECK(hipMalloc(p, need));
+    *have = need;
+    if (zero) NG_HIP_CHECK(hipMemsetAsync(*p, 0, need, s));
     return 0;
 }
 
@@ -342,9 +432,11 @@ int gemm_lt(void* c, const void* a, const void* b, const void* q, const void* sc
     std::lock_guard<std::mutex> lock(g_mu);
     const Plan* p = nullptr;
     if (get_plan(dev, M, K, N, ta, tb, &p) != 0) return -1;
-    StreamBuffers* sb = nullptr;
-    const size_t deq_bytes = q != nullptr ? static_cast<size_t>(K) * static_cast<size_t>(N) * 2 : 0;
-    if (stream_buffers(dev, s, deq_bytes, &sb) != 0) return -1;
+    StreamBuffers* sb = &g_buffers[{dev, s}];
+    if (grow(s, &sb->ws, &sb->ws_bytes, p->ws, false) != 0) return -1;
+    if (q != nullptr &&
+        grow(s, &sb->deq, &sb->deq_bytes, static_cast<size_t>(K) * static_cast<size_t>(N) * 2, false) != 0)
+        return -1;
     if (q != nullptr) {
         const int r = tb ? cuda_dequantize_weights(sb->deq, q, scale, N, K, 1)
                          : cuda_dequantize_weights(sb->deq, q, scale, K, N, 0);
@@ -355,6 +447,65 @@ int gemm_lt(void* c, const void* a, const void* b, const void* q, const void* sc
     NG_LT_CHECK(hipblasLtMatmul(g_handles[dev], p->desc, &alpha, b, p->lw, a, p->lx, &beta, c, p->ly, c, p->ly,
                                 &p->algo, sb->ws, p->ws, s));
     return 0;
+}
+
+template <int MT, int U>
+int launch_split(uint16_t* c, const uint16_t* a, const int8_t* b, const float* scale, int M, int N, int K) {
+    const int tiles = (N + 16 * kSplitWaves - 1) / (16 * kSplitWaves);
+    const int nchunks = K / kChunk;
+    // Enough slices of K for about 256 blocks (512 for K >= 8192), at most 8,
+    // each of at least two chunks, none empty.
+    const int target = K >= 8192 ? 512 : 256;
+    int S = (target + tiles - 1) / tiles;
+    S = max(1, min(S, min(8, nchunks / 2)));
+    const int cps = (nchunks + S - 1) / S;
+    S = (nchunks + cps - 1) / cps;
+    float* part = nullptr;
+    if (S > 1) {
+        int dev = 0;
+        NG_HIP_CHECK(hipGetDevice(&dev));
+        const hipStream_t s = stream();
+        std::lock_guard<std::mutex> lock(g_mu);
+        StreamBuffers* sb = &g_buffers[{dev, s}];
+        if (grow(s, &sb->part, &sb->part_bytes, static_cast<size_t>(S) * M * N * sizeof(float), false) != 0)
+            return -1;
+        part = static_cast<float*>(sb->part);
+    }
+    gemm_i8w_split_kernel<MT, U><<<dim3(static_cast<unsigned>(tiles * S)), dim3(kSplitWaves * kWave), 0, stream()>>>(
+        c, a, b, scale, part, M, N, K, S, tiles, cps);
+    NG_CHECK_LAUNCH("cuda_gemm_int8");
+    if (S > 1) {
+        const size_t mn = static_cast<size_t>(M) * N;
+        split_reduce_kernel<<<dim3(static_cast<unsigned>((mn + 255) / 256)), dim3(256), 0, stream()>>>(
+            c, part, scale, M, N, S);
+        NG_CHECK_LAUNCH("cuda_gemm_int8");
+    }
+    return 0;
+}
+
+// Kernel and tile shape by M, K and N, from sweeps on MI355X over K x N in
+// {4096 x 4096, 4096 x 1024, 4096 x 14336, 14336 x 4096} and M in {1, 4, 16,
+// 32, 64}: the split kernel from M = 17 on (and for 4 < M <= 16 with K or N of
+// 8192 or more), otherwise the kernel that reads A from L2 directly. There,
+// wide weights (N >= 8192) give every block two row tiles, which halves the
+// reads of A per weight byte.
+int gemm_i8w(void* c, const void* a, const void* b, const void* scale, int M, int K, int N) {
+    auto* cp = static_cast<uint16_t*>(c);
+    auto* ap = static_cast<const uint16_t*>(a);
+    auto* bp = static_cast<const int8_t*>(b);
+    auto* sp = static_cast<const float*>(scale);
+    const bool big = K >= 8192 || N >= 8192;
+    if (M > 64) return launch_split<8, kSplitU>(cp, ap, bp, sp, M, N, K);
+    if (M > 32) return launch_split<4, kSplitU>(cp, ap, bp, sp, M, N, K);
+    if (M > 16) return launch_split<2, kSplitU>(cp, ap, bp, sp, M, N, K);
+    if (M > 4 && big) return launch_split<1, kSplitU>(cp, ap, bp, sp, M, N, K);
+    if (N >= 8192 && M > 2) return launch_i8w<1, 2, 16, 4>(cp, ap, bp, sp, M, N, K);
+    return launch_i8w<1, 1, 8, 8>(cp, ap, bp, sp, M, N, K);
+}
+
+// The weight-streaming path takes transpose_b, M <= kMaxFusedM and K % 64 == 0.
+bool use_i8w(const void* a, const void* b, int M, int K, int N, bool transpose_b) {
+    return transpose_b && M <= kMaxFusedM && K % kChunk == 0 && aligned16(a) && aligned16(b);
 }
 
 }  // namespace

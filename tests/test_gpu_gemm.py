@@ -79,12 +79,15 @@ def assert_within_bound(got_bits, a, q, scale, tb: bool, what: str, ora) -> None
                           f"max |d|/bound {(d / bound).max():.3g}"
 
 
-# M, K, N: the weight-streaming path takes transpose_b, M <= 64 and K % 64 == 0
-# (and N >= 2048 when M > 32); N >= 8192 selects two row tiles per block.
+# M, K, N: the weight-streaming path takes transpose_b, M <= 128 and K % 64 == 0.
+# M > 16 (and 4 < M <= 16 with K or N >= 8192) runs the split-K kernel, with
+# 1 to 8 slices of K; M <= 4 with N >= 8192 gives each block two row tiles.
 FUSED = [
     (1, 4096, 4096), (3, 4096, 1024), (16, 4096, 4096), (17, 4096, 1000), (32, 1024, 512), (33, 4096, 4096),
-    (64, 4096, 4096), (64, 4096, 2048), (8, 14336, 4096), (64, 14336, 4096), (5, 64, 16), (2, 128, 7),
-    (64, 4096, 14336), (1, 4096, 14336), (5, 4096, 8192), (20, 1024, 8200), (40, 512, 8208), (2, 256, 9000),
+    (64, 4096, 4096), (64, 4096, 1024), (8, 14336, 4096), (64, 14336, 4096), (5, 64, 16), (2, 128, 7),
+    (64, 4096, 14336), (1, 4096, 14336), (3, 4096, 8192), (5, 4096, 8192), (20, 1024, 8200), (40, 512, 8208),
+    (2, 256, 9000), (48, 4096, 1024), (65, 4096, 1024), (96, 4096, 4096), (128, 14336, 4096), (100, 1024, 300),
+    (7, 8192, 64), (128, 64, 64),
 ]
 
 
@@ -101,7 +104,7 @@ def test_int8_weight_streaming_bit_exact(lib, M, K, N):
 
 
 @pytest.mark.parametrize("M,K,N", [(1, 4096, 4096), (64, 4096, 2048), (16, 14336, 512), (30, 2048, 300),
-                                   (12, 4096, 14336)])
+                                   (12, 4096, 14336), (128, 4096, 1024)])
 def test_int8_weight_streaming_random(lib, ora, M, K, N):
     banner(f"gemm_int8 streaming random M={M} K={K} N={N}")
     a = f16bits(RNG.standard_normal((M, K)))
@@ -111,11 +114,11 @@ def test_int8_weight_streaming_random(lib, ora, M, K, N):
     assert_within_bound(got, a, q, scale, True, "C", ora)
 
 
-# The dequantize + hipBLASLt path: B [K, N] with per-column scales, M > 64,
-# K not a multiple of 64, or 32 < M with N < 2048.
+# The dequantize + hipBLASLt path: B [K, N] with per-column scales, M > 128 or
+# K not a multiple of 64.
 LIBRARY = [
-    (4, 256, 128, False), (65, 4096, 1024, True), (256, 1024, 512, False), (7, 200, 96, True),
-    (512, 4096, 4096, True), (33, 1024, 4096, False), (48, 4096, 1024, True),
+    (4, 256, 128, False), (129, 4096, 1024, True), (256, 1024, 512, False), (7, 200, 96, True),
+    (512, 4096, 4096, True), (33, 1024, 4096, False),
 ]
 
 
@@ -132,7 +135,7 @@ def test_int8_dequant_library_bit_exact(lib, M, K, N, tb):
     assert_bits_equal(got, S.astype(np.float16).view(np.uint16), "C")
 
 
-@pytest.mark.parametrize("M,K,N,tb", [(65, 4096, 1024, True), (16, 1024, 512, False), (100, 960, 200, True)])
+@pytest.mark.parametrize("M,K,N,tb", [(129, 4096, 1024, True), (16, 1024, 512, False), (100, 960, 200, True)])
 def test_int8_dequant_library_random(lib, ora, M, K, N, tb):
     banner(f"gemm_int8 library random M={M} K={K} N={N} tb={tb}")
     a = f16bits(RNG.standard_normal((M, K)))
@@ -143,22 +146,23 @@ def test_int8_dequant_library_random(lib, ora, M, K, N, tb):
 
 
 def test_int8_paths_agree(lib, ora):
-    """The same product through both paths (M <= 64 streams, M = 65 goes
+    """The same product through both paths (M <= 128 streams, M = 129 goes
     through the library): rows shared by the two calls agree to the bound."""
     banner("gemm_int8 both paths")
     K, N = 4096, 2048
-    a = f16bits(RNG.standard_normal((65, K)))
+    a = f16bits(RNG.standard_normal((129, K)))
     q = codes((N, K))
     scale = RNG.uniform(1e-3, 1e-2, N).astype(np.float32)
-    big = gemm_int8(lib, a, q, scale, 65, K, N, True)
-    small = gemm_int8(lib, a[:64], q, scale, 64, K, N, True)
-    assert_within_bound(big[:64], a[:64], q, scale, True, "library", ora)
-    assert_within_bound(small, a[:64], q, scale, True, "streaming", ora)
+    big = gemm_int8(lib, a, q, scale, 129, K, N, True)
+    small = gemm_int8(lib, a[:128], q, scale, 128, K, N, True)
+    assert_within_bound(big[:128], a[:128], q, scale, True, "library", ora)
+    assert_within_bound(small, a[:128], q, scale, True, "streaming", ora)
 
 
-def test_int8_streaming_is_deterministic(lib):
-    banner("gemm_int8 streaming repeat")
-    M, K, N = 16, 4096, 4096
+@pytest.mark.parametrize("M", [16, 64])
+def test_int8_streaming_is_deterministic(lib, M):
+    banner(f"gemm_int8 streaming repeat M={M}")
+    K, N = 4096, 4096
     a = f16bits(RNG.standard_normal((M, K)))
     q = codes((N, K))
     scale = RNG.uniform(1e-3, 1e-2, N).astype(np.float32)
@@ -172,11 +176,25 @@ def test_int8_streaming_is_deterministic(lib):
     assert_bits_equal(outs[2], outs[0], "repeat 2")
 
 
+def test_int8_split_partials_grow(lib):
+    """The split kernel's per-stream partial-sum buffer grows from a small call
+    to a larger one and is reused by a smaller one after that."""
+    banner("gemm_int8 split partials growth")
+    for (M, K, N) in [(20, 1024, 128), (100, 14336, 4096), (33, 4096, 512)]:
+        a = exact_activations(M, K)
+        q = codes((N, K))
+        scale = RNG.uniform(1e-3, 1e-2, N).astype(np.float16).astype(np.float32)
+        got = gemm_int8(lib, a, q, scale, M, K, N, True)
+        S = f16val(a) @ q.astype(np.float64).T
+        want = (S.astype(np.float32) * scale[None, :]).astype(np.float16).view(np.uint16)
+        assert_bits_equal(got, want, f"C {M}x{K}x{N}")
+
+
 def test_int8_library_buffer_grows(lib):
     """The per-stream fp16 weight copy grows from a small call to a larger one
     and is reused by a smaller one after that."""
     banner("gemm_int8 library buffer growth")
-    for (M, K, N) in [(70, 128, 64), (70, 2048, 2048), (70, 256, 64)]:
+    for (M, K, N) in [(170, 128, 64), (170, 2048, 2048), (170, 256, 64)]:
         a = exact_activations(M, K)
         q = codes((K, N))
         scale = np.full(N, 2.0 ** -7, np.float32)
