@@ -85,6 +85,14 @@ int ng_bf16_qk_rmsnorm_rope_with_theta(void* q_out, const void* q_in, void* k_ou
 int ng_fp32_to_fp16(void* output, const void* input, size_t num_elements);
 int ng_fp16_to_fp32(void* output, const void* input, size_t num_elements);
 
+/* bf16 [n] -> fp16 [n] with the model loader's truncating rule
+ * (pkg/model/loader.go:23-85, ConvertBF16ToFP16, which runs on the host when a
+ * bf16 safetensors checkpoint is loaded for the fp16 engine): the same bits,
+ * produced on the device. Differs from cuda_bf16_to_fp16 (round to nearest
+ * even) only below 2^-14, where it truncates toward zero, and in the NaN
+ * payload (always 0x7E00 with the sign). */
+int ng_bf16_to_fp16_truncate(void* output, const void* input, size_t num_elements);
+
 /* int8 [rows, cols] -> fp16 [rows, cols], out = fp16(float(q) * scale) with
  * scales[rows] (scale_per_row != 0) or scales[cols]. The dequantisation stage
  * of cuda_gemm_int8, gpu/cuda/matmul.cu:169-187 (dequantize_and_copy), exported

@@ -78,6 +78,7 @@ SIGNATURES: dict[str, tuple] = {
     "ng_bf16_silu_mul": (_i, [_vp, _cvp, _cvp, _sz]),
     "ng_fp32_to_fp16": (_i, [_vp, _cvp, _sz]),
     "ng_fp16_to_fp32": (_i, [_vp, _cvp, _sz]),
+    "ng_bf16_to_fp16_truncate": (_i, [_vp, _cvp, _sz]),
     "cuda_dequantize_weights": (_i, [_vp, _cvp, _cvp, _i, _i, _i]),
     "ng_gather_embeddings_checked": (_i, [_vp, _cvp, _ip, _i, _i, _i, _ip]),
     "ng_rope_qk_with_theta": (_i, [_vp, _cvp, _vp, _cvp, _ip, _i, _i, _i, _i, _i, _i, _f]),

@@ -203,6 +203,45 @@ static int launch_cvt(const char* name, void* out, const void* in, size_t n) {
     return 0;
 }
 
+// bf16 -> fp16 as the model loader converts weights on the host
+// (pkg/model/loader.go:23-85): through fp32, then the fp16 mantissa is
+// truncated, fp16-subnormal results truncate toward zero, magnitudes from
+// 2^16 up become infinity, NaN becomes 0x7E00 with its sign, and values below
+// 2^-24 become a signed zero. bf16's 7 mantissa bits fit in fp16's 10, so in
+// fp16's normal range the value is exact; the rest is integer bit work.
+__device__ __forceinline__ uint32_t bf16_to_f16_trunc(uint32_t b) {
+    const uint32_t sign = (b & 0x8000u);
+    const int e8 = static_cast<int>((b >> 7) & 0xffu);
+    const uint32_t m7 = b & 0x7fu;
+    const int e16 = e8 - 112;  // fp16 biased exponent
+    uint32_t mag;
+    if (e8 == 0xff) mag = m7 == 0 ? 0x7c00u : 0x7e00u;
+    else if (e16 >= 31) mag = 0x7c00u;
+    else if (e16 >= 1) mag = (static_cast<uint32_t>(e16) << 10) | (m7 << 3);
+    else if (e16 >= -10) mag = ((m7 | 0x80u) << 16) >> (14 - e16);
+    else mag = 0u;
+    return sign | mag;
+}
+
+__global__ __launch_bounds__(kEwThreads) void bf16_to_f16_trunc_kernel(uint16_t* out, const uint16_t* in, size_t n,
+                                                                       int vec) {
+    const size_t stride = static_cast<size_t>(gridDim.x) * kEwThreads;
+    const size_t t0 = static_cast<size_t>(blockIdx.x) * kEwThreads + threadIdx.x;
+    size_t done = 0;
+    if (vec) {
+        const size_t nvec = n / 8;
+        for (size_t i = t0; i < nvec; i += stride) {
+            u32x4 v = ld16_stream(in + i * 8);
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+                v[j] = bf16_to_f16_trunc(v[j] & 0xffffu) | (bf16_to_f16_trunc(v[j] >> 16) << 16);
+            st16_stream(out + i * 8, v);
+        }
+        done = nvec * 8;
+    }
+    for (size_t i = done + t0; i < n; i += stride) out[i] = static_cast<uint16_t>(bf16_to_f16_trunc(in[i]));
+}
+
 }  // namespace ng
 
 using namespace ng;
@@ -251,4 +290,17 @@ extern "C" int ng_fp32_to_fp16(void* output, const void* input, size_t n) {
 }
 extern "C" int ng_fp16_to_fp32(void* output, const void* input, size_t n) {
     return launch_cvt<CVT_F16_TO_F32>("ng_fp16_to_fp32", output, input, n);
+}
+extern "C" int ng_bf16_to_fp16_truncate(void* output, const void* input, size_t n) {
+    NG_REQUIRE(output && input, "ng_bf16_to_fp16_truncate: null pointer");
+    NG_REQUIRE(n > 0, "ng_bf16_to_fp16_truncate: num_elements must be > 0");
+    const int vec = aligned16(output) && aligned16(input);
+    size_t blocks = (n / 8 + kEwThreads - 1) / kEwThreads;
+    if (blocks < 1) blocks = 1;
+    const size_t cap = static_cast<size_t>(device_cu_count()) * 16;
+    if (blocks > cap) blocks = cap;
+    bf16_to_f16_trunc_kernel<<<dim3(static_cast<unsigned>(blocks)), dim3(kEwThreads), 0, stream()>>>(
+        static_cast<uint16_t*>(output), static_cast<const uint16_t*>(input), n, vec);
+    NG_CHECK_LAUNCH("ng_bf16_to_fp16_truncate");
+    return 0;
 }

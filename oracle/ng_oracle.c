@@ -475,6 +475,38 @@ void ora_rope_f32(float* out, const float* in, const int* pos, int T, int nh, in
     free(inv);
 }
 
+/* bf16 -> fp16 the way the model loader converts a bf16 checkpoint on the host
+ * (pkg/model/loader.go:23-85): widen to fp32 by a 16-bit shift (:30-32), then
+ * float32ToFloat16Bits (:46-85): Inf -> 0x7C00, NaN -> 0x7E00 (sign kept),
+ * exponent >= 31 after rebias -> Inf, rebias <= 0 -> subnormal by shifting
+ * the mantissa with its hidden bit right (1 - exp16) and then 13 (zero below
+ * -10), otherwise the mantissa truncated to 10 bits. */
+static uint16_t loader_f32_to_f16(float f) {
+    uint32_t bits;
+    memcpy(&bits, &f, 4);
+    uint32_t sign = (bits >> 31) & 1u;
+    int exp = (int)((bits >> 23) & 0xffu) - 127;
+    uint32_t mant = bits & 0x7fffffu;
+    if (exp == 128) return (uint16_t)((sign << 15) | (mant == 0 ? 0x7c00u : 0x7e00u));
+    int exp16 = exp + 15;
+    if (exp16 <= 0) {
+        if (exp16 < -10) return (uint16_t)(sign << 15);
+        mant = (mant | 0x800000u) >> (unsigned)(1 - exp16);
+        return (uint16_t)((sign << 15) | (mant >> 13));
+    }
+    if (exp16 >= 31) return (uint16_t)((sign << 15) | 0x7c00u);
+    return (uint16_t)((sign << 15) | ((uint32_t)exp16 << 10) | (mant >> 13));
+}
+
+void ora_bf16_to_f16_trunc(uint16_t* out, const uint16_t* in, size_t n) {
+    for (size_t i = 0; i < n; ++i) {
+        uint32_t b = (uint32_t)in[i] << 16;
+        float f;
+        memcpy(&f, &b, 4);
+        out[i] = loader_f32_to_f16(f);
+    }
+}
+
 /* Row gather of any element size (bit copy). */
 void ora_gather_bytes(void* out, const void* table, const int* ids, int T, size_t row_bytes) {
 #pragma omp parallel for schedule(static)

@@ -50,6 +50,7 @@ _SIGS = {
     "ora_elementwise_f32": (None, [_f32p, _f32p, _f32p, _f, _sz, _i]),
     "ora_rope_f32": (None, [_f32p, _f32p, _i32p, _i, _i, _i, _i, _f]),
     "ora_gather_bytes": (None, [C.c_void_p, C.c_void_p, _i32p, _i, _sz]),
+    "ora_bf16_to_f16_trunc": (None, [_u16p, _u16p, _sz]),
 }
 
 OPS = {"add": 0, "mul": 1, "silu": 2, "silu_mul": 3, "scale": 4}
@@ -224,6 +225,15 @@ def dequant(q, scales, mode: str):
     out = np.empty(q.shape, np.uint16)
     lib().ora_dequant(_p(out, _u16p), _p(q, _i8p), _p(scales, _f32p), rows, cols,
                       {"row": 0, "col": 1, "tensor": 2}[mode])
+    return out
+
+
+def bf16_to_f16_trunc(h) -> np.ndarray:
+    """bf16 bits -> fp16 bits with the model loader's truncating rule
+    (pkg/model/loader.go:23-85)."""
+    h = _u16(h)
+    out = np.empty_like(h)
+    lib().ora_bf16_to_f16_trunc(_p(out, _u16p), _p(h, _u16p), h.size)
     return out
 
 

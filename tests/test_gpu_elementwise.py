@@ -121,6 +121,20 @@ def test_converters_exact(lib, ora, n):
                       "bf16->fp16")
 
 
+@pytest.mark.parametrize("off,extra", [(0, 0), (1, 7)])
+def test_bf16_to_fp16_truncate_every_pattern(lib, ora, off, extra):
+    """All 65 536 bf16 patterns (plus a ragged tail, from an unaligned start)
+    through the loader's truncating conversion, bit-exact with the oracle."""
+    banner(f"bf16->fp16 truncate off={off} extra={extra}")
+    x = np.concatenate([np.arange(65536, dtype=np.uint16), RNG.integers(0, 65536, extra).astype(np.uint16)])
+    n = x.size
+    xb = dev(np.concatenate([np.zeros(off, np.uint16), x]))
+    ob = empty(2 * (n + off))
+    ok(lib.ng_bf16_to_fp16_truncate(C.c_void_p(ob.ptr + 2 * off), C.c_void_p(xb.ptr + 2 * off), n))
+    got = get(ob, np.uint16, (n + off,))[off:]
+    assert_bits_equal(got, ora.bf16_to_f16_trunc(x), "bf16->fp16 truncate")
+
+
 def test_softmax_close(lib, ora):
     banner("softmax")
     x = bits(RNG.standard_normal((33, 1000)) * 4, "f16")

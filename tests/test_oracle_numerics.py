@@ -435,6 +435,33 @@ def test_dequant_reference_kat(ora):
     assert (np.abs(out - codes * np.float32(0.01)) > 1e-3).sum() < 10
 
 
+# --------------------------------------------------------------- loader bf16 -> fp16
+
+def test_bf16_to_f16_trunc_every_pattern(ora):
+    """loader.go:23-85 for all 65 536 bf16 inputs against an independent rule:
+    round toward zero to fp16 (numpy's nearest conversion, stepped one ulp
+    toward zero where it rounded away), except |x| >= 2^16 -> inf and
+    NaN -> 0x7E00 with the sign."""
+    h = np.arange(65536, dtype=np.uint16)
+    got = ora.bf16_to_f16_trunc(h)
+    x = ora.bf16_bits_to_f32(h)
+    with np.errstate(over="ignore"):
+        near = x.astype(np.float16)
+    nb = near.view(np.uint16).astype(np.int32)
+    away = np.abs(near.astype(np.float64)) > np.abs(x.astype(np.float64))
+    want = np.where(away, nb - 1, nb)
+    sign = (h & 0x8000).astype(np.int32)
+    want = np.where(np.abs(x) >= 65536.0, sign | 0x7C00, want)
+    want = np.where(np.isnan(x), sign | 0x7E00, want)
+    assert (got == want.astype(np.uint16)).all()
+
+
+def test_bf16_to_f16_trunc_reference_kat(ora):
+    """TestBF16ToFP16Conversion (tests/model/loader_test.go:443-470): 1.0 -> 0x3C00, 0.0 -> 0."""
+    assert ora.bf16_to_f16_trunc(np.array([0x3F80], np.uint16))[0] == 0x3C00
+    assert ora.bf16_to_f16_trunc(np.array([0x0000], np.uint16))[0] == 0x0000
+
+
 # --------------------------------------------------------------- int8-weight GEMM
 
 def _gemm_int8_loops(a_bits, q, scale, transpose_b):
