@@ -44,10 +44,7 @@ typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 
 constexpr int kChunk = 64;          // k per wave step
-#ifndef NG_I8W_MAX_M
-#define NG_I8W_MAX_M 128
-#endif
-constexpr int kMaxFusedM = NG_I8W_MAX_M;  // rows of A the weight-streaming path takes
+constexpr int kMaxFusedM = 128;     // rows of A the weight-streaming path takes
 
 // Two int8 codes (bytes SEL0 and SEL1 of one dword) -> two exact fp16 values.
 // The bytes are biased to u = q + 128, placed under an fp16 exponent of 2^10
@@ -201,7 +198,7 @@ int launch_i8w(uint16_t* c, const uint16_t* a, const int8_t* b, const float* sca
 // an agent-scope release and acquire per block, which on MI355X write back and
 // invalidate the whole L2: measured 3-5x slower.)
 constexpr int kSplitWaves = 4;
-constexpr int kSplitU = 4;
+constexpr int kSplitU = 2;  // chunks per batch (2 and 4 measured; 2 is 5% faster at M = 64)
 
 template <int MT, int U>
 __global__ __launch_bounds__(kSplitWaves * kWave) void gemm_i8w_split_kernel(
@@ -211,7 +208,7 @@ __global__ __launch_bounds__(kSplitWaves * kWave) void gemm_i8w_split_kernel(
     constexpr int kPieces = 16 * MT * U * 8;        // 16-byte pieces of A per batch
     constexpr int kThreads = kSplitWaves * kWave;
     static_assert(kPieces % kThreads == 0, "A pieces must divide among the threads");
-    __shared__ __align__(16) uint8_t lds_a[16 * MT * kRowBytes];
+    __shared__ __align__(16) uint8_t lds_a[2][16 * MT * kRowBytes];
 
     const int sl = blockIdx.x % S;
     const int tile = blockIdx.x / S;
@@ -231,28 +228,37 @@ __global__ __launch_bounds__(kSplitWaves * kWave) void gemm_i8w_split_kernel(
 #pragma unroll
     for (int i = 0; i < MT; ++i) acc[i] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
 
-    for (int cb = c0; cb < c1; cb += U) {
-        u32x4 bv[U];
+    // Batches of U chunks, two in flight: the loads of batch i + 1 (B into
+    // registers, A into registers on their way to LDS) are issued before batch
+    // i is multiplied; A alternates between two LDS buffers, so one barrier
+    // per batch separates a buffer's writes from its reads and from its reuse
+    // two batches later.
+    constexpr int kP = kPieces / kThreads;
+    // A first: staging it into LDS then waits only for A, not for B. Chunks
+    // past the slice (a batch past the last is loaded too, to keep every load
+    // unconditional) are clamped to its last chunk.
+    auto load = [&](u32x4 (&bv)[U], u32x4 (&ar)[kP], int cb) {
 #pragma unroll
-        for (int u = 0; u < U; ++u) bv[u] = ld16_stream(brow + static_cast<size_t>(min(cb + u, c1 - 1)) * kChunk);
-        u32x4 ar[kPieces / kThreads];
-#pragma unroll
-        for (int j = 0; j < kPieces / kThreads; ++j) {
+        for (int j = 0; j < kP; ++j) {
             const int pc = j * kThreads + tid;
             const int row = pc / (U * 8);
             const int q = pc % (U * 8);
             const int ch = min(cb + q / 8, c1 - 1);
             ar[j] = ld16(a + static_cast<size_t>(min(row, M - 1)) * K + ch * kChunk + 8 * (q % 8));
         }
-        __syncthreads();  // the previous batch has been read from LDS
 #pragma unroll
-        for (int j = 0; j < kPieces / kThreads; ++j) {
+        for (int u = 0; u < U; ++u) bv[u] = ld16_stream(brow + static_cast<size_t>(min(cb + u, c1 - 1)) * kChunk);
+    };
+    auto stage = [&](int buf, const u32x4 (&ar)[kP]) {
+#pragma unroll
+        for (int j = 0; j < kP; ++j) {
             const int pc = j * kThreads + tid;
             const int row = pc / (U * 8);
             const int q = pc % (U * 8);
-            *reinterpret_cast<u32x4*>(lds_a + row * kRowBytes + (q / 8) * (kChunk * 2) + 16 * (q % 8)) = ar[j];
+            *reinterpret_cast<u32x4*>(lds_a[buf] + row * kRowBytes + (q / 8) * (kChunk * 2) + 16 * (q % 8)) = ar[j];
         }
-        __syncthreads();
+    };
+    auto multiply = [&](int buf, u32x4 (&bv)[U], int cb) {
 #pragma unroll
         for (int u = 0; u < U; ++u) {
             if (cb + u >= c1) bv[u] = u32x4{0u, 0u, 0u, 0u};  // a clamped chunk multiplies zero codes
@@ -260,13 +266,32 @@ __global__ __launch_bounds__(kSplitWaves * kWave) void gemm_i8w_split_kernel(
             codes16_to_operands(bv[u], b0, b1);
 #pragma unroll
             for (int t = 0; t < MT; ++t) {
-                const uint8_t* ap = lds_a + (16 * t + col) * kRowBytes + u * (kChunk * 2) + 32 * grp;
+                const uint8_t* ap = lds_a[buf] + (16 * t + col) * kRowBytes + u * (kChunk * 2) + 32 * grp;
                 const u32x4 a0 = *reinterpret_cast<const u32x4*>(ap);
                 const u32x4 a1 = *reinterpret_cast<const u32x4*>(ap + 16);
                 acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, a0), b0, acc[t], 0, 0, 0);
                 acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, a1), b1, acc[t], 0, 0, 0);
             }
         }
+    };
+    // The batch count is rounded up to even: an extra batch past the slice
+    // multiplies zero codes. (Leaving the loop after an odd batch instead lets
+    // the compiler sink the next batch's loads below the multiply.)
+    const int nb = (c1 - c0 + U - 1) / U;
+    u32x4 bv0[U], bv1[U];
+    u32x4 ar0[kP], ar1[kP];
+    load(bv0, ar0, c0);
+    for (int i = 0; i < nb; i += 2) {
+        stage(0, ar0);
+        __syncthreads();
+        load(bv1, ar1, min(c0 + (i + 1) * U, c1 - 1));
+        __builtin_amdgcn_sched_barrier(0);
+        multiply(0, bv0, c0 + i * U);
+        stage(1, ar1);
+        __syncthreads();
+        load(bv0, ar0, min(c0 + (i + 2) * U, c1 - 1));
+        __builtin_amdgcn_sched_barrier(0);
+        multiply(1, bv1, c0 + (i + 1) * U);
     }
 
     if (S == 1) {
