@@ -25,11 +25,14 @@ Printed JSON line: value = layer algorithmic bytes / step time (GB/s);
 us_per_layer = sum of the six kernels' average durations; per-kernel GB/s
 and fraction of 8 TB/s; extra layer configurations (decode T=64, Llama-2-13B,
 Mistral-Nemo bf16) and kernels (gather per forward, fused RMSNorm+int8, int8
-dequant); the roofline of the dominant kernel (SwiGLU); and the CPU oracle
-timed on the host cores on a bounded token sample of the same layer.
+dequant, QK LayerNorm + RoPE, cuda_gemm_int8 at Mistral-7B's INT8 projections);
+the layer with this library's fused entry points; the roofline of the dominant
+kernel (SwiGLU); and the CPU oracle timed on the host cores on a bounded token
+sample of the same layer.
 
 Usage: python bench.py [--gpus 1] [--steps 50] [--warmup 5] [--no-cpu] [--no-extra]
        python bench.py --pmc-pass   (short run for rocprofv3 --pmc: copy probe + layer kernels)
+       python bench.py --gemm-only  (cuda_gemm_int8 timings only)
 """
 from __future__ import annotations
 
@@ -608,6 +611,8 @@ def main():
     ap.add_argument("--no-extra", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--pmc-pass", action="store_true")
+    ap.add_argument("--gemm-only", action="store_true",
+                    help="time only cuda_gemm_int8 at Mistral-7B's INT8 projections and print that JSON")
     args = ap.parse_args()
     if args.gpus != 1:
         print(json.dumps({"error": "this build runs on one GPU: every kernel shards over tokens with no exchange, "
@@ -622,6 +627,9 @@ def main():
     L.ng_set_stream(stream)
     if args.pmc_pass:
         pmc_pass(L, hip, stream)
+        return
+    if args.gemm_only:
+        print(json.dumps({"gemm_int8": gemm_extras(L, hip, stream)}), flush=True)
         return
 
     cfg = W.CONFIGS[args.config]
@@ -642,6 +650,17 @@ def main():
                 "us_per_layer": us_layer - per["rope_q"] - per["rope_k"] + per["rope_qk"],
                 "note": "Q and K rotated in one launch; the engine's own sequence (the headline) calls "
                         "cuda_rope_with_theta twice"}
+    # Steady state with this library's fused entry points: the residual add
+    # that ends layer L and the RMSNorm that starts layer L+1 are one
+    # cuda_add_rmsnorm, and Q and K rotate in one launch. Needs call-site
+    # changes in the engine, so it is reported beside the headline.
+    fl_bytes = 2 * lb["add_rmsnorm"] + qk_bytes + lb["silu_mul"]
+    fl_us = 2 * per["add_rmsnorm"] + per["rope_qk"] + per["silu_mul"]
+    fused_layer = {"kernels": ["add_rmsnorm (residual add of the previous layer + RMSNorm)", "rope_qk",
+                               "add_rmsnorm", "silu_mul"],
+                   "us_per_layer": fl_us, "layer_bytes": fl_bytes, "GBps": fl_bytes / fl_us / 1e3,
+                   "frac": fl_bytes / fl_us / 1e3 / PEAK_GBPS,
+                   "note": "sum of the per-kernel averages above; the engine's six-kernel sequence is the headline"}
 
     extra = {}
     if not args.no_extra:
@@ -658,7 +677,7 @@ def main():
         extra.update(extra_kernels(L, hip, stream))
 
     dom = "silu_mul"
-    roof = {"kernel": "cuda_silu_mul (ng::ew_vec_kernel<_Float16, EW_SILU_MUL, 4>)", "bound": "hbm",
+    roof = {"kernel": "cuda_silu_mul (ng::ew_vec_kernel<_Float16, EW_SILU_MUL, 1>)", "bound": "hbm",
             "achieved": kernels[dom]["GBps"], "peak": PEAK_GBPS, "unit": "GB/s",
             "frac": kernels[dom]["GBps"] / PEAK_GBPS, "traffic": load_traffic(),
             "algorithmic_bytes_per_launch": lb[dom], "avg_launch_us": kernels[dom]["us"]}
@@ -687,6 +706,7 @@ def main():
                    "rope_theta": cfg.theta, "eps": cfg.eps, "rotating_sets": nsets},
         "us_per_layer": us_layer,
         "fused_qk_variant": fused_qk,
+        "fused_layer_variant": fused_layer,
         "pct_of_peak": layer_bytes / us_layer / 1e3 / PEAK_GBPS * 100,
         "host_wall_ms_per_step": wall_ms,
         "layer_bytes": layer_bytes,
