@@ -534,6 +534,26 @@ bool use_i8w(const void* a, const void* b, int M, int K, int N, bool transpose_b
 }
 
 }  // namespace
+
+void gemm_release() {
+    std::lock_guard<std::mutex> lock(g_mu);
+    for (auto& kv : g_plans) {
+        Plan& p = kv.second;
+        hipblasLtMatrixLayoutDestroy(p.lw);
+        hipblasLtMatrixLayoutDestroy(p.lx);
+        hipblasLtMatrixLayoutDestroy(p.ly);
+        hipblasLtMatmulDescDestroy(p.desc);
+    }
+    g_plans.clear();
+    for (auto& kv : g_buffers) {
+        for (void* b : {kv.second.ws, kv.second.deq, kv.second.part})
+            if (b != nullptr) (void)hipFree(b);
+    }
+    g_buffers.clear();
+    for (auto& kv : g_handles) hipblasLtDestroy(kv.second);
+    g_handles.clear();
+}
+
 }  // namespace ng
 
 using namespace ng;

@@ -64,6 +64,11 @@ inline hipStream_t stream() { return ng_get_stream(); }
 // Number of compute units of the current device (cached per device id).
 int device_cu_count();
 
+// Frees every buffer, plan and library handle held by the GEMM entry points
+// (matmul.hip), on every device. cuda_shutdown calls it before it resets the
+// device, which would otherwise leave them pointing at released memory.
+__attribute__((visibility("hidden"))) void gemm_release();
+
 // RMSNorm of `rows` rows of H 16-bit elements through the row kernels
 // (norm.hip); launches on stream(), returns 0 or -1.
 template <typename T>

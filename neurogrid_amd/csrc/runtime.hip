@@ -104,6 +104,7 @@ extern "C" void cuda_shutdown(void) {
     if (g_initialized) {
         (void)hipDeviceSynchronize();
         (void)hipGetLastError();
+        gemm_release();
         (void)hipDeviceReset();
         g_initialized = false;
     }

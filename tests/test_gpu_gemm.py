@@ -17,6 +17,10 @@ Bars:
 from __future__ import annotations
 
 import math
+import subprocess
+import sys
+import textwrap
+from pathlib import Path
 
 import numpy as np
 import pytest
@@ -201,6 +205,43 @@ def test_int8_library_buffer_grows(lib):
         got = gemm_int8(lib, a, q, scale, M, K, N, False)
         S = f16val(a) @ (q.astype(np.float64) * 2.0 ** -7)
         assert_bits_equal(got, S.astype(np.float16).view(np.uint16), f"C {M}x{K}x{N}")
+
+
+def test_int8_across_shutdown_and_init():
+    """cuda_shutdown resets the device. The GEMM buffers, plans and hipBLASLt
+    handle made before it are released first, and calls after cuda_init build
+    new ones. Runs in a child process: the reset releases every device
+    allocation of the process, including other tests' buffers."""
+    banner("gemm_int8 across cuda_shutdown / cuda_init (child process)")
+    root = str(Path(__file__).resolve().parent.parent)
+    script = textwrap.dedent(f"""
+        import sys
+        sys.path.insert(0, {root!r})
+        import numpy as np
+        from neurogrid_amd import _lib
+        from neurogrid_amd.device import DeviceBuffer as DB
+        L = _lib.load()
+        rng = np.random.Generator(np.random.PCG64(3))
+        for rnd in range(2):
+            assert L.cuda_init(0) == 0
+            # streaming (tb, small M), split-K (M = 40) and dequant + hipBLASLt (M = 200)
+            for M, K, N, tb in [(1, 256, 64, True), (40, 512, 128, True), (200, 128, 64, False)]:
+                a = (rng.integers(-64, 65, (M, K)) / 64.0).astype(np.float16)
+                q = rng.integers(-128, 128, (N, K) if tb else (K, N)).astype(np.int8)
+                s = np.full(N, 2.0 ** -7, np.float32)
+                ab, qb, sb, cb = DB.from_array(a.view(np.uint16)), DB.from_array(q), DB.from_array(s), DB(2 * M * N)
+                assert L.cuda_gemm_int8(cb.vp, ab.vp, qb.vp, sb.vp, M, K, N, tb) == 0
+                got = cb.download(np.uint16, (M, N))
+                w = q.astype(np.float64) * 2.0 ** -7
+                want = (a.astype(np.float64) @ (w.T if tb else w)).astype(np.float16).view(np.uint16)
+                assert (got == want).all(), (rnd, M, K, N, tb)
+                for b in (ab, qb, sb, cb):
+                    b.free()
+            L.cuda_shutdown()
+        print("ok", flush=True)
+    """)
+    r = subprocess.run([sys.executable, "-c", script], capture_output=True, text=True, timeout=120)
+    assert r.returncode == 0 and "ok" in r.stdout, r.stdout + r.stderr
 
 
 @pytest.mark.parametrize("ta", [False, True])
