@@ -12,8 +12,8 @@ Reference wrappers restated here (gpu/bindings/gpu.go):
   GetDeviceInfo :106, SyncDevice :121, GetMemoryUsed :130,
   AllocateTensor :140, FreeTensor :162, CopyToDevice :171, CopyToHost :192,
   CopyToDeviceINT8 :213, CopyToHostINT8 :236, RMSNorm :256, SiLU :282,
-  Add :299, RoPE :317, QuantizePerTensor :427, DequantizePerTensor :445,
-  QuantizeWeights :463, GatherEmbeddings :1277.
+  Add :299, RoPE :317, GEMMFP16 :357, GEMMINT8 :395, QuantizePerTensor :427,
+  DequantizePerTensor :445, QuantizeWeights :463, GatherEmbeddings :1277.
 Tensor and Dtype restate pkg/types/tensor.go:11-104.
 """
 from __future__ import annotations
@@ -275,6 +275,28 @@ def RoPE(output: Tensor, input: Tensor, positions, head_dim: int) -> None:
         lib.cuda_sync_device()
     finally:
         lib.cuda_free(dpos)
+
+
+def GEMMFP16(c: Tensor, a: Tensor, b: Tensor, transposeA: bool, transposeB: bool) -> None:
+    """gpu.go:357-391: M, K from a's shape (swapped when transposeA), N from b's."""
+    if c is None or a is None or b is None:
+        raise GPUError("nil tensor")
+    M, K = (a.shape[1], a.shape[0]) if transposeA else (a.shape[0], a.shape[1])
+    N = b.shape[0] if transposeB else b.shape[1]
+    r = _lib().cuda_gemm_fp16(_ptr(c), _ptr(a), _ptr(b), M, K, N, bool(transposeA), bool(transposeB))
+    if r != 0:
+        raise GPUError(f"GEMM FP16 failed: {r}")
+
+
+def GEMMINT8(c: Tensor, a: Tensor, b: Tensor, scale: Tensor, transposeB: bool) -> None:
+    """gpu.go:395-424: M, K from a; N = b.shape[0] when transposeB (B [N, K]), else b.shape[1]."""
+    if c is None or a is None or b is None or scale is None:
+        raise GPUError("nil tensor")
+    M, K = a.shape[0], a.shape[1]
+    N = b.shape[0] if transposeB else b.shape[1]
+    r = _lib().cuda_gemm_int8(_ptr(c), _ptr(a), _ptr(b), _ptr(scale), M, K, N, bool(transposeB))
+    if r != 0:
+        raise GPUError(f"GEMM INT8 failed: {r}")
 
 
 def QuantizePerTensor(output: Tensor, scale: Tensor, input: Tensor) -> None:

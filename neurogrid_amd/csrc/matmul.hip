@@ -485,24 +485,28 @@ int launch_split(uint16_t* c, const uint16_t* a, const int8_t* b, const float* s
     S = max(1, min(S, min(8, nchunks / 2)));
     const int cps = (nchunks + S - 1) / S;
     S = (nchunks + cps - 1) / cps;
+    // With S > 1 the partial-sum buffer is this stream's: the lock is held
+    // until both kernels are enqueued, so calls from other host threads on the
+    // same stream cannot slip a launch between them.
+    const hipStream_t s = stream();
     float* part = nullptr;
+    std::unique_lock<std::mutex> lock(g_mu, std::defer_lock);
     if (S > 1) {
         int dev = 0;
         NG_HIP_CHECK(hipGetDevice(&dev));
-        const hipStream_t s = stream();
-        std::lock_guard<std::mutex> lock(g_mu);
+        lock.lock();
         StreamBuffers* sb = &g_buffers[{dev, s}];
         if (grow(s, &sb->part, &sb->part_bytes, static_cast<size_t>(S) * M * N * sizeof(float), false) != 0)
             return -1;
         part = static_cast<float*>(sb->part);
     }
-    gemm_i8w_split_kernel<MT, U><<<dim3(static_cast<unsigned>(tiles * S)), dim3(kSplitWaves * kWave), 0, stream()>>>(
+    gemm_i8w_split_kernel<MT, U><<<dim3(static_cast<unsigned>(tiles * S)), dim3(kSplitWaves * kWave), 0, s>>>(
         c, a, b, scale, part, M, N, K, S, tiles, cps);
     NG_CHECK_LAUNCH("cuda_gemm_int8");
     if (S > 1) {
         const size_t mn = static_cast<size_t>(M) * N;
-        split_reduce_kernel<<<dim3(static_cast<unsigned>((mn + 255) / 256)), dim3(256), 0, stream()>>>(
-            c, part, scale, M, N, S);
+        split_reduce_kernel<<<dim3(static_cast<unsigned>((mn + 255) / 256)), dim3(256), 0, s>>>(c, part, scale, M, N,
+                                                                                                 S);
         NG_CHECK_LAUNCH("cuda_gemm_int8");
     }
     return 0;

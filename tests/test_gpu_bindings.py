@@ -3,14 +3,17 @@ bindings (neurogrid_amd.bindings, restating gpu/bindings/gpu.go) so that they
 drive the gfx950 library through the same wrapper calls and shape rules.
 
 Sources: tests/kernels_test.go:19-274, tests/quantize_test.go:20-280,
-tests/e2e/real_inference_test.go:218-279 (embedding lookup), and the device
-plumbing they use. The Go suites draw from Go's math/rand seed 42, which
+tests/matmul_test.go:96-179 (GEMMINT8), tests/cgo_test.go:244-313 (call
+overhead, concurrent calls), tests/e2e/real_inference_test.go:218-279
+(embedding lookup), and the device plumbing they use. The Go suites draw from Go's math/rand seed 42, which
 cannot be reproduced here; any seeded stream is equivalent for these
 tolerance checks, so numpy PCG64 seed 42 is used.
 """
 from __future__ import annotations
 
 import math
+import threading
+import time
 
 import numpy as np
 import pytest
@@ -190,3 +193,118 @@ def test_errors_surface_as_go_errors(gpu):
         B.RoPE(t, t, [0], 128)
     with pytest.raises(B.GPUError, match="tensor dimension 0 must be positive"):
         B.AllocateTensor(B.NewTensor([0], B.Dtype.FP16))
+
+
+def test_gemm_int8_wrapper(gpu):
+    """TestGEMMINT8 (matmul_test.go:96-179) through the GEMMINT8 wrapper, in
+    both layouts: A [32,128] U(-1,1), codes U{-128..127}, scales 0.01, max |d|
+    < 5e-2 against the fp32 CPU matmul."""
+    banner("bindings GEMMINT8")
+    rng = np.random.Generator(np.random.PCG64(42))
+    M, K, N = 32, 128, 64
+    data_a = (rng.random(M * K, dtype=np.float32) * 2 - 1).reshape(M, K)
+    for transpose_b in (False, True):
+        codes = rng.integers(-128, 128, (N, K) if transpose_b else (K, N)).astype(np.int8)
+        scale = np.full(N, 0.01, np.float32)
+        a, c = alloc([M, K], B.Dtype.FP16), alloc([M, N], B.Dtype.FP16)
+        b = alloc(list(codes.shape), B.Dtype.INT8)
+        sc = alloc([N], B.Dtype.FP32)
+        B.CopyToDevice(a, data_a)
+        B.CopyToDeviceINT8(b, codes)
+        B.CopyToDevice(sc, scale)
+        B.GEMMINT8(c, a, b, sc, transpose_b)
+        out = np.empty(M * N, np.float32)
+        B.CopyToHost(out, c)
+        w = codes.astype(np.float32) * (scale[:, None] if transpose_b else scale[None, :])
+        ref = data_a @ (w.T if transpose_b else w)
+        assert np.abs(out.reshape(M, N) - ref).max() < 5e-2
+        for t in (a, b, c, sc):
+            B.FreeTensor(t)
+
+
+def test_call_overhead(gpu):
+    """TestCGOOverheadValidation (cgo_test.go:244-271): SyncDevice on an idle
+    device, 10 000 calls through the C ABI, under 10 us per call (here the
+    call crosses ctypes instead of cgo)."""
+    banner("bindings call overhead")
+    for _ in range(100):
+        B.SyncDevice()
+    n = 10000
+    t0 = time.perf_counter()
+    for _ in range(n):
+        B.SyncDevice()
+    us = (time.perf_counter() - t0) / n * 1e6
+    print(f"SyncDevice: {us:.2f} us per call")
+    assert us < 10.0
+
+
+def test_concurrent_calls(gpu):
+    """TestCGOConcurrentCalls (cgo_test.go:274-313): 10 threads x 100 rounds of
+    allocate / copy in / copy out / free of a [256] fp16 tensor."""
+    banner("bindings concurrent calls")
+    errors = []
+
+    def worker(seed):
+        try:
+            data = np.random.Generator(np.random.PCG64(seed)).standard_normal(256).astype(np.float32)
+            want = data.astype(np.float16).astype(np.float32)
+            for _ in range(100):
+                t = alloc([256], B.Dtype.FP16)
+                B.CopyToDevice(t, data)
+                back = np.empty(256, np.float32)
+                B.CopyToHost(back, t)
+                B.FreeTensor(t)
+                if not (back == want).all():
+                    raise AssertionError("round trip differs")
+        except Exception as e:  # reported by the main thread
+            errors.append(repr(e))
+
+    threads = [threading.Thread(target=worker, args=(i,)) for i in range(10)]
+    for t in threads:
+        t.start()
+    for t in threads:
+        t.join(timeout=120)
+    assert not any(t.is_alive() for t in threads)
+    assert not errors, errors[:3]
+
+
+def test_concurrent_gemm_int8(gpu):
+    """Several host threads call cuda_gemm_int8 on the one launch stream at
+    once, through the split-K path (M = 40, two kernels per call sharing the
+    stream's partial-sum buffer) and the library path (M = 200, the stream's
+    fp16 weight copy); every result is exact."""
+    banner("bindings concurrent GEMMINT8")
+    K, N = 512, 256
+    errors = []
+
+    def worker(seed):
+        try:
+            rng = np.random.Generator(np.random.PCG64(100 + seed))
+            for M in (40, 200, 40, 200):
+                data_a = (rng.integers(-64, 65, (M, K)) / 64.0).astype(np.float32)
+                codes = rng.integers(-128, 128, (N, K)).astype(np.int8)
+                scale = np.full(N, 2.0 ** -7, np.float32)
+                a, c = alloc([M, K], B.Dtype.FP16), alloc([M, N], B.Dtype.FP16)
+                b, sc = alloc([N, K], B.Dtype.INT8), alloc([N], B.Dtype.FP32)
+                B.CopyToDevice(a, data_a)
+                B.CopyToDeviceINT8(b, codes)
+                B.CopyToDevice(sc, scale)
+                for _ in range(5):
+                    B.GEMMINT8(c, a, b, sc, True)
+                out = np.empty(M * N, np.float32)
+                B.CopyToHost(out, c)
+                ref = (data_a.astype(np.float64) @ (codes.astype(np.float64).T * 2.0 ** -7)).astype(np.float16)
+                if not (out.reshape(M, N) == ref.astype(np.float32)).all():
+                    raise AssertionError(f"M={M}: results differ")
+                for t in (a, b, c, sc):
+                    B.FreeTensor(t)
+        except Exception as e:  # reported by the main thread
+            errors.append(repr(e))
+
+    threads = [threading.Thread(target=worker, args=(i,)) for i in range(6)]
+    for t in threads:
+        t.start()
+    for t in threads:
+        t.join(timeout=120)
+    assert not any(t.is_alive() for t in threads)
+    assert not errors, errors[:3]
