@@ -57,6 +57,10 @@ __device__ __forceinline__ uint32_t codes_to_f16x2(uint32_t w) {
     return __builtin_bit_cast(uint32_t, v);
 }
 
+// A dword as two fp16 values. Takes the dword by value: __builtin_bit_cast
+// applied directly to an ext_vector element (v[i]) reads element 0.
+__device__ __forceinline__ f16x2 as_f16x2(uint32_t v) { return __builtin_bit_cast(f16x2, v); }
+
 // 16 codes of one row of B -> the B operands of two MFMAs (codes 0-7, 8-15).
 __device__ __forceinline__ void codes16_to_operands(const u32x4 v, f16x8& b0, f16x8& b1) {
     const u32x4 x = {codes_to_f16x2<0x04010400u>(v[0]), codes_to_f16x2<0x04030402u>(v[0]),
@@ -182,6 +186,110 @@ int launch_i8w(uint16_t* c, const uint16_t* a, const int8_t* b, const float* sca
     const unsigned blocks = static_cast<unsigned>((N + 16 * NT - 1) / (16 * NT));
     gemm_i8w_kernel<MT, NT, WAVES, U>
         <<<dim3(blocks), dim3(WAVES * kWave), 0, stream()>>>(c, a, b, scale, M, N, K);
+    NG_CHECK_LAUNCH("cuda_gemm_int8");
+    return 0;
+}
+
+// ---- GEMV-shaped variant (M <= 4) -------------------------------------------
+// With one to four rows of A the MFMA layout costs a 16-byte load of A per
+// 16 codes in every lane and reads 64 bytes per row of B per instruction.
+// Here lane l of a wave takes codes [16l, 16l + 16) of a 1024-code segment, so
+// each load instruction reads 1 KiB contiguous of one row of B; the lane's A
+// values for that segment are loaded once and reused for R rows. Products are
+// summed with v_dot2_f32_f16 (pairs of fp16 products, fp32 sums); the block's
+// waves take different segments, and the 256 partial sums of each output are
+// added through LDS in a fixed order.
+constexpr int kGvWaves = 4;
+constexpr int kGvSeg = 1024;  // codes per wave step: 64 lanes x 16
+
+template <int MR, int R>
+__global__ __launch_bounds__(kGvWaves * kWave) void gemv_i8w_kernel(uint16_t* __restrict__ c,
+                                                                    const uint16_t* __restrict__ a,
+                                                                    const int8_t* __restrict__ b,
+                                                                    const float* __restrict__ scale, int M, int N,
+                                                                    int K) {
+    constexpr int V = R * MR;                 // outputs per block
+    constexpr int kParts = kGvWaves * kWave / V;  // threads that share one output in the first reduction stage
+    static_assert(kGvWaves * kWave % V == 0 && kWave % kParts == 0, "reduction shape");
+    __shared__ float red[kGvWaves * V * kWave];
+    const int tid = threadIdx.x;
+    const int lane = tid & (kWave - 1);
+    const int wave = __builtin_amdgcn_readfirstlane(tid / kWave);
+    const int n0 = blockIdx.x * R;
+    const int nseg = (K + kGvSeg - 1) / kGvSeg;
+
+    float acc[R][MR];
+#pragma unroll
+    for (int r = 0; r < R; ++r)
+#pragma unroll
+        for (int m = 0; m < MR; ++m) acc[r][m] = 0.0f;
+
+    for (int sg = wave; sg < nseg; sg += kGvWaves) {
+        const int k = sg * kGvSeg + 16 * lane;
+        const bool kin = k < K;           // the last segment may end early (K % 16 == 0)
+        const int kc = kin ? k : K - 16;  // lanes past K load the last codes and multiply zeros
+        u32x4 av[MR][2];
+#pragma unroll
+        for (int m = 0; m < MR; ++m) {
+            const uint16_t* ar = a + static_cast<size_t>(min(m, M - 1)) * K + kc;
+            av[m][0] = ld16(ar);
+            av[m][1] = ld16(ar + 8);
+        }
+        u32x4 bv[R];
+#pragma unroll
+        for (int r = 0; r < R; ++r) bv[r] = ld16_stream(b + static_cast<size_t>(min(n0 + r, N - 1)) * K + kc);
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            const u32x4 q = kin ? bv[r] : u32x4{0u, 0u, 0u, 0u};
+            f16x8 w0, w1;
+            codes16_to_operands(q, w0, w1);
+            const u32x4 wl = __builtin_bit_cast(u32x4, w0), wh = __builtin_bit_cast(u32x4, w1);
+#pragma unroll
+            for (int m = 0; m < MR; ++m) {
+                float s = acc[r][m];
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    s = __builtin_amdgcn_fdot2(as_f16x2(av[m][0][j]), as_f16x2(wl[j]), s, false);
+                    s = __builtin_amdgcn_fdot2(as_f16x2(av[m][1][j]), as_f16x2(wh[j]), s, false);
+                }
+                acc[r][m] = s;
+            }
+        }
+    }
+
+    // Output o = r * MR + m sums red[(w * V + o) * 64 + l] over waves w and
+    // lanes l: kParts threads add 256 / kParts values each, then one thread adds
+    // the parts, both in a fixed order.
+#pragma unroll
+    for (int r = 0; r < R; ++r)
+#pragma unroll
+        for (int m = 0; m < MR; ++m) red[(wave * V + r * MR + m) * kWave + lane] = acc[r][m];
+    __syncthreads();
+    const int o = tid % V;
+    const int part = tid / V;
+    constexpr int kPerPart = kGvWaves * kWave / kParts;  // values summed by one thread
+    float sum = 0.0f;
+#pragma unroll 4
+    for (int j = 0; j < kPerPart; ++j) {
+        const int idx = part * kPerPart + j;  // (wave, lane) pair
+        sum += red[((idx / kWave) * V + o) * kWave + idx % kWave];
+    }
+    __syncthreads();
+    red[o * kParts + part] = sum;
+    __syncthreads();
+    if (tid < V) {
+        float v = 0.0f;
+        for (int q = 0; q < kParts; ++q) v += red[tid * kParts + q];
+        const int r = tid / MR, m = tid % MR, n = n0 + r;
+        if (m < M && n < N) c[static_cast<size_t>(m) * N + n] = from_f32<f16>(v * scale[n]);
+    }
+}
+
+template <int MR, int R>
+int launch_gemv(uint16_t* c, const uint16_t* a, const int8_t* b, const float* scale, int M, int N, int K) {
+    const unsigned blocks = static_cast<unsigned>((N + R - 1) / R);
+    gemv_i8w_kernel<MR, R><<<dim3(blocks), dim3(kGvWaves * kWave), 0, stream()>>>(c, a, b, scale, M, N, K);
     NG_CHECK_LAUNCH("cuda_gemm_int8");
     return 0;
 }
@@ -513,28 +621,34 @@ int launch_split(uint16_t* c, const uint16_t* a, const int8_t* b, const float* s
 }
 
 // Kernel and tile shape by M, K and N, from sweeps on MI355X over K x N in
-// {4096 x 4096, 4096 x 1024, 4096 x 14336, 14336 x 4096} and M in {1, 4, 16,
-// 32, 64}: the split kernel from M = 17 on (and for 4 < M <= 16 with K or N of
-// 8192 or more), otherwise the kernel that reads A from L2 directly. There,
-// wide weights (N >= 8192) give every block two row tiles, which halves the
-// reads of A per weight byte.
+// {4096 x 4096, 4096 x 1024, 4096 x 14336, 14336 x 4096} and M from 1 to 128:
+// the GEMV kernel up to M = 4 (8 rows of B per block for M <= 2, 4 for M = 3,
+// 4: 23-33% faster than the MFMA kernels at M = 1), the split kernel from
+// M = 17 on (and for 4 < M <= 16 with K or N of 8192 or more), otherwise the
+// MFMA kernel that reads A from L2 directly.
 int gemm_i8w(void* c, const void* a, const void* b, const void* scale, int M, int K, int N) {
     auto* cp = static_cast<uint16_t*>(c);
     auto* ap = static_cast<const uint16_t*>(a);
     auto* bp = static_cast<const int8_t*>(b);
     auto* sp = static_cast<const float*>(scale);
     const bool big = K >= 8192 || N >= 8192;
+    if (M <= 4 && K % 16 == 0) {
+        if (M == 1) return launch_gemv<1, 8>(cp, ap, bp, sp, M, N, K);
+        if (M == 2) return launch_gemv<2, 8>(cp, ap, bp, sp, M, N, K);
+        return launch_gemv<4, 4>(cp, ap, bp, sp, M, N, K);
+    }
     if (M > 64) return launch_split<8, kSplitU>(cp, ap, bp, sp, M, N, K);
     if (M > 32) return launch_split<4, kSplitU>(cp, ap, bp, sp, M, N, K);
     if (M > 16) return launch_split<2, kSplitU>(cp, ap, bp, sp, M, N, K);
-    if (M > 4 && big) return launch_split<1, kSplitU>(cp, ap, bp, sp, M, N, K);
-    if (N >= 8192 && M > 2) return launch_i8w<1, 2, 16, 4>(cp, ap, bp, sp, M, N, K);
+    if (big) return launch_split<1, kSplitU>(cp, ap, bp, sp, M, N, K);
     return launch_i8w<1, 1, 8, 8>(cp, ap, bp, sp, M, N, K);
 }
 
-// The weight-streaming path takes transpose_b, M <= kMaxFusedM and K % 64 == 0.
+// The weight-streaming path takes transpose_b, M <= kMaxFusedM, 16-byte aligned
+// A and B, and K % 64 == 0 (K % 16 == 0 for M <= 4).
 bool use_i8w(const void* a, const void* b, int M, int K, int N, bool transpose_b) {
-    return transpose_b && M <= kMaxFusedM && K % kChunk == 0 && aligned16(a) && aligned16(b);
+    if (!transpose_b || M > kMaxFusedM || !aligned16(a) || !aligned16(b)) return false;
+    return K % kChunk == 0 || (M <= 4 && K % 16 == 0);
 }
 
 }  // namespace
