@@ -7,9 +7,10 @@
  * cuda_gemm_int8 computes C[M,N] = A[M,K] @ (B * scale)^T when transpose_b
  * (B int8 [N,K], scale[n] per row of B, the engine's layout), or
  * A @ (B * scale) when not (B int8 [K,N], scale[n] per column). Two paths:
- *   - transpose_b, K % 64 == 0, M <= 128, 16-byte aligned A and B: the int8
- *     weights are read once, converted to fp16 exactly in registers and
- *     multiplied on the matrix cores with fp32 sums; scale[n] is applied to
+ *   - transpose_b, M <= 128, K % 64 == 0 (K % 16 == 0 for M <= 4), 16-byte
+ *     aligned A and B: the int8 weights are read once, converted to fp16
+ *     exactly in registers and multiplied with fp32 sums (dot-product
+ *     instructions up to M = 4, matrix cores above); scale[n] is applied to
  *     the sum. No fp16 copy of the weights. For M > 4 the sum over K may be
  *     split into up to 8 slices whose fp32 partial sums (a per-stream buffer
  *     of S * M * N floats) a second kernel adds in a fixed order.
