@@ -428,15 +428,27 @@ __global__ __launch_bounds__(kSplitWaves * kWave) void gemm_i8w_split_kernel(
 }
 
 // C[m, n] = fp16(scale[n] * sum over slices q = 0 .. S-1, in that order, of
-// part[q][m][n]). One thread per element.
+// part[q][m][n]). Four outputs per thread when N % 4 == 0 (16-byte loads of
+// the partial sums and scales, one 8-byte store), else one.
+template <bool VEC4>
 __global__ __launch_bounds__(256) void split_reduce_kernel(uint16_t* __restrict__ c, const float* __restrict__ part,
                                                            const float* __restrict__ scale, int M, int N, int S) {
-    const size_t i = static_cast<size_t>(blockIdx.x) * 256 + threadIdx.x;
     const size_t mn = static_cast<size_t>(M) * N;
-    if (i >= mn) return;
-    float v = part[i];
-    for (int q = 1; q < S; ++q) v += part[static_cast<size_t>(q) * mn + i];
-    c[i] = from_f32<f16>(v * scale[i % N]);
+    const size_t t = static_cast<size_t>(blockIdx.x) * 256 + threadIdx.x;
+    if (VEC4) {
+        const size_t i = 4 * t;
+        if (i >= mn) return;
+        f32x4 v = *reinterpret_cast<const f32x4*>(part + i);
+        for (int q = 1; q < S; ++q) v += *reinterpret_cast<const f32x4*>(part + static_cast<size_t>(q) * mn + i);
+        const f32x4 sc = *reinterpret_cast<const f32x4*>(scale + i % N);
+        const u32x2 out = {pack2<f16>(v[0] * sc[0], v[1] * sc[1]), pack2<f16>(v[2] * sc[2], v[3] * sc[3])};
+        *reinterpret_cast<u32x2*>(c + i) = out;
+    } else {
+        if (t >= mn) return;
+        float v = part[t];
+        for (int q = 1; q < S; ++q) v += part[static_cast<size_t>(q) * mn + t];
+        c[t] = from_f32<f16>(v * scale[t % N]);
+    }
 }
 
 
@@ -613,8 +625,12 @@ int launch_split(uint16_t* c, const uint16_t* a, const int8_t* b, const float* s
     NG_CHECK_LAUNCH("cuda_gemm_int8");
     if (S > 1) {
         const size_t mn = static_cast<size_t>(M) * N;
-        split_reduce_kernel<<<dim3(static_cast<unsigned>((mn + 255) / 256)), dim3(256), 0, s>>>(c, part, scale, M, N,
-                                                                                                 S);
+        if (N % 4 == 0 && aligned16(scale) && aligned8(c))
+            split_reduce_kernel<true><<<dim3(static_cast<unsigned>((mn / 4 + 255) / 256)), dim3(256), 0, s>>>(
+                c, part, scale, M, N, S);
+        else
+            split_reduce_kernel<false><<<dim3(static_cast<unsigned>((mn + 255) / 256)), dim3(256), 0, s>>>(
+                c, part, scale, M, N, S);
         NG_CHECK_LAUNCH("cuda_gemm_int8");
     }
     return 0;
