@@ -16,16 +16,21 @@
 // fp16 first and sums those; the two differ by at most 2^-11 of
 // sum_k |A[m, k] * q[n, k] * scale[n]| plus the accumulation error.
 //
-// Layout of one wave's work: v_mfma_f32_16x16x32_f16 multiplies a 16 x 32
-// tile of A (rows m) by a 32 x 16 tile of B^T (columns n). Lane l supplies
-// row (l % 16) of each operand and 8 values of k; the accumulator lane l holds
-// rows 4 * (l / 16) + i, column l % 16. In a chunk of 64 k, lane group
-// g = l / 16 loads k = 16g .. 16g + 15 of its row of B with one 16-byte load
-// (64 bytes per row per instruction); the first 8 feed one MFMA and the last
-// 8 another, and A's lanes take the same k, so each MFMA sums matching k.
-// A block's waves split K between them (chunk c goes to wave c % WAVES) and
-// add their partial sums through LDS in a fixed order, so results do not
-// depend on timing.
+// Three kernels, by M (see gemm_i8w):
+//   M <= 4         gemv_i8w_kernel: dot-product instructions, each load reads
+//                  1 KiB contiguous of one row of B;
+//   4 < M <= 16    gemm_i8w_kernel: matrix cores, A read from L2;
+//   16 < M <= 128  gemm_i8w_split_kernel: matrix cores, A staged in LDS, K
+//                  split into slices whose sums a second kernel adds.
+// MFMA layout: v_mfma_f32_16x16x32_f16 multiplies a 16 x 32 tile of A (rows
+// m) by a 32 x 16 tile of B^T (columns n). Lane l supplies row (l % 16) of
+// each operand and 8 values of k; the accumulator lane l holds rows
+// 4 * (l / 16) + i, column l % 16. In a chunk of 64 k, lane group g = l / 16
+// loads k = 16g .. 16g + 15 of its row of B with one 16-byte load (64 bytes
+// per row per instruction); the first 8 feed one MFMA and the last 8 another,
+// and A's lanes take the same k, so each MFMA sums matching k.
+// Every sum is taken in a fixed order (partial sums meet in LDS or in the
+// slice buffer, never through atomics), so results do not depend on timing.
 #include "ng_common.hpp"
 #include "../../include/matmul.h"
 #include "../../include/neurogrid_ext.h"
@@ -71,8 +76,10 @@ __device__ __forceinline__ void codes16_to_operands(const u32x4 v, f16x8& b0, f1
     b1 = __builtin_bit_cast(f16x8, y);
 }
 
-// MT tiles of 16 rows of A x NT tiles of 16 rows of B per block; WAVES waves
-// split K; each wave loads U chunks, then multiplies them.
+// MT tiles of 16 rows of A x NT tiles of 16 rows of B per block. The WAVES
+// waves split K (chunk c goes to wave c % WAVES); each loads U chunks, then
+// multiplies them, and the waves' partial sums are added through LDS in wave
+// order.
 template <int MT, int NT, int WAVES, int U>
 __global__ __launch_bounds__(WAVES * kWave) void gemm_i8w_kernel(uint16_t* __restrict__ c,
                                                                   const uint16_t* __restrict__ a,
