@@ -38,7 +38,11 @@ struct EwArity {
     static constexpr bool binary = (OP == EW_ADD || OP == EW_MUL || OP == EW_SILU_MUL);
 };
 
-constexpr int kEwThreads = 256;
+// One wave per workgroup: measured on MI355X, 64-thread workgroups are 6-7%
+// faster than 256-thread ones for the streaming kernels here (SwiGLU on
+// [4096, 14336]: 53.4 vs 57.5 us; residual add on [4096, 4096]: 16.4 vs
+// 17.4 us), and 128 threads fall in between.
+constexpr int kEwThreads = 64;
 // One 16-byte vector per operand per thread: measured on MI355X, deeper
 // per-thread unrolling (2 or 4 vectors) is slower at every size from 0.5 MB
 // to 350 MB, and at decode sizes it leaves most CUs idle.
@@ -196,7 +200,7 @@ static int launch_cvt(const char* name, void* out, const void* in, size_t n) {
     const int vec = aligned16(out) && aligned16(in);
     size_t blocks = (n / 8 + kEwThreads - 1) / kEwThreads;
     if (blocks < 1) blocks = 1;
-    const size_t cap = static_cast<size_t>(device_cu_count()) * 16;
+    const size_t cap = static_cast<size_t>(device_cu_count()) * 64;  // 64 one-wave workgroups per CU
     if (blocks > cap) blocks = cap;
     cvt_kernel<K><<<dim3(static_cast<unsigned>(blocks)), dim3(kEwThreads), 0, stream()>>>(out, in, n, vec);
     NG_CHECK_LAUNCH(name);
@@ -297,7 +301,7 @@ extern "C" int ng_bf16_to_fp16_truncate(void* output, const void* input, size_t 
     const int vec = aligned16(output) && aligned16(input);
     size_t blocks = (n / 8 + kEwThreads - 1) / kEwThreads;
     if (blocks < 1) blocks = 1;
-    const size_t cap = static_cast<size_t>(device_cu_count()) * 16;
+    const size_t cap = static_cast<size_t>(device_cu_count()) * 64;  // 64 one-wave workgroups per CU
     if (blocks > cap) blocks = cap;
     bf16_to_f16_trunc_kernel<<<dim3(static_cast<unsigned>(blocks)), dim3(kEwThreads), 0, stream()>>>(
         static_cast<uint16_t*>(output), static_cast<const uint16_t*>(input), n, vec);

@@ -221,7 +221,7 @@ template <int MODE>
 __global__ __launch_bounds__(kQThreads) void dequant_chunk_kernel(uint16_t* out, const int8_t* q, const float* scales,
                                                                   uint32_t nchunks, FastDiv chunks_per_row) {
     const int lane = threadIdx.x & 63;
-    const uint32_t wv = blockIdx.x * (kQThreads / kWave) + (threadIdx.x >> 6);
+    const uint32_t wv = blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
     u32x2 v[kDqChunks];
     uint32_t ch[kDqChunks];
 #pragma unroll
@@ -279,8 +279,9 @@ static int launch_dequant(const char* name, void* out, const void* q, const void
     if (vec && cols % 512 == 0 && aligned8(q) && n / 512 < (1ull << 32)) {
         const uint32_t nchunks = static_cast<uint32_t>(n / 512);
         const uint32_t waves = (nchunks + kDqChunks - 1) / kDqChunks;
-        const unsigned blocks = (waves + kQThreads / kWave - 1) / (kQThreads / kWave);
-        dequant_chunk_kernel<MODE><<<dim3(blocks), dim3(kQThreads), 0, stream()>>>(
+        // One wave per workgroup: 28.7 vs 30.2 us at [14336, 4096] with four.
+        const unsigned blocks = waves;
+        dequant_chunk_kernel<MODE><<<dim3(blocks), dim3(kWave), 0, stream()>>>(
             static_cast<uint16_t*>(out), static_cast<const int8_t*>(q), static_cast<const float*>(scales), nchunks,
             make_fastdiv(static_cast<uint32_t>(cols / 512)));
     } else if (vec) {

@@ -214,7 +214,7 @@ __device__ __forceinline__ void head_rmsnorm(u32x4 (&x)[NV], const u32x4 (&w)[NV
 template <typename T, int STYLE, int HPL, bool QKNORM, bool ROT = true>
 __global__ __launch_bounds__(kRopeThreads) void rope_wave_kernel(RopeWaveArgs a) {
     const int lane = threadIdx.x & 63;
-    const uint32_t w = blockIdx.x * (kRopeThreads / kWave) + (threadIdx.x >> 6);
+    const uint32_t w = blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
     const int t = static_cast<int>(fdiv(w, a.div_G));
     if (t >= a.T) return;
     const int g = static_cast<int>(w) - t * a.G;
