@@ -25,9 +25,10 @@
  * Both return 0, or -1 with one line on stderr. They launch on ng_get_stream().
  * Buffers (library workspace, fp16 weight copy, partial sums) belong to a
  * (device, stream) pair; the first call that needs one allocates it and a
- * larger call grows it after synchronising the stream. A call that would
- * allocate while the stream is being captured fails instead: make one call
- * of each shape before capture.
+ * larger call replaces it with one at least twice its size. Replaced buffers
+ * are kept until cuda_shutdown, so a HIP graph that captured an earlier call
+ * stays valid. A call that would allocate while the stream is being captured
+ * fails instead: make one call of each shape before capture.
  */
 #ifndef NG_MATMUL_H
 #define NG_MATMUL_H

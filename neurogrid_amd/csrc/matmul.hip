@@ -41,6 +41,7 @@
 #include <mutex>
 #include <tuple>
 #include <utility>
+#include <vector>
 
 namespace ng {
 namespace {
@@ -498,6 +499,9 @@ std::mutex g_mu;
 std::map<int, hipblasLtHandle_t> g_handles;
 std::map<PlanKey, Plan> g_plans;
 std::map<std::pair<int, hipStream_t>, StreamBuffers> g_buffers;
+// Buffers replaced by larger ones. A HIP graph that captured an earlier call
+// still names the old buffer, so it is kept until gemm_release().
+std::vector<void*> g_retired;
 
 int capturing(hipStream_t s, bool* out) {
     hipStreamCaptureStatus st = hipStreamCaptureStatusNone;
@@ -506,25 +510,23 @@ int capturing(hipStream_t s, bool* out) {
     return 0;
 }
 
-// Make *p hold at least `need` bytes (zeroed if `zero`). Growing while the
-// stream is being captured is refused: allocation cannot be captured. Caller
-// holds g_mu.
-int grow(hipStream_t s, void** p, size_t* have, size_t need, bool zero) {
+// Make *p hold at least `need` bytes. Growing while the stream is being
+// captured is refused: allocation cannot be captured. The old buffer is
+// retired, not freed, so that graphs captured before the growth stay valid;
+// a new buffer is at least twice the old one, which bounds what is retired by
+// the final size. Caller holds g_mu.
+int grow(hipStream_t s, void** p, size_t* have, size_t need) {
     if (need <= *have) return 0;
     bool cap = false;
     if (capturing(s, &cap) != 0) return -1;
     NG_REQUIRE(!cap, "cuda_gemm: the stream is being captured and a buffer of %zu bytes must be allocated first; "
                      "make one call of this shape on the stream before capture", need);
-    if (*p != nullptr) {
-        // Earlier calls on this stream may still use the old buffer.
-        NG_HIP_CHECK(hipStreamSynchronize(s));
-        NG_HIP_CHECK(hipFree(*p));
-        *p = nullptr;
-        *have = 0;
-    }
-    NG_HIP_CHECK(hipMalloc(p, need));
-    *have = need;
-    if (zero) NG_HIP_CHECK(hipMemsetAsync(*p, 0, need, s));
+    const size_t bytes = need > 2 * *have ? need : 2 * *have;
+    void* fresh = nullptr;
+    NG_HIP_CHECK(hipMalloc(&fresh, bytes));
+    if (*p != nullptr) g_retired.push_back(*p);
+    *p = fresh;
+    *have = bytes;
     return 0;
 }
 
@@ -585,9 +587,9 @@ int gemm_lt(void* c, const void* a, const void* b, const void* q, const void* sc
     const Plan* p = nullptr;
     if (get_plan(dev, M, K, N, ta, tb, &p) != 0) return -1;
     StreamBuffers* sb = &g_buffers[{dev, s}];
-    if (grow(s, &sb->ws, &sb->ws_bytes, p->ws, false) != 0) return -1;
+    if (grow(s, &sb->ws, &sb->ws_bytes, p->ws) != 0) return -1;
     if (q != nullptr &&
-        grow(s, &sb->deq, &sb->deq_bytes, static_cast<size_t>(K) * static_cast<size_t>(N) * 2, false) != 0)
+        grow(s, &sb->deq, &sb->deq_bytes, static_cast<size_t>(K) * static_cast<size_t>(N) * 2) != 0)
         return -1;
     if (q != nullptr) {
         const int r = tb ? cuda_dequantize_weights(sb->deq, q, scale, N, K, 1)
@@ -623,7 +625,7 @@ int launch_split(uint16_t* c, const uint16_t* a, const int8_t* b, const float* s
         NG_HIP_CHECK(hipGetDevice(&dev));
         lock.lock();
         StreamBuffers* sb = &g_buffers[{dev, s}];
-        if (grow(s, &sb->part, &sb->part_bytes, static_cast<size_t>(S) * M * N * sizeof(float), false) != 0)
+        if (grow(s, &sb->part, &sb->part_bytes, static_cast<size_t>(S) * M * N * sizeof(float)) != 0)
             return -1;
         part = static_cast<float*>(sb->part);
     }
@@ -691,6 +693,8 @@ void gemm_release() {
             if (b != nullptr) (void)hipFree(b);
     }
     g_buffers.clear();
+    for (void* b : g_retired) (void)hipFree(b);
+    g_retired.clear();
     for (auto& kv : g_handles) hipblasLtDestroy(kv.second);
     g_handles.clear();
 }
