@@ -26,9 +26,11 @@
 // m) by a 32 x 16 tile of B^T (columns n). Lane l supplies row (l % 16) of
 // each operand and 8 values of k; the accumulator lane l holds rows
 // 4 * (l / 16) + i, column l % 16. In a chunk of 64 k, lane group g = l / 16
-// loads k = 16g .. 16g + 15 of its row of B with one 16-byte load (64 bytes
-// per row per instruction); the first 8 feed one MFMA and the last 8 another,
-// and A's lanes take the same k, so each MFMA sums matching k.
+// holds k = 16g .. 16g + 15 of its row of B (16 codes); the first 8 feed one
+// MFMA and the last 8 another, and A's lanes take the same k, so each MFMA
+// sums matching k. The small-M kernel loads B straight into that layout (64
+// bytes per row per instruction); the split kernel reads whole 128-byte lines
+// and reorders them through LDS.
 // Every sum is taken in a fixed order (partial sums meet in LDS or in the
 // slice buffer, never through atomics), so results do not depend on timing.
 #include "ng_common.hpp"
@@ -306,25 +308,35 @@ int launch_gemv(uint16_t* c, const uint16_t* a, const int8_t* b, const float* sc
 // For more than a few rows of A the kernel above reads A from L2 once per
 // 16 rows of B: at M = 64 that is 8 bytes of A per weight byte. Here a block
 // of kSplitWaves waves owns 16 * kSplitWaves rows of B and one of S slices of
-// K; the A columns of each batch of U chunks are staged once in LDS and shared
-// by the block's waves (2M / (16 * kSplitWaves) bytes of A per weight byte).
+// K; the A columns of each 128-k batch are staged once in LDS and shared by
+// the block's waves (2M / (16 * kSplitWaves) bytes of A per weight byte).
+//
+// B is read in whole 128-byte lines: each load instruction of a wave covers
+// 8 rows x 128 codes (8 lanes per row), two instructions a wave's 16 rows.
+// Loading B straight into the MFMA layout instead (4 lanes per row, 64 bytes
+// per row per instruction) streams about 25% slower on MI355X. The codes
+// reach the MFMA layout through a per-wave LDS buffer: piece p (16 codes) of
+// row r sits in slot 8r + ((p + r / 2) mod 8), so the writes are contiguous
+// and the 16 rows read by one lane group fall in 16 different bank groups.
+//
 // With S > 1 each block stores its fp32 partial sums in `part` [S][M][N] and a
 // second kernel adds the S slices in slice order, so the result does not
 // depend on timing. (Having the last block of each tile add them instead needs
 // an agent-scope release and acquire per block, which on MI355X write back and
 // invalidate the whole L2: measured 3-5x slower.)
 constexpr int kSplitWaves = 4;
-constexpr int kSplitU = 2;  // chunks per batch (2 and 4 measured; 2 is 5% faster at M = 64)
+constexpr int kBatch = 128;  // k per batch
 
-template <int MT, int U>
+template <int MT>
 __global__ __launch_bounds__(kSplitWaves * kWave) void gemm_i8w_split_kernel(
     uint16_t* __restrict__ c, const uint16_t* __restrict__ a, const int8_t* __restrict__ b,
     const float* __restrict__ scale, float* __restrict__ part, int M, int N, int K, int S, int tiles, int cps) {
-    constexpr int kRowBytes = U * kChunk * 2 + 16;  // one row of a batch of A in LDS, padded by 16 bytes
-    constexpr int kPieces = 16 * MT * U * 8;        // 16-byte pieces of A per batch
+    constexpr int kRowBytes = kBatch * 2 + 16;  // one row of a batch of A in LDS, padded by 16 bytes
+    constexpr int kPieces = 16 * MT * 16;       // 16-byte pieces of A per batch
     constexpr int kThreads = kSplitWaves * kWave;
     static_assert(kPieces % kThreads == 0, "A pieces must divide among the threads");
     __shared__ __align__(16) uint8_t lds_a[2][16 * MT * kRowBytes];
+    __shared__ __align__(16) u32x4 lds_b[kSplitWaves][2 * kWave];
 
     const int sl = blockIdx.x % S;
     const int tile = blockIdx.x / S;
@@ -334,80 +346,108 @@ __global__ __launch_bounds__(kSplitWaves * kWave) void gemm_i8w_split_kernel(
     const int wave = __builtin_amdgcn_readfirstlane(tid / kWave);
     const int col = lane & 15;
     const int grp = lane >> 4;
-    const int nchunks = K / kChunk;
+    const int nbatch = (K + kBatch - 1) / kBatch;  // the last batch holds 64 k when K % 128 == 64
+    const bool half_last = (K % kBatch) != 0;
     const int c0 = sl * cps;
-    const int c1 = min(c0 + cps, nchunks);
-    const int n = tile * (16 * kSplitWaves) + 16 * wave + col;
-    const int8_t* brow = b + static_cast<size_t>(min(n, N - 1)) * K + 16 * grp;
+    const int c1 = min(c0 + cps, nbatch);
+    const int nw = tile * (16 * kSplitWaves) + 16 * wave;  // first row of B of this wave
+    const int n = nw + col;                                 // row of B this lane multiplies
+
+    // Row and piece this lane loads in each of the two B instructions.
+    const int8_t* brow[2];
+    int bpiece[2];
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+        const int r = 8 * j + (lane >> 3);
+        bpiece[j] = ((lane & 7) - (r >> 1)) & 7;
+        brow[j] = b + static_cast<size_t>(min(nw + r, N - 1)) * K;
+    }
 
     f32x4 acc[MT];
 #pragma unroll
     for (int i = 0; i < MT; ++i) acc[i] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
 
-    // Batches of U chunks, two in flight: the loads of batch i + 1 (B into
-    // registers, A into registers on their way to LDS) are issued before batch
-    // i is multiplied; A alternates between two LDS buffers, so one barrier
-    // per batch separates a buffer's writes from its reads and from its reuse
-    // two batches later.
+    // Batches, two in flight: the loads of batch i + 1 (B into registers, A
+    // into registers on their way to LDS) are issued before batch i is
+    // multiplied; A alternates between two LDS buffers, so one barrier per
+    // batch separates a buffer's writes from its reads and from its reuse two
+    // batches later.
     constexpr int kP = kPieces / kThreads;
-    // A first: staging it into LDS then waits only for A, not for B. Chunks
-    // past the slice (a batch past the last is loaded too, to keep every load
-    // unconditional) are clamped to its last chunk.
-    auto load = [&](u32x4 (&bv)[U], u32x4 (&ar)[kP], int cb) {
+    // A first: staging it into LDS then waits only for A, not for B. Batches
+    // past the slice (one past the last is loaded too, to keep every load
+    // unconditional) are clamped to its last batch.
+    auto load = [&](u32x4 (&bv)[2], u32x4 (&ar)[kP], int cb) {
+        const bool half = half_last && cb == nbatch - 1;
+        const size_t kb = static_cast<size_t>(cb) * kBatch;
 #pragma unroll
         for (int j = 0; j < kP; ++j) {
             const int pc = j * kThreads + tid;
-            const int row = pc / (U * 8);
-            const int q = pc % (U * 8);
-            const int ch = min(cb + q / 8, c1 - 1);
-            ar[j] = ld16(a + static_cast<size_t>(min(row, M - 1)) * K + ch * kChunk + 8 * (q % 8));
+            const int row = pc / 16;
+            int q = pc % 16;
+            if (half) q &= 7;  // k past K: load the batch's first 64 k again
+            ar[j] = ld16(a + static_cast<size_t>(min(row, M - 1)) * K + kb + 8 * q);
         }
+        __builtin_amdgcn_sched_barrier(0);  // keep A's loads ahead of B's
+        // Pieces 4-7 of a half batch would lie past K: they load pieces 0-3
+        // again (and multiply zero codes).
 #pragma unroll
-        for (int u = 0; u < U; ++u) bv[u] = ld16_stream(brow + static_cast<size_t>(min(cb + u, c1 - 1)) * kChunk);
+        for (int j = 0; j < 2; ++j) {
+            const int pcs = half ? (bpiece[j] & 3) : bpiece[j];
+            bv[j] = ld16_stream(brow[j] + kb + 16 * pcs);
+        }
     };
     auto stage = [&](int buf, const u32x4 (&ar)[kP]) {
 #pragma unroll
         for (int j = 0; j < kP; ++j) {
             const int pc = j * kThreads + tid;
-            const int row = pc / (U * 8);
-            const int q = pc % (U * 8);
-            *reinterpret_cast<u32x4*>(lds_a[buf] + row * kRowBytes + (q / 8) * (kChunk * 2) + 16 * (q % 8)) = ar[j];
+            *reinterpret_cast<u32x4*>(lds_a[buf] + (pc / 16) * kRowBytes + 16 * (pc % 16)) = ar[j];
         }
     };
-    auto multiply = [&](int buf, u32x4 (&bv)[U], int cb) {
+    auto multiply = [&](int buf, const u32x4 (&bv)[2], int cb) {
+        // This wave's codes into the MFMA layout. LDS operations of one wave
+        // complete in order, so the reads see the writes, and the next batch's
+        // writes come after these reads.
+        lds_b[wave][lane] = bv[0];
+        lds_b[wave][kWave + lane] = bv[1];
+        __builtin_amdgcn_wave_barrier();
+        const bool past = cb >= c1;                               // clamped batch: multiplies zero codes
+        const bool half = half_last && cb == nbatch - 1;          // its second 64 k lie past K
 #pragma unroll
-        for (int u = 0; u < U; ++u) {
-            if (cb + u >= c1) bv[u] = u32x4{0u, 0u, 0u, 0u};  // a clamped chunk multiplies zero codes
+        for (int st = 0; st < 2; ++st) {
+            const int p = 4 * st + grp;
+            u32x4 v = lds_b[wave][8 * col + ((p + (col >> 1)) & 7)];
+            if (past || (half && st == 1)) v = u32x4{0u, 0u, 0u, 0u};
             f16x8 b0, b1;
-            codes16_to_operands(bv[u], b0, b1);
+            codes16_to_operands(v, b0, b1);
 #pragma unroll
             for (int t = 0; t < MT; ++t) {
-                const uint8_t* ap = lds_a[buf] + (16 * t + col) * kRowBytes + u * (kChunk * 2) + 32 * grp;
+                const uint8_t* ap = lds_a[buf] + (16 * t + col) * kRowBytes + st * 128 + 32 * grp;
                 const u32x4 a0 = *reinterpret_cast<const u32x4*>(ap);
                 const u32x4 a1 = *reinterpret_cast<const u32x4*>(ap + 16);
                 acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, a0), b0, acc[t], 0, 0, 0);
                 acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, a1), b1, acc[t], 0, 0, 0);
             }
         }
+        __builtin_amdgcn_wave_barrier();
     };
     // The batch count is rounded up to even: an extra batch past the slice
     // multiplies zero codes. (Leaving the loop after an odd batch instead lets
     // the compiler sink the next batch's loads below the multiply.)
-    const int nb = (c1 - c0 + U - 1) / U;
-    u32x4 bv0[U], bv1[U];
+    const int nb = c1 - c0;
+    u32x4 bv0[2], bv1[2];
     u32x4 ar0[kP], ar1[kP];
     load(bv0, ar0, c0);
     for (int i = 0; i < nb; i += 2) {
         stage(0, ar0);
         __syncthreads();
-        load(bv1, ar1, min(c0 + (i + 1) * U, c1 - 1));
+        load(bv1, ar1, min(c0 + i + 1, c1 - 1));
         __builtin_amdgcn_sched_barrier(0);
-        multiply(0, bv0, c0 + i * U);
+        multiply(0, bv0, c0 + i);
         stage(1, ar1);
         __syncthreads();
-        load(bv0, ar0, min(c0 + (i + 2) * U, c1 - 1));
+        load(bv0, ar0, min(c0 + i + 2, c1 - 1));
         __builtin_amdgcn_sched_barrier(0);
-        multiply(1, bv1, c0 + (i + 1) * U);
+        multiply(1, bv1, c0 + i + 1);
     }
 
     if (S == 1) {
@@ -603,17 +643,17 @@ int gemm_lt(void* c, const void* a, const void* b, const void* q, const void* sc
     return 0;
 }
 
-template <int MT, int U>
+template <int MT>
 int launch_split(uint16_t* c, const uint16_t* a, const int8_t* b, const float* scale, int M, int N, int K) {
     const int tiles = (N + 16 * kSplitWaves - 1) / (16 * kSplitWaves);
-    const int nchunks = K / kChunk;
+    const int nbatch = (K + kBatch - 1) / kBatch;
     // Enough slices of K for about 256 blocks (512 for K >= 8192), at most 8,
-    // each of at least two chunks, none empty.
+    // each of at least two batches, none empty.
     const int target = K >= 8192 ? 512 : 256;
     int S = (target + tiles - 1) / tiles;
-    S = max(1, min(S, min(8, nchunks / 2)));
-    const int cps = (nchunks + S - 1) / S;
-    S = (nchunks + cps - 1) / cps;
+    S = max(1, min(S, min(8, nbatch / 2)));
+    const int cps = (nbatch + S - 1) / S;
+    S = (nbatch + cps - 1) / cps;
     // With S > 1 the partial-sum buffer is this stream's: the lock is held
     // until both kernels are enqueued, so calls from other host threads on the
     // same stream cannot slip a launch between them.
@@ -629,7 +669,7 @@ int launch_split(uint16_t* c, const uint16_t* a, const int8_t* b, const float* s
             return -1;
         part = static_cast<float*>(sb->part);
     }
-    gemm_i8w_split_kernel<MT, U><<<dim3(static_cast<unsigned>(tiles * S)), dim3(kSplitWaves * kWave), 0, s>>>(
+    gemm_i8w_split_kernel<MT><<<dim3(static_cast<unsigned>(tiles * S)), dim3(kSplitWaves * kWave), 0, s>>>(
         c, a, b, scale, part, M, N, K, S, tiles, cps);
     NG_CHECK_LAUNCH("cuda_gemm_int8");
     if (S > 1) {
@@ -662,10 +702,10 @@ int gemm_i8w(void* c, const void* a, const void* b, const void* scale, int M, in
         if (M == 2) return launch_gemv<2, 8>(cp, ap, bp, sp, M, N, K);
         return launch_gemv<4, 4>(cp, ap, bp, sp, M, N, K);
     }
-    if (M > 64) return launch_split<8, kSplitU>(cp, ap, bp, sp, M, N, K);
-    if (M > 32) return launch_split<4, kSplitU>(cp, ap, bp, sp, M, N, K);
-    if (M > 16) return launch_split<2, kSplitU>(cp, ap, bp, sp, M, N, K);
-    if (big) return launch_split<1, kSplitU>(cp, ap, bp, sp, M, N, K);
+    if (M > 64) return launch_split<8>(cp, ap, bp, sp, M, N, K);
+    if (M > 32) return launch_split<4>(cp, ap, bp, sp, M, N, K);
+    if (M > 16) return launch_split<2>(cp, ap, bp, sp, M, N, K);
+    if (big) return launch_split<1>(cp, ap, bp, sp, M, N, K);
     return launch_i8w<1, 1, 8, 8>(cp, ap, bp, sp, M, N, K);
 }
 
