@@ -18,7 +18,8 @@
 // read their fp16 operands directly (v_fma_mix_f32, see el_mul / el_add), so
 // the kernels spend about 6 VALU operations per element (13 with int8 codes)
 // and stay under the HBM time. The sum of squares runs in fp64 (exact
-// squares, error-free combination across lanes and waves).
+// squares, any order) and is resolved to RN_f32 against a rigorous error
+// bound, with an exact fallback (ng_exact.hpp).
 //
 // Layout: one workgroup per row, the row held in registers. Lane l of a
 // workgroup of nthr threads owns the 16-byte vectors l, l + nthr, ...; a row
@@ -137,20 +138,35 @@ __global__ __launch_bounds__(MaxThreads<V>::value) void row_kernel(RowArgs a) {
         // converts again instead of holding 8 V unpacked floats.
 #pragma unroll
         for (int k = 0; k < V; ++k) __asm__("" : "+v"(ov[k]));
-        DD S = dd_add(two_sum(acc[0], acc[1]), two_sum(acc[2], acc[3]));
-        S = wave_sum_dd(S);
-        if (nw > 1) {
-            if (lane == 0) {
-                s_part[wid][0] = S.hi;
-                s_part[wid][1] = S.lo;
+        // S sums the nthr * V * 8 squares (padding included) in fp64. Plain
+        // RMSNorm combines them with error-free transformations instead: the
+        // bound is then tighter, and the extra arithmetic before its first
+        // store makes it faster (measured on MI355X at T = H = 4096: 11.0 vs
+        // 11.45 us); the other variants are faster without it.
+        double S;
+        if constexpr (kWeightsLate) {
+            DD D2 = wave_sum_dd(dd_add(two_sum(acc[0], acc[1]), two_sum(acc[2], acc[3])));
+            if (nw > 1) {
+                if (lane == 0) {
+                    s_part[wid][0] = D2.hi;
+                    s_part[wid][1] = D2.lo;
+                }
+                __syncthreads();
+                D2 = {s_part[0][0], s_part[0][1]};
+                for (int j = 1; j < nw; ++j) D2 = dd_add(D2, DD{s_part[j][0], s_part[j][1]});
             }
-            __syncthreads();
-            S = {s_part[0][0], s_part[0][1]};
-            for (int j = 1; j < nw; ++j) S = dd_add(S, DD{s_part[j][0], s_part[j][1]});
+            S = D2.hi;
+        } else {
+            S = wave_sum_f64_dpp((acc[0] + acc[1]) + (acc[2] + acc[3]));
+            if (nw > 1) {
+                if (lane == 0) s_part[wid][0] = S;
+                __syncthreads();
+                S = s_part[0][0];
+                for (int j = 1; j < nw; ++j) S += s_part[j][0];
+            }
         }
         float ss;
-        // Each accumulator holds 2 V squares.
-        if (!ss_fast_resolve(S.hi, 2 * V, ss)) {
+        if (!ss_fast_resolve(S, nthr * V * 8, ss)) {
             // Exact path (identical decision in every thread of the row). It
             // re-reads the row: nothing has been stored yet, so in-place
             // calls still see their inputs, and the registers above stay free.
@@ -341,10 +357,9 @@ __global__ __launch_bounds__(64) void add_rms_rows_kernel(RowArgs a, int rows) {
                 acc[(2 * i + 1) & 3] = __builtin_fma(d1, d1, acc[(2 * i + 1) & 3]);
             }
         }
-        DD S = dd_add(two_sum(acc[0], acc[1]), two_sum(acc[2], acc[3]));
-        S = wave_sum_dd(S);
+        const double S = wave_sum_f64_dpp((acc[0] + acc[1]) + (acc[2] + acc[3]));
         float ss;
-        if (!ss_fast_resolve(S.hi, 2 * V, ss)) exact_row_ss_wave<T, true>(X + off, RS + off, a.nvec, lane, ss);
+        if (!ss_fast_resolve(S, kWave * V * 8, ss)) exact_row_ss_wave<T, true>(X + off, RS + off, a.nvec, lane, ss);
         const float r = 1.0f / __builtin_sqrtf(ss / static_cast<float>(a.H) + a.eps);
         uint16_t* ro = static_cast<uint16_t*>(a.res_out) + off;
         uint16_t* yr = static_cast<uint16_t*>(a.y) + off;

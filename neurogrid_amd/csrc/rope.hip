@@ -152,16 +152,7 @@ struct RopeWaveArgs {
 // Sums over the lph consecutive lanes that hold one head (lph a power of two
 // up to 32). Each step adds the value of a partner lane in the complementary
 // half of the current group, so every lane of the group ends with the same
-// bits (dd_add is commutative bit for bit).
-__device__ __forceinline__ DD group_sum_dd(DD v, int lph) {
-    if (lph > 1) v = dd_add(v, dpp_dd<kDppQuadSwap1>(v));
-    if (lph > 2) v = dd_add(v, dpp_dd<kDppQuadSwap2>(v));
-    if (lph > 4) v = dd_add(v, dpp_dd<kDppRowHalfMirror>(v));
-    if (lph > 8) v = dd_add(v, dpp_dd<kDppRowMirror>(v));
-    if (lph > 16) v = dd_add(v, DD{__shfl_xor(v.hi, 16, kWave), __shfl_xor(v.lo, 16, kWave)});
-    return v;
-}
-
+// bits (fp64 addition is commutative bit for bit).
 __device__ __forceinline__ double group_sum_f64(double v, int lph) {
     if (lph > 1) v += dpp_f64<kDppQuadSwap1>(v);
     if (lph > 2) v += dpp_f64<kDppQuadSwap2>(v);
@@ -186,9 +177,9 @@ __device__ __forceinline__ void head_rmsnorm(u32x4 (&x)[NV], const u32x4 (&w)[NV
             acc[(2 * i) & 3] = __builtin_fma(d0, d0, acc[(2 * i) & 3]);
             acc[(2 * i + 1) & 3] = __builtin_fma(d1, d1, acc[(2 * i + 1) & 3]);
         }
-    const DD S = group_sum_dd(dd_add(two_sum(acc[0], acc[1]), two_sum(acc[2], acc[3])), lph);
+    const double S = group_sum_f64((acc[0] + acc[1]) + (acc[2] + acc[3]), lph);
     float ss;
-    if (!ss_fast_resolve(S.hi, 2 * NV, ss)) {
+    if (!ss_fast_resolve(S, lph * NV * 8, ss)) {
         // Exact path for this head (the whole lane group takes it together).
         Limbs Lm{0.0, 0.0, 0.0, 0};
 #pragma unroll
