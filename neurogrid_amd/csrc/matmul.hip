@@ -19,7 +19,8 @@
 // Three kernels, by M (see gemm_i8w):
 //   M <= 4         gemv_i8w_kernel: dot-product instructions, each load reads
 //                  1 KiB contiguous of one row of B;
-//   4 < M <= 16    gemm_i8w_kernel: matrix cores, A read from L2;
+//   4 < M <= 16    gemm_i8w_kernel: matrix cores, A read from L2, waves
+//                  split K within the block;
 //   16 < M <= 128  gemm_i8w_split_kernel: matrix cores, A staged in LDS, K
 //                  split into slices whose sums a second kernel adds.
 // MFMA layout: v_mfma_f32_16x16x32_f16 multiplies a 16 x 32 tile of A (rows
@@ -28,9 +29,10 @@
 // 4 * (l / 16) + i, column l % 16. In a chunk of 64 k, lane group g = l / 16
 // holds k = 16g .. 16g + 15 of its row of B (16 codes); the first 8 feed one
 // MFMA and the last 8 another, and A's lanes take the same k, so each MFMA
-// sums matching k. The small-M kernel loads B straight into that layout (64
-// bytes per row per instruction); the split kernel reads whole 128-byte lines
-// and reorders them through LDS.
+// sums matching k. The two MFMA kernels read B in whole 128-byte lines (8 rows
+// x 128 codes per load instruction) and reorder the codes into that layout
+// through LDS: loading straight into it reads 64 bytes per row per
+// instruction, which streams about 25% slower on MI355X.
 // Every sum is taken in a fixed order (partial sums meet in LDS or in the
 // slice buffer, never through atomics), so results do not depend on timing.
 #include "ng_common.hpp"
@@ -79,114 +81,116 @@ __device__ __forceinline__ void codes16_to_operands(const u32x4 v, f16x8& b0, f1
     b1 = __builtin_bit_cast(f16x8, y);
 }
 
-// MT tiles of 16 rows of A x NT tiles of 16 rows of B per block. The WAVES
-// waves split K (chunk c goes to wave c % WAVES); each loads U chunks, then
-// multiplies them, and the waves' partial sums are added through LDS in wave
-// order.
+// MT tiles of 16 rows of A x one tile of 16 rows of B per block. The WAVES
+// waves split K in 128-k batches (batch b goes to wave b % WAVES); each loads
+// U batches, then multiplies them, and the waves' partial sums are added
+// through LDS in wave order. B is read in whole 128-byte lines (8 rows x 128
+// codes per instruction) and reordered into the MFMA layout through a per-wave
+// LDS buffer, as in the split kernel below.
 template <int MT, int NT, int WAVES, int U>
 __global__ __launch_bounds__(WAVES * kWave) void gemm_i8w_kernel(uint16_t* __restrict__ c,
                                                                   const uint16_t* __restrict__ a,
                                                                   const int8_t* __restrict__ b,
                                                                   const float* __restrict__ scale, int M, int N,
                                                                   int K) {
-    __shared__ f32x4 partial[WAVES - 1][MT * NT][kWave];
+    static_assert(NT == 1, "one tile of B per block");
+    __shared__ f32x4 partial[WAVES - 1][MT][kWave];
+    __shared__ __align__(16) u32x4 lds_b[WAVES][2 * kWave];
     const int lane = threadIdx.x & (kWave - 1);
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
     const int col = lane & 15;
     const int grp = lane >> 4;
-    const int n0 = blockIdx.x * (16 * NT);
+    const int n0 = blockIdx.x * 16;
+    const int nbatch = (K + 127) / 128;
+    const bool half_last = (K % 128) != 0;
 
-    // Rows past N (M) are clamped to the last row: they are loaded and
-    // multiplied like the others, and their outputs are never stored.
-    const int8_t* bp[NT];
+    const int8_t* brow[2];
+    int bpiece[2];
 #pragma unroll
-    for (int t = 0; t < NT; ++t) {
-        const int n = min(n0 + 16 * t + col, N - 1);
-        bp[t] = b + static_cast<size_t>(n) * K + 16 * grp;
+    for (int j = 0; j < 2; ++j) {
+        const int r = 8 * j + (lane >> 3);
+        bpiece[j] = ((lane & 7) - (r >> 1)) & 7;
+        brow[j] = b + static_cast<size_t>(min(n0 + r, N - 1)) * K;
     }
     const uint16_t* ap[MT];
 #pragma unroll
-    for (int t = 0; t < MT; ++t) {
-        const int m = min(16 * t + col, M - 1);
-        ap[t] = a + static_cast<size_t>(m) * K + 16 * grp;
-    }
+    for (int t = 0; t < MT; ++t) ap[t] = a + static_cast<size_t>(min(16 * t + col, M - 1)) * K + 16 * grp;
 
-    f32x4 acc[MT][NT];
+    f32x4 acc[MT];
 #pragma unroll
-    for (int i = 0; i < MT; ++i)
-#pragma unroll
-        for (int j = 0; j < NT; ++j) acc[i][j] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+    for (int i = 0; i < MT; ++i) acc[i] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
 
-    // This wave's chunks are wave, wave + WAVES, ...
-    const int nchunks = K / kChunk;
-    const int cnt = wave < nchunks ? (nchunks - wave + WAVES - 1) / WAVES : 0;
+    const int cnt = wave < nbatch ? (nbatch - wave + WAVES - 1) / WAVES : 0;
     if (cnt > 0) {
         const int last = wave + (cnt - 1) * WAVES;
-        u32x4 bv[U][NT];
-        u32x4 av[U][MT][2];
+        u32x4 bv[U][2];
+        u32x4 av[U][MT][2][2];
         auto load = [&](int slot, int i) {
-            // Chunks past this wave's last are clamped to it (and multiply zero codes).
-            const size_t k = static_cast<size_t>(min(wave + i * WAVES, last)) * kChunk;
+            // Batches past this wave's last are clamped to it (and multiply zero codes).
+            const int bt = min(wave + i * WAVES, last);
+            const bool half = half_last && bt == nbatch - 1;
+            const size_t kb = static_cast<size_t>(bt) * 128;
 #pragma unroll
-            for (int t = 0; t < NT; ++t) bv[slot][t] = ld16_stream(bp[t] + k);
+            for (int j = 0; j < 2; ++j) bv[slot][j] = ld16_stream(brow[j] + kb + 16 * (half ? (bpiece[j] & 3) : bpiece[j]));
 #pragma unroll
-            for (int t = 0; t < MT; ++t) {
-                av[slot][t][0] = ld16(ap[t] + k);
-                av[slot][t][1] = ld16(ap[t] + k + 8);
-            }
+            for (int t = 0; t < MT; ++t)
+#pragma unroll
+                for (int st = 0; st < 2; ++st) {
+                    const size_t k = kb + ((half && st == 1) ? 0 : 64 * st);
+                    av[slot][t][st][0] = ld16(ap[t] + k);
+                    av[slot][t][st][1] = ld16(ap[t] + k + 8);
+                }
         };
-        auto multiply = [&](int u, bool valid) {
-            if (!valid) {
+        auto multiply = [&](int u, int i) {
+            const int bt = wave + i * WAVES;
+            const bool past = i >= cnt;
+            const bool half = half_last && bt == nbatch - 1;
+            lds_b[wave][lane] = bv[u][0];
+            lds_b[wave][kWave + lane] = bv[u][1];
+            __builtin_amdgcn_wave_barrier();
 #pragma unroll
-                for (int t = 0; t < NT; ++t) bv[u][t] = u32x4{0u, 0u, 0u, 0u};
-            }
-#pragma unroll
-            for (int t = 0; t < NT; ++t) {
+            for (int st = 0; st < 2; ++st) {
+                const int p = 4 * st + grp;
+                u32x4 v = lds_b[wave][8 * col + ((p + (col >> 1)) & 7)];
+                if (past || (half && st == 1)) v = u32x4{0u, 0u, 0u, 0u};
                 f16x8 b0, b1;
-                codes16_to_operands(bv[u][t], b0, b1);
+                codes16_to_operands(v, b0, b1);
 #pragma unroll
-                for (int s = 0; s < MT; ++s) {
-                    acc[s][t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, av[u][s][0]), b0,
-                                                                       acc[s][t], 0, 0, 0);
-                    acc[s][t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, av[u][s][1]), b1,
-                                                                       acc[s][t], 0, 0, 0);
+                for (int t = 0; t < MT; ++t) {
+                    acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, av[u][t][st][0]), b0,
+                                                                    acc[t], 0, 0, 0);
+                    acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, av[u][t][st][1]), b1,
+                                                                    acc[t], 0, 0, 0);
                 }
             }
+            __builtin_amdgcn_wave_barrier();
         };
-        // U chunks are loaded, then multiplied. (Refilling each slot as soon as it
-        // is multiplied measured slower: the compiler then waits for all but the
-        // newest chunk at the top of every iteration.)
         for (int i = 0; i < cnt; i += U) {
 #pragma unroll
             for (int u = 0; u < U; ++u) load(u, i + u);
             __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-            for (int u = 0; u < U; ++u) multiply(u, i + u < cnt);
+            for (int u = 0; u < U; ++u) multiply(u, i + u);
         }
     }
 
     if (wave > 0) {
 #pragma unroll
-        for (int i = 0; i < MT; ++i)
-#pragma unroll
-            for (int j = 0; j < NT; ++j) partial[wave - 1][i * NT + j][lane] = acc[i][j];
+        for (int i = 0; i < MT; ++i) partial[wave - 1][i][lane] = acc[i];
     }
     __syncthreads();
     if (wave != 0) return;
+    const int n = n0 + col;
+    const float s = scale[min(n, N - 1)];
 #pragma unroll
-    for (int j = 0; j < NT; ++j) {
-        const int n = n0 + 16 * j + col;
-        const float s = scale[min(n, N - 1)];
+    for (int i = 0; i < MT; ++i) {
+        f32x4 v = acc[i];
 #pragma unroll
-        for (int i = 0; i < MT; ++i) {
-            f32x4 v = acc[i][j];
+        for (int w = 0; w < WAVES - 1; ++w) v += partial[w][i][lane];
 #pragma unroll
-            for (int w = 0; w < WAVES - 1; ++w) v += partial[w][i * NT + j][lane];
-#pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                const int m = 16 * i + 4 * grp + e;
-                if (m < M && n < N) c[static_cast<size_t>(m) * N + n] = from_f32<f16>(v[e] * s);
-            }
+        for (int e = 0; e < 4; ++e) {
+            const int m = 16 * i + 4 * grp + e;
+            if (m < M && n < N) c[static_cast<size_t>(m) * N + n] = from_f32<f16>(v[e] * s);
         }
     }
 }
@@ -331,7 +335,10 @@ template <int MT>
 __global__ __launch_bounds__(kSplitWaves * kWave) void gemm_i8w_split_kernel(
     uint16_t* __restrict__ c, const uint16_t* __restrict__ a, const int8_t* __restrict__ b,
     const float* __restrict__ scale, float* __restrict__ part, int M, int N, int K, int S, int tiles, int cps) {
-    constexpr int kRowBytes = kBatch * 2 + 16;  // one row of a batch of A in LDS, padded by 16 bytes
+    // One row of a batch of A in LDS, padded by 32 bytes: measured on MI355X,
+    // 16 bytes of padding leave bank conflicts that cost 3-6% at M = 64-128
+    // (none: 1.6-1.8x slower; 48-96 bytes: no better at M = 64, slower at 128).
+    constexpr int kRowBytes = kBatch * 2 + 32;
     constexpr int kPieces = 16 * MT * 16;       // 16-byte pieces of A per batch
     constexpr int kThreads = kSplitWaves * kWave;
     static_assert(kPieces % kThreads == 0, "A pieces must divide among the threads");
@@ -706,7 +713,7 @@ int gemm_i8w(void* c, const void* a, const void* b, const void* scale, int M, in
     if (M > 32) return launch_split<4>(cp, ap, bp, sp, M, N, K);
     if (M > 16) return launch_split<2>(cp, ap, bp, sp, M, N, K);
     if (big) return launch_split<1>(cp, ap, bp, sp, M, N, K);
-    return launch_i8w<1, 1, 8, 8>(cp, ap, bp, sp, M, N, K);
+    return launch_i8w<1, 1, 8, 4>(cp, ap, bp, sp, M, N, K);
 }
 
 // The weight-streaming path takes transpose_b, M <= kMaxFusedM, 16-byte aligned
