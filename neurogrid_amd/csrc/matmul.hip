@@ -426,14 +426,21 @@ __global__ __launch_bounds__(kSplitWaves * kWave) void gemm_i8w_split_kernel(
             if (past || (half && st == 1)) v = u32x4{0u, 0u, 0u, 0u};
             f16x8 b0, b1;
             codes16_to_operands(v, b0, b1);
+            // All tiles' first halves, then their second halves: consecutive
+            // MFMAs update different accumulators (2-4% faster at M = 64-128).
+            u32x4 a0[MT], a1[MT];
 #pragma unroll
             for (int t = 0; t < MT; ++t) {
                 const uint8_t* ap = lds_a[buf] + (16 * t + col) * kRowBytes + st * 128 + 32 * grp;
-                const u32x4 a0 = *reinterpret_cast<const u32x4*>(ap);
-                const u32x4 a1 = *reinterpret_cast<const u32x4*>(ap + 16);
-                acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, a0), b0, acc[t], 0, 0, 0);
-                acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, a1), b1, acc[t], 0, 0, 0);
+                a0[t] = *reinterpret_cast<const u32x4*>(ap);
+                a1[t] = *reinterpret_cast<const u32x4*>(ap + 16);
             }
+#pragma unroll
+            for (int t = 0; t < MT; ++t)
+                acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, a0[t]), b0, acc[t], 0, 0, 0);
+#pragma unroll
+            for (int t = 0; t < MT; ++t)
+                acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, a1[t]), b1, acc[t], 0, 0, 0);
         }
         __builtin_amdgcn_wave_barrier();
     };
