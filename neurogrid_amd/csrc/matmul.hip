@@ -53,7 +53,7 @@ namespace {
 typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 
-constexpr int kChunk = 64;          // k per wave step
+constexpr int kChunk = 64;          // K granularity of the MFMA kernels (one 16x16x32 MFMA pair per lane group)
 constexpr int kMaxFusedM = 128;     // rows of A the weight-streaming path takes
 
 // Two int8 codes (bytes SEL0 and SEL1 of one dword) -> two exact fp16 values.
