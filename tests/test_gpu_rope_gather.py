@@ -96,8 +96,12 @@ def test_rope_position_zero_identity(lib):
     assert_bits_equal(got, x, "identity")
 
 
+# Kernel shapes covered: four rows per wave (T >= 4096, H <= 4096) with 2, 4 and
+# 8 vectors per lane and a ragged last wave; one row per wave with 2, 4, 8 and
+# 10 vectors per lane; rows of more than 5120 elements (chunked); H % 8 != 0.
 @pytest.mark.parametrize("V,H,T", [(32000, 4096, 4096), (100, 128, 1), (1000, 2048, 7), (50, 4100, 9),
-                                   (131072, 5120, 64)])
+                                   (131072, 5120, 64), (1000, 256, 4096), (1000, 1024, 4099),
+                                   (500, 2048, 4097), (300, 4096, 100), (64, 8192, 33)])
 def test_gather_bit_exact(lib, ora, V, H, T):
     banner(f"gather V={V} H={H} T={T}")
     table = RNG.integers(0, 65536, (V, H)).astype(np.uint16)
@@ -120,6 +124,28 @@ def test_gather_checked_zero_fills_bad_ids(lib):
     for i, t in enumerate(ids):
         want = table[t] if 0 <= t < V else np.zeros(H, np.uint16)
         assert_bits_equal(got[i], want, f"row {i}")
+
+
+@pytest.mark.parametrize("T", [4101, 37])
+def test_gather_checked_rows_per_wave(lib, T):
+    """The checked gather with four rows per wave (T >= 4096, ragged last wave)
+    and with one: bad ids anywhere, including the last rows, are zero-filled
+    and counted."""
+    banner(f"gather checked T={T}")
+    V, H = 700, 1024
+    table = RNG.integers(0, 65536, (V, H)).astype(np.uint16)
+    ids = RNG.integers(0, V, T).astype(np.int32)
+    bad_at = np.unique(np.concatenate([RNG.choice(T, min(T, 40), replace=False), [0, T - 1]]))
+    ids[bad_at] = np.where(np.arange(bad_at.size) % 2 == 0, -3, V + 11)
+    tb, ib, ob = dev(table), dev(ids), empty(2 * T * H)
+    eb = dev(np.zeros(1, np.int32))
+    ok(lib.ng_gather_embeddings_checked(ob.vp, tb.vp, ib.ip, H, T, V, eb.ip), "gather checked")
+    got = get(ob, np.uint16, (T, H))
+    assert get(eb, np.int32, (1,))[0] == bad_at.size
+    valid = (ids >= 0) & (ids < V)
+    want = np.zeros((T, H), np.uint16)
+    want[valid] = table[ids[valid]]
+    assert_bits_equal(got, want, "checked gather")
 
 
 QK_CASES = [
