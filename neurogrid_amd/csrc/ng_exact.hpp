@@ -6,17 +6,18 @@
 // the GPU result match a sequential CPU oracle bit for bit.
 //
 // Fast path. Every v_i is an fp32 value with at most 24 significant bits, so
-// v_i^2 is exact in fp64. The squares are summed in fp64, in any order
-// (per-lane accumulators, then across lanes and waves). A sum of m
-// nonnegative terms computed in any order differs from the exact sum by at
-// most (m-1) u / (1 - (m-1) u) of it, u = 2^-53. With k = ceil(log2 m) + 1,
-// the interval S (1 +- 2^(k-53)) therefore contains the exact sum; when both
-// of its ends round to the same fp32 value, that value is RN_f32(exact sum).
-// Otherwise (a fraction of about 2^(k-29) of rows: the interval is
-// 2^(k-52) S wide, fp32 values are about 2^-23 S apart; 2^-16 for a row of
-// 4096) the slow path runs. The row kernel of the element-wise fallback still
-// combines lanes with error-free transformations (two_sum), which keeps the
-// same bound.
+// v_i^2 is exact in fp64. The squares are summed in fp64 (per-lane
+// accumulators, then across lanes and waves). A sum of nonnegative terms
+// computed by a summation tree in which no term passes through more than h
+// rounded additions differs from the exact sum by at most h u / (1 - h u) of
+// it, u = 2^-53 (Higham, Accuracy and Stability of Numerical Algorithms,
+// 4.2); callers pass m > h. Where the lanes' partial sums are combined with
+// error-free transformations (two_sum), h is that of one lane accumulator.
+// With k = ceil(log2 m) + 1, the interval S (1 +- 2^(k-53)) contains the
+// exact sum; when both of its ends round to the same fp32 value, that value
+// is RN_f32(exact sum). Otherwise (a fraction of about 2^(k-29) of rows: the
+// interval is 2^(k-52) S wide, fp32 values are about 2^-23 S apart; 2^-23
+// for a row of 4096 held by one wave) the slow path runs.
 //
 // Slow path. A value v on the 2^-24 grid with |v| < 2^17 (every value derived
 // from fp16 inputs) has v^2 = t 2^16 + u 2^-16 + w 2^-48 with integers
@@ -72,9 +73,9 @@ __device__ __forceinline__ DD wave_sum_dd(DD v) {
     return dd_add(dd_add(readlane_dd(v, 0), readlane_dd(v, 16)), dd_add(readlane_dd(v, 32), readlane_dd(v, 48)));
 }
 
-// Resolve the fp64 sum S of m nonnegative terms (error below (m-1) 2^-53 S
-// up to a factor 1 + 2^-40) to RN_f32(exact), or report that the slow path is
-// needed.
+// Resolve the fp64 sum S of nonnegative terms (tree height below m, so the
+// error is below (m-1) 2^-53 S up to a factor 1 + 2^-40) to RN_f32(exact),
+// or report that the slow path is needed.
 __device__ __forceinline__ bool ss_fast_resolve(double S, int m, float& ss) {
     ss = static_cast<float>(S);
     if (!__builtin_isfinite(S)) return true;

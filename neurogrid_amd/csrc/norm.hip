@@ -138,11 +138,11 @@ __global__ __launch_bounds__(MaxThreads<V>::value) void row_kernel(RowArgs a) {
         // converts again instead of holding 8 V unpacked floats.
 #pragma unroll
         for (int k = 0; k < V; ++k) __asm__("" : "+v"(ov[k]));
-        // S sums the nthr * V * 8 squares (padding included) in fp64. Plain
-        // RMSNorm combines them with error-free transformations instead: the
-        // bound is then tighter, and the extra arithmetic before its first
-        // store makes it faster (measured on MI355X at T = H = 4096: 11.0 vs
-        // 11.45 us); the other variants are faster without it.
+        // S sums the squares in fp64. Plain RMSNorm combines the lanes' and
+        // waves' partial sums with error-free transformations: the extra
+        // arithmetic before its first store makes it faster (measured on
+        // MI355X at T = H = 4096: 11.0 vs 11.45 us); the other variants are
+        // faster without it.
         double S;
         if constexpr (kWeightsLate) {
             DD D2 = wave_sum_dd(dd_add(two_sum(acc[0], acc[1]), two_sum(acc[2], acc[3])));
@@ -165,8 +165,12 @@ __global__ __launch_bounds__(MaxThreads<V>::value) void row_kernel(RowArgs a) {
                 for (int j = 1; j < nw; ++j) S += s_part[j][0];
             }
         }
+        // Error bound: with the error-free combination, that of one lane
+        // accumulator (2 V terms); otherwise the height of the summation tree
+        // (2 V terms per accumulator, 2 to join the four, 6 across the wave,
+        // nw - 1 across waves).
         float ss;
-        if (!ss_fast_resolve(S, nthr * V * 8, ss)) {
+        if (!ss_fast_resolve(S, kWeightsLate ? 2 * V : 2 * V + 8 + nw, ss)) {
             // Exact path (identical decision in every thread of the row). It
             // re-reads the row: nothing has been stored yet, so in-place
             // calls still see their inputs, and the registers above stay free.
@@ -359,7 +363,8 @@ __global__ __launch_bounds__(64) void add_rms_rows_kernel(RowArgs a, int rows) {
         }
         const double S = wave_sum_f64_dpp((acc[0] + acc[1]) + (acc[2] + acc[3]));
         float ss;
-        if (!ss_fast_resolve(S, kWave * V * 8, ss)) exact_row_ss_wave<T, true>(X + off, RS + off, a.nvec, lane, ss);
+        // Summation tree height: 2 V per accumulator, 2 to join them, 6 across the wave.
+        if (!ss_fast_resolve(S, 2 * V + 8, ss)) exact_row_ss_wave<T, true>(X + off, RS + off, a.nvec, lane, ss);
         const float r = 1.0f / __builtin_sqrtf(ss / static_cast<float>(a.H) + a.eps);
         uint16_t* ro = static_cast<uint16_t*>(a.res_out) + off;
         uint16_t* yr = static_cast<uint16_t*>(a.y) + off;

@@ -179,7 +179,8 @@ __device__ __forceinline__ void head_rmsnorm(u32x4 (&x)[NV], const u32x4 (&w)[NV
         }
     const double S = group_sum_f64((acc[0] + acc[1]) + (acc[2] + acc[3]), lph);
     float ss;
-    if (!ss_fast_resolve(S, lph * NV * 8, ss)) {
+    // Summation tree height: 2 NV per accumulator, 2 to join them, log2(lph) <= 5 across the head's lanes.
+    if (!ss_fast_resolve(S, 2 * NV + 8, ss)) {
         // Exact path for this head (the whole lane group takes it together).
         Limbs Lm{0.0, 0.0, 0.0, 0};
 #pragma unroll
