@@ -311,9 +311,11 @@ int launch_gemv(uint16_t* c, const uint16_t* a, const int8_t* b, const float* sc
 // ---- split-K variant --------------------------------------------------------
 // For more than a few rows of A the kernel above reads A from L2 once per
 // 16 rows of B: at M = 64 that is 8 bytes of A per weight byte. Here a block
-// of kSplitWaves waves owns 16 * kSplitWaves rows of B and one of S slices of
-// K; the A columns of each 128-k batch are staged once in LDS and shared by
-// the block's waves (2M / (16 * kSplitWaves) bytes of A per weight byte).
+// of W waves owns 16 W rows of B and one of S slices of K; the A columns of
+// each 128-k batch are staged once in LDS and shared by the block's waves
+// (2M / (16 W) bytes of A per weight byte). W = 4, or 8 for K >= 8192 (the
+// down projection: 22.5 vs 25.2 us at M = 64, 34.5 vs 40.1 us at M = 128;
+// 8 waves were slower at K = 4096, and 2 slower everywhere but N = 1024).
 //
 // B is read in whole 128-byte lines: each load instruction of a wave covers
 // 8 rows x 128 codes (8 lanes per row), two instructions a wave's 16 rows.
@@ -328,11 +330,10 @@ int launch_gemv(uint16_t* c, const uint16_t* a, const int8_t* b, const float* sc
 // depend on timing. (Having the last block of each tile add them instead needs
 // an agent-scope release and acquire per block, which on MI355X write back and
 // invalidate the whole L2: measured 3-5x slower.)
-constexpr int kSplitWaves = 4;
 constexpr int kBatch = 128;  // k per batch
 
-template <int MT>
-__global__ __launch_bounds__(kSplitWaves * kWave) void gemm_i8w_split_kernel(
+template <int MT, int W>
+__global__ __launch_bounds__(W * kWave) void gemm_i8w_split_kernel(
     uint16_t* __restrict__ c, const uint16_t* __restrict__ a, const int8_t* __restrict__ b,
     const float* __restrict__ scale, float* __restrict__ part, int M, int N, int K, int S, int tiles, int cps) {
     // One row of a batch of A in LDS, padded by 32 bytes: measured on MI355X,
@@ -340,10 +341,10 @@ __global__ __launch_bounds__(kSplitWaves * kWave) void gemm_i8w_split_kernel(
     // (none: 1.6-1.8x slower; 48-96 bytes: no better at M = 64, slower at 128).
     constexpr int kRowBytes = kBatch * 2 + 32;
     constexpr int kPieces = 16 * MT * 16;       // 16-byte pieces of A per batch
-    constexpr int kThreads = kSplitWaves * kWave;
+    constexpr int kThreads = W * kWave;
     static_assert(kPieces % kThreads == 0, "A pieces must divide among the threads");
     __shared__ __align__(16) uint8_t lds_a[2][16 * MT * kRowBytes];
-    __shared__ __align__(16) u32x4 lds_b[kSplitWaves][2 * kWave];
+    __shared__ __align__(16) u32x4 lds_b[W][2 * kWave];
 
     const int sl = blockIdx.x % S;
     const int tile = blockIdx.x / S;
@@ -357,7 +358,7 @@ __global__ __launch_bounds__(kSplitWaves * kWave) void gemm_i8w_split_kernel(
     const bool half_last = (K % kBatch) != 0;
     const int c0 = sl * cps;
     const int c1 = min(c0 + cps, nbatch);
-    const int nw = tile * (16 * kSplitWaves) + 16 * wave;  // first row of B of this wave
+    const int nw = tile * (16 * W) + 16 * wave;  // first row of B of this wave
     const int n = nw + col;                                 // row of B this lane multiplies
 
     // Row and piece this lane loads in each of the two B instructions.
@@ -671,9 +672,9 @@ int gemm_lt(void* c, const void* a, const void* b, const void* q, const void* sc
     return 0;
 }
 
-template <int MT>
+template <int MT, int W>
 int launch_split(uint16_t* c, const uint16_t* a, const int8_t* b, const float* scale, int M, int N, int K) {
-    const int tiles = (N + 16 * kSplitWaves - 1) / (16 * kSplitWaves);
+    const int tiles = (N + 16 * W - 1) / (16 * W);
     const int nbatch = (K + kBatch - 1) / kBatch;
     // Enough slices of K for about 256 blocks (512 for K >= 8192), at most 8,
     // each of at least two batches, none empty.
@@ -697,7 +698,7 @@ int launch_split(uint16_t* c, const uint16_t* a, const int8_t* b, const float* s
             return -1;
         part = static_cast<float*>(sb->part);
     }
-    gemm_i8w_split_kernel<MT><<<dim3(static_cast<unsigned>(tiles * S)), dim3(kSplitWaves * kWave), 0, s>>>(
+    gemm_i8w_split_kernel<MT, W><<<dim3(static_cast<unsigned>(tiles * S)), dim3(W * kWave), 0, s>>>(
         c, a, b, scale, part, M, N, K, S, tiles, cps);
     NG_CHECK_LAUNCH("cuda_gemm_int8");
     if (S > 1) {
@@ -730,10 +731,14 @@ int gemm_i8w(void* c, const void* a, const void* b, const void* scale, int M, in
         if (M == 2) return launch_gemv<2, 8>(cp, ap, bp, sp, M, N, K);
         return launch_gemv<4, 4>(cp, ap, bp, sp, M, N, K);
     }
-    if (M > 64) return launch_split<8>(cp, ap, bp, sp, M, N, K);
-    if (M > 32) return launch_split<4>(cp, ap, bp, sp, M, N, K);
-    if (M > 16) return launch_split<2>(cp, ap, bp, sp, M, N, K);
-    if (big) return launch_split<1>(cp, ap, bp, sp, M, N, K);
+    const bool deep = K >= 8192;
+    if (M > 64)
+        return deep ? launch_split<8, 8>(cp, ap, bp, sp, M, N, K) : launch_split<8, 4>(cp, ap, bp, sp, M, N, K);
+    if (M > 32)
+        return deep ? launch_split<4, 8>(cp, ap, bp, sp, M, N, K) : launch_split<4, 4>(cp, ap, bp, sp, M, N, K);
+    if (M > 16)
+        return deep ? launch_split<2, 8>(cp, ap, bp, sp, M, N, K) : launch_split<2, 4>(cp, ap, bp, sp, M, N, K);
+    if (big) return launch_split<1, 4>(cp, ap, bp, sp, M, N, K);
     return launch_i8w<1, 1, 8, 4>(cp, ap, bp, sp, M, N, K);
 }
 

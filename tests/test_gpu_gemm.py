@@ -86,8 +86,9 @@ def assert_within_bound(got_bits, a, q, scale, tb: bool, what: str, ora) -> None
 # M, K, N: the weight-streaming path takes transpose_b, M <= 128 and K % 64 == 0
 # (K % 16 == 0 for M <= 4). M <= 4 runs the GEMV kernel (K in 1024-code
 # segments, the last one possibly partial); M > 16, and 4 < M <= 16 with K or
-# N >= 8192, the split-K kernel with 1 to 8 slices of K; 4 < M <= 16 otherwise
-# the MFMA kernel that reads A from L2.
+# N >= 8192, the split-K kernel with 1 to 8 slices of K (4 waves per block, 8
+# for K >= 8192 and M > 16); 4 < M <= 16 otherwise the MFMA kernel that reads
+# A from L2.
 FUSED = [
     (1, 4096, 4096), (3, 4096, 1024), (16, 4096, 4096), (17, 4096, 1000), (32, 1024, 512), (33, 4096, 4096),
     (64, 4096, 4096), (64, 4096, 1024), (8, 14336, 4096), (64, 14336, 4096), (5, 64, 16), (2, 128, 7),
@@ -95,6 +96,8 @@ FUSED = [
     (2, 256, 9000), (48, 4096, 1024), (65, 4096, 1024), (96, 4096, 4096), (128, 14336, 4096), (100, 1024, 300),
     (7, 8192, 64), (128, 64, 64), (4, 4096, 4096), (1, 1040, 100), (4, 2064, 33), (2, 14352, 64),
     (3, 16, 5), (12, 1024, 4096),
+    # K >= 8192 with M > 16: eight waves per block in the split kernel (one case with K % 128 == 64)
+    (24, 8192, 1000), (100, 8256, 384), (48, 9216, 2048),
 ]
 
 
