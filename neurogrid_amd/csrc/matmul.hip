@@ -361,14 +361,28 @@ __global__ __launch_bounds__(W * kWave) void gemm_i8w_split_kernel(
     const int nw = tile * (16 * W) + 16 * wave;  // first row of B of this wave
     const int n = nw + col;                                 // row of B this lane multiplies
 
-    // Row and piece this lane loads in each of the two B instructions.
-    const int8_t* brow[2];
+    // A and B are read with buffer loads: B from this wave's first row (rows
+    // past N clamp to the last one), A from its start, so that per-load
+    // offsets are 32-bit instead of 64-bit addresses (2-6% faster at
+    // M = 64-128). Offsets are below 16 K bytes for B and 2 M K bytes for A.
+    const int nbase = min(nw, N - 1);
+    const __amdgpu_buffer_rsrc_t rb = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<int8_t*>(b + static_cast<size_t>(nbase) * K), 0, 0x7fffffff, 0x00020000);
+    const __amdgpu_buffer_rsrc_t ra = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(a), 0, 0x7fffffff,
+                                                                        0x00020000);
+    uint32_t boff[2];
     int bpiece[2];
 #pragma unroll
     for (int j = 0; j < 2; ++j) {
         const int r = 8 * j + (lane >> 3);
         bpiece[j] = ((lane & 7) - (r >> 1)) & 7;
-        brow[j] = b + static_cast<size_t>(min(nw + r, N - 1)) * K;
+        boff[j] = static_cast<uint32_t>((min(nw + r, N - 1) - nbase) * K);
+    }
+    uint32_t aoff[kPieces / kThreads];
+#pragma unroll
+    for (int j = 0; j < kPieces / kThreads; ++j) {
+        const int pc = j * kThreads + tid;
+        aoff[j] = static_cast<uint32_t>(min(pc / 16, M - 1) * K * 2);
     }
 
     f32x4 acc[MT];
@@ -393,7 +407,7 @@ __global__ __launch_bounds__(W * kWave) void gemm_i8w_split_kernel(
             const int row = pc / 16;
             int q = pc % 16;
             if (half) q &= 7;  // k past K: load the batch's first 64 k again
-            ar[j] = ld16(a + static_cast<size_t>(min(row, M - 1)) * K + kb + 8 * q);
+            ar[j] = __builtin_amdgcn_raw_buffer_load_b128(ra, aoff[j] + static_cast<uint32_t>((kb + 8 * q) * 2), 0, 0);
         }
         __builtin_amdgcn_sched_barrier(0);  // keep A's loads ahead of B's
         // Pieces 4-7 of a half batch would lie past K: they load pieces 0-3
@@ -401,7 +415,7 @@ __global__ __launch_bounds__(W * kWave) void gemm_i8w_split_kernel(
 #pragma unroll
         for (int j = 0; j < 2; ++j) {
             const int pcs = half ? (bpiece[j] & 3) : bpiece[j];
-            bv[j] = ld16_stream(brow[j] + kb + 16 * pcs);
+            bv[j] = __builtin_amdgcn_raw_buffer_load_b128(rb, boff[j] + static_cast<uint32_t>(kb + 16 * pcs), 0, 2);
         }
     };
     auto stage = [&](int buf, const u32x4 (&ar)[kP]) {
