@@ -109,7 +109,7 @@ __global__ __launch_bounds__(WAVES * kWave) void gemm_i8w_kernel(uint16_t* __res
 #pragma unroll
     for (int j = 0; j < 2; ++j) {
         const int r = 8 * j + (lane >> 3);
-        bpiece[j] = ((lane & 7) - (r >> 1)) & 7;
+        bpiece[j] = (lane & 7) ^ (r >> 1);
         brow[j] = b + static_cast<size_t>(min(n0 + r, N - 1)) * K;
     }
     const uint16_t* ap[MT];
@@ -151,7 +151,7 @@ __global__ __launch_bounds__(WAVES * kWave) void gemm_i8w_kernel(uint16_t* __res
 #pragma unroll
             for (int st = 0; st < 2; ++st) {
                 const int p = 4 * st + grp;
-                u32x4 v = lds_b[wave][8 * col + ((p + (col >> 1)) & 7)];
+                u32x4 v = lds_b[wave][8 * col + (p ^ (col >> 1))];
                 if (past || (half && st == 1)) v = u32x4{0u, 0u, 0u, 0u};
                 f16x8 b0, b1;
                 codes16_to_operands(v, b0, b1);
@@ -322,8 +322,12 @@ int launch_gemv(uint16_t* c, const uint16_t* a, const int8_t* b, const float* sc
 // Loading B straight into the MFMA layout instead (4 lanes per row, 64 bytes
 // per row per instruction) streams about 25% slower on MI355X. The codes
 // reach the MFMA layout through a per-wave LDS buffer: piece p (16 codes) of
-// row r sits in slot 8r + ((p + r / 2) mod 8), so the writes are contiguous
-// and the 16 rows read by one lane group fall in 16 different bank groups.
+// row r sits in slot 8r + (p xor r / 2), so the writes are contiguous and the
+// reads conflict-free. (LDS on MI355X serves 256 bytes per clock from 64
+// banks. Measured with access-pattern probes, 16-byte reads are conflict-free
+// when the rows 0-7 of one lane group and the rows 8-15 of another fall in
+// opposite halves of the banks; (p + r / 2) mod 8 breaks that and took two
+// clocks per 16 lanes.)
 //
 // With S > 1 each block stores its fp32 partial sums in `part` [S][M][N] and a
 // second kernel adds the S slices in slice order, so the result does not
@@ -336,10 +340,11 @@ template <int MT, int W>
 __global__ __launch_bounds__(W * kWave) void gemm_i8w_split_kernel(
     uint16_t* __restrict__ c, const uint16_t* __restrict__ a, const int8_t* __restrict__ b,
     const float* __restrict__ scale, float* __restrict__ part, int M, int N, int K, int S, int tiles, int cps) {
-    // One row of a batch of A in LDS, padded by 32 bytes: measured on MI355X,
-    // 16 bytes of padding leave bank conflicts that cost 3-6% at M = 64-128
-    // (none: 1.6-1.8x slower; 48-96 bytes: no better at M = 64, slower at 128).
-    constexpr int kRowBytes = kBatch * 2 + 32;
+    // A batch of A in LDS: 256 bytes per row, 16-byte piece q of row m stored
+    // at piece q xor (m mod 16). The MFMA reads (16 rows, one piece each per
+    // lane group) are then conflict-free; padded rows (16, 32 or 64 bytes)
+    // leave two-way conflicts, unpadded unswizzled rows eight-way ones.
+    constexpr int kRowBytes = kBatch * 2;
     constexpr int kPieces = 16 * MT * 16;       // 16-byte pieces of A per batch
     constexpr int kThreads = W * kWave;
     static_assert(kPieces % kThreads == 0, "A pieces must divide among the threads");
@@ -375,7 +380,7 @@ __global__ __launch_bounds__(W * kWave) void gemm_i8w_split_kernel(
 #pragma unroll
     for (int j = 0; j < 2; ++j) {
         const int r = 8 * j + (lane >> 3);
-        bpiece[j] = ((lane & 7) - (r >> 1)) & 7;
+        bpiece[j] = (lane & 7) ^ (r >> 1);
         boff[j] = static_cast<uint32_t>((min(nw + r, N - 1) - nbase) * K);
     }
     uint32_t aoff[kPieces / kThreads];
@@ -422,7 +427,8 @@ __global__ __launch_bounds__(W * kWave) void gemm_i8w_split_kernel(
 #pragma unroll
         for (int j = 0; j < kP; ++j) {
             const int pc = j * kThreads + tid;
-            *reinterpret_cast<u32x4*>(lds_a[buf] + (pc / 16) * kRowBytes + 16 * (pc % 16)) = ar[j];
+            const int row = pc / 16;
+            *reinterpret_cast<u32x4*>(lds_a[buf] + row * kRowBytes + 16 * ((pc % 16) ^ (row & 15))) = ar[j];
         }
     };
     auto multiply = [&](int buf, const u32x4 (&bv)[2], int cb) {
@@ -437,7 +443,7 @@ __global__ __launch_bounds__(W * kWave) void gemm_i8w_split_kernel(
 #pragma unroll
         for (int st = 0; st < 2; ++st) {
             const int p = 4 * st + grp;
-            u32x4 v = lds_b[wave][8 * col + ((p + (col >> 1)) & 7)];
+            u32x4 v = lds_b[wave][8 * col + (p ^ (col >> 1))];
             if (past || (half && st == 1)) v = u32x4{0u, 0u, 0u, 0u};
             f16x8 b0, b1;
             codes16_to_operands(v, b0, b1);
@@ -446,9 +452,10 @@ __global__ __launch_bounds__(W * kWave) void gemm_i8w_split_kernel(
             u32x4 a0[MT], a1[MT];
 #pragma unroll
             for (int t = 0; t < MT; ++t) {
-                const uint8_t* ap = lds_a[buf] + (16 * t + col) * kRowBytes + st * 128 + 32 * grp;
-                a0[t] = *reinterpret_cast<const u32x4*>(ap);
-                a1[t] = *reinterpret_cast<const u32x4*>(ap + 16);
+                // pieces 8 st + 2 grp and the next one of row 16 t + col
+                const uint8_t* ap = lds_a[buf] + (16 * t + col) * kRowBytes;
+                a0[t] = *reinterpret_cast<const u32x4*>(ap + 16 * ((8 * st + 2 * grp) ^ col));
+                a1[t] = *reinterpret_cast<const u32x4*>(ap + 16 * ((8 * st + 2 * grp + 1) ^ col));
             }
 #pragma unroll
             for (int t = 0; t < MT; ++t)
