@@ -329,15 +329,21 @@ int launch_gemv(uint16_t* c, const uint16_t* a, const int8_t* b, const float* sc
 // opposite halves of the banks; (p + r / 2) mod 8 breaks that and took two
 // clocks per 16 lanes.)
 //
-// With S > 1 each block stores its fp32 partial sums in `part` [S][M][N] and a
-// second kernel adds the S slices in slice order, so the result does not
-// depend on timing. (Having the last block of each tile add them instead needs
-// an agent-scope release and acquire per block, which on MI355X write back and
-// invalidate the whole L2: measured 3-5x slower.)
+// K is divided among blocks and inside them. The G groups of W waves of a
+// block take turns of G consecutive batches (group g the batch g of each
+// turn), each group with its own LDS copy of its batch of A; at the end the
+// groups' sums are added through LDS in group order. With S > 1 each block
+// stores those sums in `part` [S][M][N] and a second kernel adds the S slices
+// in slice order. Either way the result does not depend on timing. (Having
+// the last block of each tile add the slices instead needs an agent-scope
+// release and acquire per block, which on MI355X write back and invalidate
+// the whole L2: measured 3-5x slower.) Groups inside the block replace slices
+// where there are enough tiles to fill the GPU with one slice: no partial
+// sums in memory and no second launch.
 constexpr int kBatch = 128;  // k per batch
 
-template <int MT, int W>
-__global__ __launch_bounds__(W * kWave) void gemm_i8w_split_kernel(
+template <int MT, int W, int G>
+__global__ __launch_bounds__(G * W * kWave) void gemm_i8w_split_kernel(
     uint16_t* __restrict__ c, const uint16_t* __restrict__ a, const int8_t* __restrict__ b,
     const float* __restrict__ scale, float* __restrict__ part, int M, int N, int K, int S, int tiles, int cps) {
     // A batch of A in LDS: 256 bytes per row, 16-byte piece q of row m stored
@@ -346,10 +352,12 @@ __global__ __launch_bounds__(W * kWave) void gemm_i8w_split_kernel(
     // leave two-way conflicts, unpadded unswizzled rows eight-way ones.
     constexpr int kRowBytes = kBatch * 2;
     constexpr int kPieces = 16 * MT * 16;       // 16-byte pieces of A per batch
-    constexpr int kThreads = W * kWave;
-    static_assert(kPieces % kThreads == 0, "A pieces must divide among the threads");
-    __shared__ __align__(16) uint8_t lds_a[2][16 * MT * kRowBytes];
-    __shared__ __align__(16) u32x4 lds_b[W][2 * kWave];
+    constexpr int kThreads = G * W * kWave;
+    static_assert((G * kPieces) % kThreads == 0, "A pieces must divide among the threads");
+    static_assert(G == 1 || (G - 1) * W * MT * kWave * 16 <= 2 * G * 16 * MT * kRowBytes,
+                  "the groups' sums must fit in the A buffers");
+    __shared__ __align__(16) uint8_t lds_a[2][G][16 * MT * kRowBytes];
+    __shared__ __align__(16) u32x4 lds_b[G * W][2 * kWave];
 
     const int sl = blockIdx.x % S;
     const int tile = blockIdx.x / S;
@@ -357,13 +365,15 @@ __global__ __launch_bounds__(W * kWave) void gemm_i8w_split_kernel(
     const int tid = threadIdx.x;
     const int lane = tid & (kWave - 1);
     const int wave = __builtin_amdgcn_readfirstlane(tid / kWave);
+    const int kg = wave / W;   // this wave's group: batch kg of each turn
+    const int wv = wave % W;   // and its tile of 16 rows of B
     const int col = lane & 15;
     const int grp = lane >> 4;
     const int nbatch = (K + kBatch - 1) / kBatch;  // the last batch holds 64 k when K % 128 == 64
     const bool half_last = (K % kBatch) != 0;
     const int c0 = sl * cps;
     const int c1 = min(c0 + cps, nbatch);
-    const int nw = tile * (16 * W) + 16 * wave;  // first row of B of this wave
+    const int nw = tile * (16 * W) + 16 * wv;  // first row of B of this wave
     const int n = nw + col;                                 // row of B this lane multiplies
 
     // A and B are read with buffer loads: B from this wave's first row (rows
@@ -383,10 +393,11 @@ __global__ __launch_bounds__(W * kWave) void gemm_i8w_split_kernel(
         bpiece[j] = (lane & 7) ^ (r >> 1);
         boff[j] = static_cast<uint32_t>((min(nw + r, N - 1) - nbase) * K);
     }
-    uint32_t aoff[kPieces / kThreads];
+    constexpr int kP = G * kPieces / kThreads;
+    uint32_t aoff[kP];
 #pragma unroll
-    for (int j = 0; j < kPieces / kThreads; ++j) {
-        const int pc = j * kThreads + tid;
+    for (int j = 0; j < kP; ++j) {
+        const int pc = (j * kThreads + tid) % kPieces;
         aoff[j] = static_cast<uint32_t>(min(pc / 16, M - 1) * K * 2);
     }
 
@@ -394,29 +405,30 @@ __global__ __launch_bounds__(W * kWave) void gemm_i8w_split_kernel(
 #pragma unroll
     for (int i = 0; i < MT; ++i) acc[i] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
 
-    // Batches, two in flight: the loads of batch i + 1 (B into registers, A
-    // into registers on their way to LDS) are issued before batch i is
+    // Turns, two in flight: the loads of turn i + 1 (B into registers, A
+    // into registers on their way to LDS) are issued before turn i is
     // multiplied; A alternates between two LDS buffers, so one barrier per
-    // batch separates a buffer's writes from its reads and from its reuse two
-    // batches later.
-    constexpr int kP = kPieces / kThreads;
-    // A first: staging it into LDS then waits only for A, not for B. Batches
-    // past the slice (one past the last is loaded too, to keep every load
-    // unconditional) are clamped to its last batch.
-    auto load = [&](u32x4 (&bv)[2], u32x4 (&ar)[kP], int cb) {
-        const bool half = half_last && cb == nbatch - 1;
-        const size_t kb = static_cast<size_t>(cb) * kBatch;
+    // turn separates a buffer's writes from its reads and from its reuse two
+    // turns later. A turn starting at batch `first` holds batches first ..
+    // first + G - 1; those past the slice load its last batch (every load
+    // stays unconditional) and multiply zero codes.
+    // A first: staging it into LDS then waits only for A, not for B.
+    auto load = [&](u32x4 (&bv)[2], u32x4 (&ar)[kP], int first) {
 #pragma unroll
         for (int j = 0; j < kP; ++j) {
             const int pc = j * kThreads + tid;
-            const int row = pc / 16;
+            const int cb = min(first + pc / kPieces, c1 - 1);
+            const size_t kb = static_cast<size_t>(cb) * kBatch;
             int q = pc % 16;
-            if (half) q &= 7;  // k past K: load the batch's first 64 k again
+            if (half_last && cb == nbatch - 1) q &= 7;  // k past K: load the batch's first 64 k again
             ar[j] = __builtin_amdgcn_raw_buffer_load_b128(ra, aoff[j] + static_cast<uint32_t>((kb + 8 * q) * 2), 0, 0);
         }
         __builtin_amdgcn_sched_barrier(0);  // keep A's loads ahead of B's
         // Pieces 4-7 of a half batch would lie past K: they load pieces 0-3
         // again (and multiply zero codes).
+        const int cb = min(first + kg, c1 - 1);
+        const bool half = half_last && cb == nbatch - 1;
+        const size_t kb = static_cast<size_t>(cb) * kBatch;
 #pragma unroll
         for (int j = 0; j < 2; ++j) {
             const int pcs = half ? (bpiece[j] & 3) : bpiece[j];
@@ -427,17 +439,19 @@ __global__ __launch_bounds__(W * kWave) void gemm_i8w_split_kernel(
 #pragma unroll
         for (int j = 0; j < kP; ++j) {
             const int pc = j * kThreads + tid;
-            const int row = pc / 16;
-            *reinterpret_cast<u32x4*>(lds_a[buf] + row * kRowBytes + 16 * ((pc % 16) ^ (row & 15))) = ar[j];
+            const int g = pc / kPieces;
+            const int row = (pc % kPieces) / 16;
+            *reinterpret_cast<u32x4*>(lds_a[buf][g] + row * kRowBytes + 16 * ((pc % 16) ^ (row & 15))) = ar[j];
         }
     };
-    auto multiply = [&](int buf, const u32x4 (&bv)[2], int cb) {
+    auto multiply = [&](int buf, const u32x4 (&bv)[2], int first) {
         // This wave's codes into the MFMA layout. LDS operations of one wave
         // complete in order, so the reads see the writes, and the next batch's
         // writes come after these reads.
         lds_b[wave][lane] = bv[0];
         lds_b[wave][kWave + lane] = bv[1];
         __builtin_amdgcn_wave_barrier();
+        const int cb = first + kg;
         const bool past = cb >= c1;                               // clamped batch: multiplies zero codes
         const bool half = half_last && cb == nbatch - 1;          // its second 64 k lie past K
 #pragma unroll
@@ -453,7 +467,7 @@ __global__ __launch_bounds__(W * kWave) void gemm_i8w_split_kernel(
 #pragma unroll
             for (int t = 0; t < MT; ++t) {
                 // pieces 8 st + 2 grp and the next one of row 16 t + col
-                const uint8_t* ap = lds_a[buf] + (16 * t + col) * kRowBytes;
+                const uint8_t* ap = lds_a[buf][kg] + (16 * t + col) * kRowBytes;
                 a0[t] = *reinterpret_cast<const u32x4*>(ap + 16 * ((8 * st + 2 * grp) ^ col));
                 a1[t] = *reinterpret_cast<const u32x4*>(ap + 16 * ((8 * st + 2 * grp + 1) ^ col));
             }
@@ -466,26 +480,43 @@ __global__ __launch_bounds__(W * kWave) void gemm_i8w_split_kernel(
         }
         __builtin_amdgcn_wave_barrier();
     };
-    // The batch count is rounded up to even: an extra batch past the slice
-    // multiplies zero codes. (Leaving the loop after an odd batch instead lets
-    // the compiler sink the next batch's loads below the multiply.)
-    const int nb = c1 - c0;
+    // The turn count is rounded up to even: an extra turn past the slice
+    // multiplies zero codes. (Leaving the loop after an odd turn instead lets
+    // the compiler sink the next turn's loads below the multiply.)
+    const int nt = (c1 - c0 + G - 1) / G;
     u32x4 bv0[2], bv1[2];
     u32x4 ar0[kP], ar1[kP];
     load(bv0, ar0, c0);
-    for (int i = 0; i < nb; i += 2) {
+    for (int i = 0; i < nt; i += 2) {
         stage(0, ar0);
         __syncthreads();
-        load(bv1, ar1, min(c0 + i + 1, c1 - 1));
+        load(bv1, ar1, c0 + G * (i + 1));
         __builtin_amdgcn_sched_barrier(0);
-        multiply(0, bv0, c0 + i);
+        multiply(0, bv0, c0 + G * i);
         stage(1, ar1);
         __syncthreads();
-        load(bv0, ar0, min(c0 + i + 2, c1 - 1));
+        load(bv0, ar0, c0 + G * (i + 2));
         __builtin_amdgcn_sched_barrier(0);
-        multiply(1, bv1, c0 + i + 1);
+        multiply(1, bv1, c0 + G * (i + 1));
     }
 
+    if (G > 1) {
+        // Groups 1 .. G-1 hand their sums to group 0 through the A buffers
+        // (free once every wave has passed this barrier), which adds them in
+        // group order.
+        __syncthreads();
+        f32x4* red = reinterpret_cast<f32x4*>(&lds_a[0][0][0]);
+        if (kg > 0) {
+#pragma unroll
+            for (int t = 0; t < MT; ++t) red[(((kg - 1) * W + wv) * MT + t) * kWave + lane] = acc[t];
+        }
+        __syncthreads();
+        if (kg > 0) return;
+#pragma unroll
+        for (int g = 1; g < G; ++g)
+#pragma unroll
+            for (int t = 0; t < MT; ++t) acc[t] += red[(((g - 1) * W + wv) * MT + t) * kWave + lane];
+    }
     if (S == 1) {
         if (n < N) {
             const float sc = scale[n];
@@ -693,15 +724,16 @@ int gemm_lt(void* c, const void* a, const void* b, const void* q, const void* sc
     return 0;
 }
 
-template <int MT, int W>
+template <int MT, int W, int G>
 int launch_split(uint16_t* c, const uint16_t* a, const int8_t* b, const float* scale, int M, int N, int K) {
     const int tiles = (N + 16 * W - 1) / (16 * W);
     const int nbatch = (K + kBatch - 1) / kBatch;
-    // Enough slices of K for about 256 blocks (512 for K >= 8192), at most 8,
-    // each of at least two batches, none empty.
-    const int target = K >= 8192 ? 512 : 256;
+    // Enough slices of K for about 256 blocks (512 for K >= 8192; with groups
+    // in the block, 192 blocks of twice the waves), at most 8, each of at
+    // least two turns, none empty.
+    const int target = G > 1 ? 192 : K >= 8192 ? 512 : 256;
     int S = (target + tiles - 1) / tiles;
-    S = max(1, min(S, min(8, nbatch / 2)));
+    S = max(1, min(S, min(8, nbatch / (2 * G))));
     const int cps = (nbatch + S - 1) / S;
     S = (nbatch + cps - 1) / cps;
     // With S > 1 the partial-sum buffer is this stream's: the lock is held
@@ -719,7 +751,7 @@ int launch_split(uint16_t* c, const uint16_t* a, const int8_t* b, const float* s
             return -1;
         part = static_cast<float*>(sb->part);
     }
-    gemm_i8w_split_kernel<MT, W><<<dim3(static_cast<unsigned>(tiles * S)), dim3(W * kWave), 0, s>>>(
+    gemm_i8w_split_kernel<MT, W, G><<<dim3(static_cast<unsigned>(tiles * S)), dim3(G * W * kWave), 0, s>>>(
         c, a, b, scale, part, M, N, K, S, tiles, cps);
     NG_CHECK_LAUNCH("cuda_gemm_int8");
     if (S > 1) {
@@ -752,14 +784,25 @@ int gemm_i8w(void* c, const void* a, const void* b, const void* scale, int M, in
         if (M == 2) return launch_gemv<2, 8>(cp, ap, bp, sp, M, N, K);
         return launch_gemv<4, 4>(cp, ap, bp, sp, M, N, K);
     }
+    // K >= 8192 (down): 8 waves per block. N >= 12288 at smaller K (gate/up):
+    // 192 or more tiles of 64 rows fill the GPU with one slice of K, split
+    // between two groups of 4 waves per block.
     const bool deep = K >= 8192;
+    const bool wide = !deep && N >= 12288;
     if (M > 64)
-        return deep ? launch_split<8, 8>(cp, ap, bp, sp, M, N, K) : launch_split<8, 4>(cp, ap, bp, sp, M, N, K);
+        return deep ? launch_split<8, 8, 1>(cp, ap, bp, sp, M, N, K)
+               : wide ? launch_split<8, 4, 2>(cp, ap, bp, sp, M, N, K)
+                      : launch_split<8, 4, 1>(cp, ap, bp, sp, M, N, K);
     if (M > 32)
-        return deep ? launch_split<4, 8>(cp, ap, bp, sp, M, N, K) : launch_split<4, 4>(cp, ap, bp, sp, M, N, K);
+        return deep ? launch_split<4, 8, 1>(cp, ap, bp, sp, M, N, K)
+               : wide ? launch_split<4, 4, 2>(cp, ap, bp, sp, M, N, K)
+                      : launch_split<4, 4, 1>(cp, ap, bp, sp, M, N, K);
     if (M > 16)
-        return deep ? launch_split<2, 8>(cp, ap, bp, sp, M, N, K) : launch_split<2, 4>(cp, ap, bp, sp, M, N, K);
-    if (big) return launch_split<1, 4>(cp, ap, bp, sp, M, N, K);
+        return deep ? launch_split<2, 8, 1>(cp, ap, bp, sp, M, N, K)
+               : wide ? launch_split<2, 4, 2>(cp, ap, bp, sp, M, N, K)
+                      : launch_split<2, 4, 1>(cp, ap, bp, sp, M, N, K);
+    if (big)
+        return wide ? launch_split<1, 4, 2>(cp, ap, bp, sp, M, N, K) : launch_split<1, 4, 1>(cp, ap, bp, sp, M, N, K);
     return launch_i8w<1, 1, 8, 4>(cp, ap, bp, sp, M, N, K);
 }
 
