@@ -98,6 +98,8 @@ FUSED = [
     (3, 16, 5), (12, 1024, 4096),
     # K >= 8192 with M > 16: eight waves per block in the split kernel (one case with K % 128 == 64)
     (24, 8192, 1000), (100, 8256, 384), (48, 9216, 2048),
+    # M = 3, 4 with K or N >= 8192: the split kernel (two wave groups per block for N >= 12288 at K < 8192)
+    (4, 4096, 14336), (3, 4096, 12300), (3, 14336, 4096), (4, 14336, 100), (4, 8256, 200),
 ]
 
 
