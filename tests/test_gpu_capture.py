@@ -28,6 +28,7 @@ pytestmark = pytest.mark.gpu
 
 T, H, I, NQ, NKV, D, V = 24, 512, 1024, 4, 2, 128, 100
 GK, GN = 512, 256
+GNW = 12288  # wide N for the GEMM
 EPS, THETA = C.c_float(1e-5), C.c_float(1e6)
 
 
@@ -68,6 +69,8 @@ def inp():
     a["wq"] = rng.integers(-127, 128, (GN, GK)).astype(np.int8)
     a["wq_kn"] = rng.integers(-127, 128, (GK, GN)).astype(np.int8)
     a["wsc"] = rng.uniform(1e-3, 1e-2, GN).astype(np.float32)
+    a["wq_wide"] = rng.integers(-127, 128, (GNW, GK)).astype(np.int8)
+    a["wsc_wide"] = rng.uniform(1e-3, 1e-2, GNW).astype(np.float32)
     a["tsc"] = np.array([0.0125], np.float32)
     a["wh"] = f16_bits(n(GK, GN, s=0.05))
     for m in (1, 3, 16, 40, 64, 100, 200):
@@ -161,6 +164,9 @@ def _ops():
     for m in (1, 3, 16, 40, 64, 100):
         add(f"cuda_gemm_int8_M{m}", {"y": (E2, (m, GN))},
             lambda L, i, o, m=m: L.cuda_gemm_int8(o["y"].vp, i[f"a{m}"].vp, i["wq"].vp, i["wsc"].vp, m, GK, GN, True))
+    # N >= 12288: one slice of K, two wave groups per block
+    add("cuda_gemm_int8_M40_wide", {"y": (E2, (40, GNW))},
+        lambda L, i, o: L.cuda_gemm_int8(o["y"].vp, i["a40"].vp, i["wq_wide"].vp, i["wsc_wide"].vp, 40, GK, GNW, True))
     add("cuda_gemm_int8_M200_library", {"y": (E2, (200, GN))},
         lambda L, i, o: L.cuda_gemm_int8(o["y"].vp, i["a200"].vp, i["wq"].vp, i["wsc"].vp, 200, GK, GN, True), False)
     add("cuda_gemm_int8_kn_library", {"y": (E2, (16, GN))},
