@@ -16,13 +16,14 @@
 // fp16 first and sums those; the two differ by at most 2^-11 of
 // sum_k |A[m, k] * q[n, k] * scale[n]| plus the accumulation error.
 //
-// Three kernels, by M (see gemm_i8w):
-//   M <= 4         gemv_i8w_kernel: dot-product instructions, each load reads
-//                  1 KiB contiguous of one row of B;
-//   4 < M <= 16    gemm_i8w_kernel: matrix cores, A read from L2, waves
-//                  split K within the block;
-//   16 < M <= 128  gemm_i8w_split_kernel: matrix cores, A staged in LDS, K
-//                  split into slices whose sums a second kernel adds.
+// Three kernels, by M, K and N (see gemm_i8w):
+//   M <= 2, and M <= 4 with K, N < 8192: gemv_i8w_kernel, dot-product
+//       instructions, each load reads 1 KiB contiguous of one row of B;
+//   4 < M <= 16 with K, N < 8192: gemm_i8w_kernel, matrix cores, A read from
+//       L2, waves split K within the block;
+//   otherwise, up to M = 128: gemm_i8w_split_kernel, matrix cores, A staged
+//       in LDS, K split between wave groups of a block and between blocks
+//       (slices whose sums a second kernel adds).
 // MFMA layout: v_mfma_f32_16x16x32_f16 multiplies a 16 x 32 tile of A (rows
 // m) by a 32 x 16 tile of B^T (columns n). Lane l supplies row (l % 16) of
 // each operand and 8 values of k; the accumulator lane l holds rows
