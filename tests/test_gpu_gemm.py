@@ -102,6 +102,7 @@ FUSED = [
     (4, 4096, 14336), (3, 4096, 12300), (3, 14336, 4096), (4, 14336, 100), (4, 8256, 200),
     # N >= 12288 at K < 8192: two wave groups per block at every tile height, odd batch counts, a half batch
     (128, 4096, 14336), (80, 4160, 12288), (20, 1088, 13000), (33, 2048, 12290), (9, 192, 12288),
+    (3, 64, 12288), (4, 128, 12300), (70, 64, 12288),
 ]
 
 
