@@ -10,10 +10,11 @@
  *   - transpose_b, M <= 128, K % 64 == 0 (K % 16 == 0 for M <= 4), 16-byte
  *     aligned A and B: the int8 weights are read once, converted to fp16
  *     exactly in registers and multiplied with fp32 sums (dot-product
- *     instructions up to M = 4, matrix cores above); scale[n] is applied to
- *     the sum. No fp16 copy of the weights. For M > 4 the sum over K may be
- *     split into up to 8 slices whose fp32 partial sums (a per-stream buffer
- *     of S * M * N floats) a second kernel adds in a fixed order.
+ *     instructions up to M = 2, and up to M = 4 when K and N are below 8192;
+ *     matrix cores otherwise); scale[n] is applied to the sum. No fp16 copy
+ *     of the weights. On the matrix cores the sum over K may be split into
+ *     up to 8 slices whose fp32 partial sums (a per-stream buffer of
+ *     S * M * N floats) a second kernel adds in a fixed order.
  *   - otherwise: the weights are dequantized to fp16 (fp16(q * scale), as the
  *     reference) into a per-stream buffer that grows on demand and is reused,
  *     then multiplied by hipBLASLt with fp32 accumulation.
