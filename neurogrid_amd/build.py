@@ -46,9 +46,6 @@ COMMON_FLAGS = [
     "-Wno-unused-variable",
     "-Wno-unused-but-set-variable",
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
-    # MFMA accumulators in VGPRs rather than AGPRs: the int8 GEMM's loop then
-    # needs no accumulator copies between the two (2-7% faster at M = 64-128).
-    "-mllvm", "-amdgpu-mfma-vgpr-form=1",
     f"-I{ROOT / 'include'}",
 ]
 
