@@ -347,11 +347,15 @@ template <int MT, int W, int G>
 __global__ __launch_bounds__(G * W * kWave) void gemm_i8w_split_kernel(
     uint16_t* __restrict__ c, const uint16_t* __restrict__ a, const int8_t* __restrict__ b,
     const float* __restrict__ scale, float* __restrict__ part, int M, int N, int K, int S, int tiles, int cps) {
-    // A batch of A in LDS: 256 bytes per row, 16-byte piece q of row m stored
-    // at piece q xor (m mod 16). The MFMA reads (16 rows, one piece each per
-    // lane group) are then conflict-free; padded rows (16, 32 or 64 bytes)
-    // leave two-way conflicts, unpadded unswizzled rows eight-way ones.
-    constexpr int kRowBytes = kBatch * 2;
+    // A batch of A in LDS. From 4 tiles of A on: 256 bytes per row, 16-byte
+    // piece q of row m stored at piece q xor (m mod 16), so the MFMA reads
+    // (16 rows, one piece each per lane group) are conflict-free; padded rows
+    // (16, 32 or 64 bytes) leave two-way conflicts, unpadded unswizzled rows
+    // eight-way ones. With 1 or 2 tiles the rows are padded by 32 bytes
+    // instead: measured 6% faster there (gate/up at M = 17-32), while the
+    // swizzle is 2-11% faster at M = 64-128.
+    constexpr bool kSwizzleA = MT >= 4;
+    constexpr int kRowBytes = kSwizzleA ? kBatch * 2 : kBatch * 2 + 32;
     constexpr int kPieces = 16 * MT * 16;       // 16-byte pieces of A per batch
     constexpr int kThreads = G * W * kWave;
     static_assert((G * kPieces) % kThreads == 0, "A pieces must divide among the threads");
@@ -442,7 +446,7 @@ __global__ __launch_bounds__(G * W * kWave) void gemm_i8w_split_kernel(
             const int pc = j * kThreads + tid;
             const int g = pc / kPieces;
             const int row = (pc % kPieces) / 16;
-            *reinterpret_cast<u32x4*>(lds_a[buf][g] + row * kRowBytes + 16 * ((pc % 16) ^ (row & 15))) = ar[j];
+            *reinterpret_cast<u32x4*>(lds_a[buf][g] + row * kRowBytes + 16 * (kSwizzleA ? (pc % 16) ^ (row & 15) : pc % 16)) = ar[j];
         }
     };
     auto multiply = [&](int buf, const u32x4 (&bv)[2], int first) {
@@ -469,8 +473,9 @@ __global__ __launch_bounds__(G * W * kWave) void gemm_i8w_split_kernel(
             for (int t = 0; t < MT; ++t) {
                 // pieces 8 st + 2 grp and the next one of row 16 t + col
                 const uint8_t* ap = lds_a[buf][kg] + (16 * t + col) * kRowBytes;
-                a0[t] = *reinterpret_cast<const u32x4*>(ap + 16 * ((8 * st + 2 * grp) ^ col));
-                a1[t] = *reinterpret_cast<const u32x4*>(ap + 16 * ((8 * st + 2 * grp + 1) ^ col));
+                const int q0 = 8 * st + 2 * grp;
+                a0[t] = *reinterpret_cast<const u32x4*>(ap + 16 * (kSwizzleA ? q0 ^ col : q0));
+                a1[t] = *reinterpret_cast<const u32x4*>(ap + 16 * (kSwizzleA ? (q0 + 1) ^ col : q0 + 1));
             }
 #pragma unroll
             for (int t = 0; t < MT; ++t)
