@@ -52,8 +52,9 @@ struct MaxThreads {
     static constexpr int value = V <= 4 ? 1024 : 256;
 };
 
-template <typename T, int V, bool NORM, bool ADD, bool QUANT>
+template <typename T, int V, bool NORM, bool ADD, bool QUANT, bool WLATE>
 __global__ __launch_bounds__(MaxThreads<V>::value) void row_kernel(RowArgs a) {
+    static_assert(!WLATE || (NORM && !ADD && !QUANT), "late weights are for plain RMSNorm");
     __shared__ double s_part[16][3];
     __shared__ int s_flag[16];
     __shared__ uint32_t s_max[16];
@@ -87,12 +88,15 @@ __global__ __launch_bounds__(MaxThreads<V>::value) void row_kernel(RowArgs a) {
         if (ADD) rv[k] = ld16_stream(rr + vc * 8);
     }
     // The weight row is the same for every row of the grid. Plain RMSNorm
-    // loads it only after the reduction: issued at kernel start by every
-    // wave at once, these loads all land on the same few L2 lines and slow
-    // the row loads behind them (measured on MI355X: 13.5 vs 10.8 us for
-    // T = H = 4096); the residual and quantising variants, which have more
-    // work after the reduction, are faster with the weights loaded early.
-    constexpr bool kWeightsLate = NORM && !ADD && !QUANT;
+    // over 2048 rows or more (WLATE) loads it only after the reduction:
+    // issued at kernel start by every wave at once, these loads all land on
+    // the same few L2 lines and slow the row loads behind them (measured on
+    // MI355X: 13.3 vs 10.9 us for T = H = 4096). With fewer rows the second
+    // memory round trip costs more than it saves (T = 64: 2.7 vs 2.4 us;
+    // T = 1024: 4.8 vs 4.3 us), and the residual and quantising variants,
+    // which have more work after the reduction, are faster with the weights
+    // loaded early at every size.
+    constexpr bool kWeightsLate = WLATE;
     if (NORM && !kWeightsLate) {
 #pragma unroll
         for (int k = 0; k < V; ++k) {
@@ -138,11 +142,11 @@ __global__ __launch_bounds__(MaxThreads<V>::value) void row_kernel(RowArgs a) {
         // converts again instead of holding 8 V unpacked floats.
 #pragma unroll
         for (int k = 0; k < V; ++k) __asm__("" : "+v"(ov[k]));
-        // S sums the squares in fp64. Plain RMSNorm combines the lanes' and
-        // waves' partial sums with error-free transformations: the extra
-        // arithmetic before its first store makes it faster (measured on
-        // MI355X at T = H = 4096: 11.0 vs 11.45 us); the other variants are
-        // faster without it.
+        // S sums the squares in fp64. Plain RMSNorm with late weights combines
+        // the lanes' and waves' partial sums with error-free transformations:
+        // the extra arithmetic before its first store makes it faster
+        // (measured on MI355X at T = H = 4096: 11.0 vs 11.45 us); the other
+        // variants are faster without it.
         double S;
         if constexpr (kWeightsLate) {
             DD D2 = wave_sum_dd(dd_add(two_sum(acc[0], acc[1]), two_sum(acc[2], acc[3])));
@@ -497,19 +501,25 @@ __global__ __launch_bounds__(256) void row_kernel_scalar(RowArgs a) {
 template <typename T, bool NORM, bool ADD, bool QUANT>
 struct RowDispatch {
     template <int V>
-    static void go(dim3 g, dim3 b, const RowArgs& a) {
-        row_kernel<T, V, NORM, ADD, QUANT><<<g, b, 0, stream()>>>(a);
+    static void go(dim3 g, dim3 b, const RowArgs& a, bool late) {
+        if constexpr (NORM && !ADD && !QUANT) {
+            if (late) {
+                row_kernel<T, V, NORM, ADD, QUANT, true><<<g, b, 0, stream()>>>(a);
+                return;
+            }
+        }
+        row_kernel<T, V, NORM, ADD, QUANT, false><<<g, b, 0, stream()>>>(a);
     }
-    static bool launch(int V, dim3 g, dim3 b, const RowArgs& a) {
+    static bool launch(int V, dim3 g, dim3 b, const RowArgs& a, bool late) {
         switch (V) {
-            case 1: go<1>(g, b, a); return true;
-            case 2: go<2>(g, b, a); return true;
-            case 3: go<3>(g, b, a); return true;
-            case 4: go<4>(g, b, a); return true;
-            case 5: go<5>(g, b, a); return true;
-            case 6: go<6>(g, b, a); return true;
-            case 7: go<7>(g, b, a); return true;
-            case 8: go<8>(g, b, a); return true;
+            case 1: go<1>(g, b, a, late); return true;
+            case 2: go<2>(g, b, a, late); return true;
+            case 3: go<3>(g, b, a, late); return true;
+            case 4: go<4>(g, b, a, late); return true;
+            case 5: go<5>(g, b, a, late); return true;
+            case 6: go<6>(g, b, a, late); return true;
+            case 7: go<7>(g, b, a, late); return true;
+            case 8: go<8>(g, b, a, late); return true;
             default: return false;
         }
     }
@@ -560,7 +570,7 @@ static int launch_rows(const char* name, int rows, const RowArgs& a0) {
                 return 0;
             }
         }
-        RowDispatch<T, NORM, ADD, QUANT>::launch(V, dim3(rows), dim3(nw * 64), a);
+        RowDispatch<T, NORM, ADD, QUANT>::launch(V, dim3(rows), dim3(nw * 64), a, rows >= 2048);
     } else {
         row_kernel_scalar<T, NORM, ADD, QUANT><<<dim3(rows), dim3(256), 0, stream()>>>(a);
     }
