@@ -127,7 +127,7 @@ __global__ __launch_bounds__(WAVES * kWave) void gemm_i8w_kernel(uint16_t* __res
         u32x4 bv[U][2];
         u32x4 av[U][MT][2][2];
         auto load = [&](int slot, int i) {
-            // Batches past this wave's last are clamped to it (and multiply zero codes).
+            // Batches past this wave's last are clamped to it (and skipped in multiply).
             const int bt = min(wave + i * WAVES, last);
             const bool half = half_last && bt == nbatch - 1;
             const size_t kb = static_cast<size_t>(bt) * 128;
@@ -151,9 +151,12 @@ __global__ __launch_bounds__(WAVES * kWave) void gemm_i8w_kernel(uint16_t* __res
             __builtin_amdgcn_wave_barrier();
 #pragma unroll
             for (int st = 0; st < 2; ++st) {
+                // A batch past this wave's last, and the second half of a half
+                // batch, hold reloaded codes and activations: skipped (an inf
+                // activation times a zero code would give NaN).
+                if (past || (half && st == 1)) continue;
                 const int p = 4 * st + grp;
-                u32x4 v = lds_b[wave][8 * col + (p ^ (col >> 1))];
-                if (past || (half && st == 1)) v = u32x4{0u, 0u, 0u, 0u};
+                const u32x4 v = lds_b[wave][8 * col + (p ^ (col >> 1))];
                 f16x8 b0, b1;
                 codes16_to_operands(v, b0, b1);
 #pragma unroll
@@ -254,6 +257,12 @@ __global__ __launch_bounds__(kGvWaves * kWave) void gemv_i8w_kernel(uint16_t* __
 #pragma unroll
         for (int r = 0; r < R; ++r) bv[r] = ld16_stream(b + static_cast<size_t>(min(n0 + r, N - 1)) * K + kc);
         __builtin_amdgcn_sched_barrier(0);
+        // Lanes past K zero both operands: an inf activation times a zero code
+        // would give NaN.
+        if (!kin) {
+#pragma unroll
+            for (int m = 0; m < MR; ++m) av[m][0] = av[m][1] = u32x4{0u, 0u, 0u, 0u};
+        }
 #pragma unroll
         for (int r = 0; r < R; ++r) {
             const u32x4 q = kin ? bv[r] : u32x4{0u, 0u, 0u, 0u};
@@ -416,7 +425,7 @@ __global__ __launch_bounds__(G * W * kWave) void gemm_i8w_split_kernel(
     // turn separates a buffer's writes from its reads and from its reuse two
     // turns later. A turn starting at batch `first` holds batches first ..
     // first + G - 1; those past the slice load its last batch (every load
-    // stays unconditional) and multiply zero codes.
+    // stays unconditional) and are skipped by multiply.
     // A first: staging it into LDS then waits only for A, not for B.
     auto load = [&](u32x4 (&bv)[2], u32x4 (&ar)[kP], int first) {
 #pragma unroll
@@ -430,7 +439,7 @@ __global__ __launch_bounds__(G * W * kWave) void gemm_i8w_split_kernel(
         }
         __builtin_amdgcn_sched_barrier(0);  // keep A's loads ahead of B's
         // Pieces 4-7 of a half batch would lie past K: they load pieces 0-3
-        // again (and multiply zero codes).
+        // again (and are skipped by multiply).
         const int cb = min(first + kg, c1 - 1);
         const bool half = half_last && cb == nbatch - 1;
         const size_t kb = static_cast<size_t>(cb) * kBatch;
@@ -457,13 +466,16 @@ __global__ __launch_bounds__(G * W * kWave) void gemm_i8w_split_kernel(
         lds_b[wave][kWave + lane] = bv[1];
         __builtin_amdgcn_wave_barrier();
         const int cb = first + kg;
-        const bool past = cb >= c1;                               // clamped batch: multiplies zero codes
+        const bool past = cb >= c1;                               // clamped batch: skipped
         const bool half = half_last && cb == nbatch - 1;          // its second 64 k lie past K
 #pragma unroll
         for (int st = 0; st < 2; ++st) {
+            // A clamped batch, and the second half of a half batch, hold
+            // reloaded codes and activations: skipped (wave-uniform), so that
+            // an inf activation never meets a padding code (inf * 0 = NaN).
+            if (past || (half && st == 1)) continue;
             const int p = 4 * st + grp;
-            u32x4 v = lds_b[wave][8 * col + (p ^ (col >> 1))];
-            if (past || (half && st == 1)) v = u32x4{0u, 0u, 0u, 0u};
+            const u32x4 v = lds_b[wave][8 * col + (p ^ (col >> 1))];
             f16x8 b0, b1;
             codes16_to_operands(v, b0, b1);
             // All tiles' first halves, then their second halves: consecutive
@@ -487,7 +499,7 @@ __global__ __launch_bounds__(G * W * kWave) void gemm_i8w_split_kernel(
         __builtin_amdgcn_wave_barrier();
     };
     // The turn count is rounded up to even: an extra turn past the slice
-    // multiplies zero codes. (Leaving the loop after an odd turn instead lets
+    // is skipped by multiply. (Leaving the loop after an odd turn instead lets
     // the compiler sink the next turn's loads below the multiply.)
     const int nt = (c1 - c0 + G - 1) / G;
     u32x4 bv0[2], bv1[2];

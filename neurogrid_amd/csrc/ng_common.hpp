@@ -250,35 +250,45 @@ __device__ __forceinline__ u32x2 qcode8(const u32x4 v, float inv, float ns) {
     return out;
 }
 
-// Codes of a row whose scale is not finite (the row holds an infinity or a
-// NaN): the IEEE quotient itself, clamped. Finite values of a row with an
-// infinite scale get code 0, as v / inf = 0; the correction step above would
-// form 0 * inf = NaN instead. Codes of infinite or NaN elements are not
-// specified (the quotient is NaN).
+// The reference's clamp of a rounded quotient, fmaxf(-127, fminf(127, q))
+// (quantize.cu:92,228,313). fminf returns its other operand when one is NaN,
+// so a NaN quotient (a NaN element, or inf / inf) gives +127.
+__device__ __forceinline__ int qclamp_ref(float q) { return static_cast<int>(fmaxf(-127.0f, fminf(127.0f, q))); }
+
+// Codes of a row that holds a NaN or whose scale is not finite: the IEEE
+// quotient itself, rounded and clamped as the reference does. Finite values
+// of a row with an infinite scale get code 0, as v / inf = 0 (the correction
+// step above would form 0 * inf = NaN instead); NaN elements, and infinite
+// elements of a row with an infinite scale, get +127.
 template <typename T>
 __device__ __forceinline__ u32x2 qcode8_div(const u32x4 v, float scale) {
     u32x2 out = {0, 0};
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
-        const float q = __builtin_rintf(to_f32<T>(lane16(v, e)) / scale);
-        const int c = static_cast<int>(fminf(fmaxf(q, -127.0f), 127.0f));
+        const int c = qclamp_ref(__builtin_rintf(to_f32<T>(lane16(v, e)) / scale));
         out[e >> 2] |= (static_cast<uint32_t>(c) & 0xffu) << ((e & 3) * 8);
     }
     return out;
 }
 
-// Scalar form of the code (for element-wise fallback paths); handles a
-// non-finite scale like qcode8_div.
+// Scalar form of the code (for element-wise fallback paths); a non-finite
+// element or scale takes the IEEE quotient, like qcode8_div.
 __device__ __forceinline__ int qcode_int(float v, float scale, float inv) {
-    if (!__builtin_isfinite(scale))
-        return static_cast<int>(fminf(fmaxf(__builtin_rintf(v / scale), -127.0f), 127.0f));
+    if (!__builtin_isfinite(scale) || !__builtin_isfinite(v)) return qclamp_ref(__builtin_rintf(v / scale));
     const float z = v * inv;
     const float z1 = __builtin_fmaf(__builtin_fmaf(z, -scale, v), inv, z);
     return static_cast<int8_t>(__builtin_bit_cast(uint32_t, fp32_barrier(z1) + kRoundMagic) & 0xffu);
 }
 
+// Magnitude pattern of +inf in the 16-bit format; larger patterns are NaNs.
+template <typename T> inline constexpr uint32_t kInfBits = 0x7c00u;
+template <> inline constexpr uint32_t kInfBits<bf16> = 0x7f80u;
+
 // Largest |value| of the 8 elements of a 16-byte vector, as the 15-bit
-// magnitude pattern (for finite values |a| < |b| iff the patterns compare so).
+// magnitude pattern (for non-NaN values |a| < |b| iff the patterns compare
+// so). A NaN pattern ranks above +inf: a result above kInfBits<T> says the
+// vectors held a NaN, and absmax_bits8_nonan then gives the maximum the
+// reference's fmaxf reduction takes, which skips NaNs (quantize.cu:24-50).
 typedef uint16_t u16x2 __attribute__((ext_vector_type(2)));
 __device__ __forceinline__ uint32_t absmax_bits8(const u32x4 v, uint32_t m) {
     u16x2 a = __builtin_bit_cast(u16x2, v[0] & 0x7fff7fffu);
@@ -287,6 +297,23 @@ __device__ __forceinline__ uint32_t absmax_bits8(const u32x4 v, uint32_t m) {
     a = __builtin_elementwise_max(a, __builtin_bit_cast(u16x2, v[3] & 0x7fff7fffu));
     const uint32_t r = a[0] > a[1] ? a[0] : a[1];
     return r > m ? r : m;
+}
+
+template <typename T>
+__device__ __forceinline__ uint32_t absmax_bits8_nonan(const u32x4 v, uint32_t m) {
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+        const uint32_t b = lane16(v, e) & 0x7fffu;
+        if (b <= kInfBits<T> && b > m) m = b;
+    }
+    return m;
+}
+
+// Magnitude pattern of one element for an absmax that skips NaNs (0 for a NaN).
+template <typename T>
+__device__ __forceinline__ uint32_t absbits_nonan(uint16_t bits) {
+    const uint32_t b = bits & 0x7fffu;
+    return b > kInfBits<T> ? 0u : b;
 }
 
 // ---------------------------------------------------------------------------

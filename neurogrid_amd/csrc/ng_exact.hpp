@@ -40,19 +40,24 @@ struct DD {
     double hi, lo;
 };
 
+// Error-free a + b. The sums here are of squares, so the only non-finite
+// sums come from an inf or NaN in a row: then the error term is 0 and the sum
+// itself carries the inf or NaN (the error formula would give inf - inf =
+// NaN, turning a row's inf sum of squares into NaN).
 __device__ __forceinline__ DD two_sum(double a, double b) {
     const double s = a + b;
     const double bp = s - a;
     const double e = (a - (s - bp)) + (b - bp);
-    return {s, e};
+    return {s, __builtin_isfinite(s) ? e : 0.0};
 }
 
-// (a.hi + a.lo) + (b.hi + b.lo), renormalised so that |lo| <= ulp(hi) / 2.
+// (a.hi + a.lo) + (b.hi + b.lo), renormalised so that |lo| <= ulp(hi) / 2;
+// a non-finite hi has lo = 0, as in two_sum.
 __device__ __forceinline__ DD dd_add(DD a, DD b) {
     DD s = two_sum(a.hi, b.hi);
     const double lo = s.lo + (a.lo + b.lo);
     const double hi = s.hi + lo;
-    return {hi, lo - (hi - s.hi)};
+    return {hi, __builtin_isfinite(hi) ? lo - (hi - s.hi) : 0.0};
 }
 
 template <int CTRL>

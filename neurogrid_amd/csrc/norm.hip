@@ -10,9 +10,12 @@
 // The reference computes the same quantities with an fp32 tree sum
 // (gpu/cuda/kernels.cu:58-95 and 196-235; bf16_utils.cu:57-93).
 // Quantisation of a row v (v = y for the fused kernels, v = x otherwise):
-//   m = max|v_i|, scale = m / 127 (1 if 0), q_i = clamp(rint(v_i / scale), +-127)
+//   m = max|v_i| over the non-NaN v_i, scale = m / 127 (1 if 0),
+//   q_i = fmaxf(-127, fminf(127, rint(v_i / scale)))
 // (reference: quantize.cu:274-316, with half-to-even rounding), where
 // v_i / scale is the IEEE quotient, obtained without a division (qcode8).
+// As in the reference, a NaN element is skipped by the maximum and gets the
+// code +127; a row holding one takes the division path (qcode8_div).
 //
 // Every element-wise step is a single fp32 rounding; for fp16 rows the steps
 // read their fp16 operands directly (v_fma_mix_f32, see el_mul / el_add), so
@@ -269,6 +272,22 @@ __global__ __launch_bounds__(MaxThreads<V>::value) void row_kernel(RowArgs a) {
         mx = 0;
         for (int j = 0; j < nw; ++j) mx = umax32(mx, s_max[j]);
     }
+    // A row holding a NaN (uniform over the workgroup): the maximum again,
+    // without the NaNs, as the reference's fmaxf reduction takes it.
+    const bool has_nan = mx > kInfBits<T>;
+    if (has_nan) {
+        __shared__ uint32_t s_max2[16];
+        mx = 0;
+#pragma unroll
+        for (int k = 0; k < V; ++k) mx = absmax_bits8_nonan<T>(act[k] ? yv[k] : u32x4{0, 0, 0, 0}, mx);
+        mx = wave_max_u32_dpp(mx);
+        if (nw > 1) {
+            if (lane == 0) s_max2[wid] = mx;
+            __syncthreads();
+            mx = 0;
+            for (int j = 0; j < nw; ++j) mx = umax32(mx, s_max2[j]);
+        }
+    }
     const float m = to_f32<T>(static_cast<uint16_t>(mx));
     float scale = m / 127.0f;
     if (scale == 0.0f) scale = 1.0f;
@@ -276,10 +295,10 @@ __global__ __launch_bounds__(MaxThreads<V>::value) void row_kernel(RowArgs a) {
     if (tid == 0) a.scales[blockIdx.x] = scale;
 
     int8_t* qr = a.q + rowoff;
-    const bool finite_scale = __builtin_isfinite(scale);  // uniform over the row
+    const bool fast = !has_nan && __builtin_isfinite(scale);  // uniform over the row
 #pragma unroll
     for (int k = 0; k < V; ++k) {
-        const u32x2 c = finite_scale ? qcode8<T>(yv[k], inv, -scale) : qcode8_div<T>(yv[k], scale);
+        const u32x2 c = fast ? qcode8<T>(yv[k], inv, -scale) : qcode8_div<T>(yv[k], scale);
         if (act[k]) __builtin_nontemporal_store(c, reinterpret_cast<u32x2*>(qr + (tid + k * nthr) * 8));
     }
 }
@@ -472,7 +491,7 @@ __global__ __launch_bounds__(256) void row_kernel_scalar(RowArgs a) {
 
     uint32_t mx = 0;
     for (int i = tid; i < a.H; i += nthr) {
-        const uint32_t b = vbits(i) & 0x7fffu;
+        const uint32_t b = absbits_nonan<T>(vbits(i));  // NaNs skipped, as fmaxf does
         mx = mx > b ? mx : b;
     }
     mx = wave_max_u32_dpp(mx);

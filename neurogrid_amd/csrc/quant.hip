@@ -2,8 +2,10 @@
 // int8 -> fp16 dequantisation (per tensor, per row, per column).
 //
 // Quantisation rule (reference: gpu/cuda/quantize.cu:59-95, 189-231, with
-// half-to-even rounding): m = max|x|, scale = m / 127 (1 if that is 0),
-// q = clamp(rint(x / scale), -127, 127), IEEE division.
+// half-to-even rounding): m = max|x| over the non-NaN elements (the
+// reference's fmaxf reduction skips NaNs), scale = m / 127 (1 if that is 0),
+// q = fmaxf(-127, fminf(127, rint(x / scale))), IEEE division; a NaN element
+// gets +127.
 // Dequantisation (quantize.cu:147-158, matmul.cu:169-187):
 // out = RN_f16(RN_f32(float(q) * scale)).
 //
@@ -47,7 +49,8 @@ __global__ __launch_bounds__(kQThreads) void tensor_absmax_kernel(uint32_t* mx_o
             const u32x4 v = ld16_stream(x + i * 8);
 #pragma unroll
             for (int k = 0; k < 4; ++k) {
-                const uint32_t lo = v[k] & 0x7fffu, hi = (v[k] >> 16) & 0x7fffu;
+                const uint32_t lo = absbits_nonan<f16>(static_cast<uint16_t>(v[k]));
+                const uint32_t hi = absbits_nonan<f16>(static_cast<uint16_t>(v[k] >> 16));
                 m = m > lo ? m : lo;
                 m = m > hi ? m : hi;
             }
@@ -55,7 +58,7 @@ __global__ __launch_bounds__(kQThreads) void tensor_absmax_kernel(uint32_t* mx_o
         done = nvec * 8;
     }
     for (size_t i = done + t0; i < n; i += stride) {
-        const uint32_t b = x[i] & 0x7fffu;
+        const uint32_t b = absbits_nonan<f16>(x[i]);
         m = m > b ? m : b;
     }
     m = wave_max_u32(m);
@@ -110,7 +113,7 @@ __global__ __launch_bounds__(kQThreads) void col_absmax_kernel(uint32_t* colmax,
             const u32x4 v = ld16(x + static_cast<size_t>(r) * N + cv * 8);
 #pragma unroll
             for (int e = 0; e < 8; ++e) {
-                const uint32_t b = lane16(v, e) & 0x7fffu;
+                const uint32_t b = absbits_nonan<f16>(lane16(v, e));
                 m[e] = m[e] > b ? m[e] : b;
             }
         }
@@ -121,7 +124,7 @@ __global__ __launch_bounds__(kQThreads) void col_absmax_kernel(uint32_t* colmax,
         if (c >= N) return;
         uint32_t m = 0;
         for (int r = r0; r < r1; ++r) {
-            const uint32_t b = x[static_cast<size_t>(r) * N + c] & 0x7fffu;
+            const uint32_t b = absbits_nonan<f16>(x[static_cast<size_t>(r) * N + c]);
             m = m > b ? m : b;
         }
         atomicMax(colmax + c, m);

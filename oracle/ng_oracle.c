@@ -237,10 +237,14 @@ static float scale_of(float m) {
     return s == 0.0f ? 1.0f : s;
 }
 
+/* q = fmaxf(-127, fminf(127, rint(v / scale))), the reference's clamp order
+ * (quantize.cu:92,228,313) with ties to even: C's fminf returns its other
+ * operand for a NaN, so a NaN quotient (a NaN element, or inf / inf) gives
+ * +127. The maxima below use fmaxf, which skips NaNs as the reference's
+ * block_reduce_max does (quantize.cu:24-50). */
 static int8_t code_of(float v, float scale) {
     float q = rintf(v / scale); /* default rounding mode: nearest, ties to even */
-    if (q > 127.0f) q = 127.0f;
-    if (q < -127.0f) q = -127.0f;
+    q = fmaxf(-127.0f, fminf(127.0f, q));
     return (int8_t)q;
 }
 

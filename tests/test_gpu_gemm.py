@@ -129,6 +129,35 @@ def test_int8_weight_streaming_random(lib, ora, M, K, N):
     assert_within_bound(got, a, q, scale, True, "C", ora)
 
 
+INF_SHAPES = [(1, 1040, 100), (2, 14352, 64), (4, 2064, 33), (8, 4160, 512), (12, 1088, 4096), (64, 4096, 4096),
+              (33, 8256, 384), (80, 4160, 12288), (3, 4096, 12300), (20, 1088, 13000), (128, 14336, 4096)]
+
+
+@pytest.mark.parametrize("M,K,N", INF_SHAPES)
+def test_int8_weight_streaming_inf_activations(lib, M, K, N):
+    """One infinite activation per row. The reference's product gives
+    +-inf in every column whose weight at that k is nonzero and NaN where it is
+    zero (inf * 0). The infs sit at the ends of 64- and 128-k batches and at
+    the last k, which the kernels' padding (partial last batch, batches past a
+    K slice, lanes past K) loads again: padding must not turn them into NaN."""
+    banner(f"gemm_int8 streaming inf activations M={M} K={K} N={N}")
+    a = exact_activations(M, K)
+    cand = sorted({K - 1, K - 64, K - 65, 0} | {min(K - 1, 64 * j + 63) for j in range(K // 64 + 1)})
+    ks = np.array([cand[(m * 7) % len(cand)] for m in range(M)])
+    sgn = np.where(np.arange(M) % 2 == 0, 1.0, -1.0)
+    a[np.arange(M), ks] = f16bits(sgn * np.inf)
+    q = codes((N, K))
+    q[: max(1, N // 9), ks[0]] = 0     # some zero codes under the first row's inf: NaN there
+    scale = RNG.uniform(1e-3, 1e-2, N).astype(np.float16).astype(np.float32)
+    got = f16val(gemm_int8(lib, a, q, scale, M, K, N, True))
+    qk = q[:, ks].T.astype(np.float64)          # [M, N]: the code under each row's inf
+    with np.errstate(invalid="ignore"):
+        want = np.where(qk == 0, np.nan, sgn[:, None] * np.sign(qk) * np.inf)
+    nan_w = np.isnan(want)
+    assert (np.isnan(got) == nan_w).all(), f"NaN pattern: {(np.isnan(got) != nan_w).sum()} outputs differ"
+    assert (got[~nan_w] == want[~nan_w]).all(), "signed infinities differ"
+
+
 # The dequantize + hipBLASLt path: B [K, N] with per-column scales, M > 128 or
 # K not a multiple of 64.
 LIBRARY = [

@@ -81,10 +81,21 @@ def adversarial_rows(H):
     return np.stack(rows)
 
 
+@pytest.mark.parametrize("T", [None, 2051])
 @pytest.mark.parametrize("H", [4096, 5120, 4100])
-def test_rmsnorm_exact_path_rows(lib, ora, H):
-    banner(f"rmsnorm exact-path rows H={H}")
-    x = bits(adversarial_rows(H), "f16")
+def test_rmsnorm_exact_path_rows(lib, ora, H, T):
+    """Rows that force the exact (integer-limb) reduction. Alone they run the
+    kernel of small batches; scattered among T = 2051 ordinary rows they run the
+    large-batch kernel, which loads the weights after the reduction and combines
+    its partial sums with error-free steps before the exact fallback."""
+    banner(f"rmsnorm exact-path rows H={H} T={T}")
+    adv = bits(adversarial_rows(H), "f16")
+    if T is None:
+        x = adv
+    else:
+        x = bits(RNG.standard_normal((T, H)), "f16")
+        at = np.sort(RNG.choice(T, adv.shape[0], replace=False))
+        x[at] = adv
     w = bits(np.ones(H), "f16")
     got = run_rmsnorm(lib, x, w, 0.0, "f16")
     assert_bits_equal(got, ora.rmsnorm(x, w, 0.0), "adversarial")
@@ -135,3 +146,46 @@ def test_add_rmsnorm_exact_path_rows(lib, ora, T):
     y_want, ro_want = ora.add_rmsnorm(x, r, w, 0.0)
     assert_bits_equal(ro, ro_want, "residual_out")
     assert_bits_equal(y, y_want, "normed")
+
+
+def assert_bits_equal_nan(got, want, dtype, what):
+    """Bit-exact except NaN payloads, which are not specified: NaN positions
+    must agree."""
+    inf = 0x7F80 if dtype == "bf16" else 0x7C00
+    nan_g, nan_w = (got & 0x7FFF) > inf, (want & 0x7FFF) > inf
+    assert (nan_g == nan_w).all(), f"{what}: NaN positions differ at {np.argwhere(nan_g != nan_w)[:5].tolist()}"
+    assert_bits_equal(got[~nan_w], want[~nan_w], what)
+
+
+def nonfinite_inputs(T, H, dtype):
+    """Ordinary rows, plus rows holding an inf, a -inf, a NaN, and both. An inf
+    makes the sum of squares inf, so r = 1 / sqrt(inf) = 0: finite values
+    normalise to +-0 and the inf to NaN. A NaN makes the whole row NaN."""
+    inf, ninf, nan = (0x7F80, 0xFF80, 0x7FC0) if dtype == "bf16" else (0x7C00, 0xFC00, 0x7E00)
+    x = bits(RNG.standard_normal((T, H)), dtype)
+    r = bits(RNG.standard_normal((T, H)) * 2, dtype)
+    x[0, 1] = inf
+    x[1, H - 1] = ninf
+    x[2, H // 2] = nan
+    x[3, 0], x[3, 9] = inf, nan
+    x[T - 1, 7] = inf
+    r[4, 3] = ninf                     # reaches the residual sum
+    return x, r
+
+
+@pytest.mark.parametrize("dtype", ["f16", "bf16"])
+@pytest.mark.parametrize("T,H", [(6, 4096), (2050, 4096), (6, 5120), (6, 4100), (4096, 4096), (1600, 5120)])
+def test_norm_rows_with_inf_and_nan(lib, ora, dtype, T, H):
+    """RMSNorm and add+RMSNorm over rows holding infinities and NaNs, through
+    every kernel shape (small and large batches, several waves per row, the
+    element-wise kernel, several rows per wave)."""
+    banner(f"rmsnorm / add_rmsnorm rows with inf and NaN {dtype} T={T} H={H}")
+    x, r = nonfinite_inputs(T, H, dtype)
+    w = bits(1 + 0.02 * RNG.standard_normal(H), dtype)
+    got = run_rmsnorm(lib, x, w, 1e-5, dtype)
+    want = ora.rmsnorm(x, w, 1e-5, dtype)
+    assert_bits_equal_nan(got, want, dtype, "rmsnorm")
+    y, ro = run_add_rmsnorm(lib, x, r, w, 1e-5, dtype)
+    y_want, ro_want = ora.add_rmsnorm(x, r, w, 1e-5, dtype)
+    assert_bits_equal_nan(ro, ro_want, dtype, "residual_out")
+    assert_bits_equal_nan(y, y_want, dtype, "normed")

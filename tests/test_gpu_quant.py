@@ -57,22 +57,32 @@ def test_per_row_quant_zero_rows_and_ties(lib, ora):
     assert q[1, 1:9].tolist() == [0, 2, 2, 0, -2, -2, 126, -126]
 
 
-@pytest.mark.parametrize("cols", [4096, 1000])
-def test_per_row_quant_rows_with_infinities(lib, ora, cols):
-    """A row holding +-inf has scale inf; its finite values get code 0 (v / inf = 0),
-    as in the oracle. Codes of the infinite elements themselves are unspecified."""
-    banner(f"per-row quant rows with infinities cols={cols}")
-    x = f16(RNG.standard_normal((6, cols)))
-    x[1, 5] = 0x7C00          # +inf
-    x[3, cols - 1] = 0xFC00   # -inf
-    x[4, 0], x[4, 7] = 0x7C00, 0xFC00
+def nonfinite_rows(rows, cols):
+    """Rows holding NaNs and infinities, the cases where the reference's rule
+    (NaNs skipped by the fmaxf absmax, fmaxf(-127, fminf(127, q)) codes) differs
+    from a naive maximum."""
+    x = f16(RNG.standard_normal((rows, cols)) * RNG.uniform(0.1, 10, (rows, 1)))
+    x[0, 3] = 0x7E00                           # a quiet NaN
+    x[1, :] = 0x7E00                           # every element NaN: scale 1, codes +127
+    x[2, 5], x[2, cols - 1] = 0x7C01, 0xFE00   # signalling and negative NaNs
+    x[3, 7] = 0x7C00                           # +inf: scale inf, finite codes 0
+    x[4, 0], x[4, 1] = 0xFC00, 0x7E00          # -inf and a NaN in one row
+    x[5, cols // 2] = 0xFC00                   # -inf alone
+    return x
+
+
+@pytest.mark.parametrize("cols", [4096, 1000, 5120])
+def test_per_row_quant_rows_with_nan_and_inf(lib, ora, cols):
+    """Scales and every code bit-exact against the oracle, including the NaN and
+    infinite elements (+127, as the reference's clamp order gives)."""
+    banner(f"per-row quant rows with NaN and inf cols={cols}")
+    x = nonfinite_rows(9, cols)
     q, s = run_rows(lib, x)
     qw, sw = ora.quant_rows(x)
     assert_bits_equal(s.view(np.uint32), sw.view(np.uint32), "scales")
-    assert np.isinf(s[[1, 3, 4]]).all()
-    finite = (x & 0x7C00) != 0x7C00
-    assert_bits_equal(q[finite], qw[finite], "codes of finite elements")
-    assert (q[[1, 3, 4]][finite[[1, 3, 4]]] == 0).all()
+    assert_bits_equal(q, qw, "codes")
+    assert np.isfinite(s[0]) and s[1] == 1 and np.isinf(s[[3, 4, 5]]).all()
+    assert q[0, 3] == 127 and (q[1] == 127).all() and q[3, 7] == 127 and q[5, cols // 2] == 127
 
 
 def run_norm_quant(lib, x, w, eps, residual=None):
@@ -125,6 +135,68 @@ def test_add_rmsnorm_quant_bit_exact(lib, ora, T, H):
     assert_bits_equal(ro, row, "residual_out")
     assert_bits_equal(s.view(np.uint32), sw.view(np.uint32), "scales")
     assert_bits_equal(q, qw, "codes")
+
+
+@pytest.mark.parametrize("T,H", [(8, 4096), (6, 5120), (6, 4100), (2048, 4096)])
+def test_norm_quant_rows_with_nan_and_inf(lib, ora, T, H):
+    """RMSNorm + int8 (and the residual-add form) over rows holding a NaN or an
+    inf: a NaN makes the whole normed row NaN (scale 1, codes +127); an inf makes
+    r = 0, so the inf element normalises to NaN (+127) and the rest to 0."""
+    banner(f"norm+int8 rows with NaN and inf T={T} H={H}")
+    x = f16(RNG.standard_normal((T, H)))
+    r = f16(RNG.standard_normal((T, H)) * 2)
+    w = f16(1 + 0.02 * RNG.standard_normal(H))
+    x[0, 1] = 0x7E00
+    x[1, H - 1] = 0x7C00
+    x[2, 0], x[2, 5] = 0xFC00, 0x7C00
+    x[T - 1, H // 3] = 0x7C01
+    r[3, 17] = 0xFE00                          # the residual's NaN reaches the sum
+    q, s = run_norm_quant(lib, x, w, 1e-5)
+    qw, sw = ora.rmsnorm_quant(x, w, 1e-5)
+    assert_bits_equal(s.view(np.uint32), sw.view(np.uint32), "scales")
+    assert_bits_equal(q, qw, "codes")
+    assert (q[0] == 127).all() and q[1, H - 1] == 127 and (q[1, :H - 1] == 0).all()
+    q, s, ro = run_norm_quant(lib, x, w, 1e-5, residual=r)
+    qw, sw, row = ora.add_rmsnorm_quant(x, r, w, 1e-5)
+    # NaN payloads are not specified (the GPU keeps a quieted input payload,
+    # the oracle writes 0x7E00): NaN positions must agree, other bits exactly.
+    nan_g, nan_w = (ro & 0x7FFF) > 0x7C00, (row & 0x7FFF) > 0x7C00
+    assert (nan_g == nan_w).all(), "residual_out NaN positions"
+    assert_bits_equal(ro[~nan_w], row[~nan_w], "residual_out")
+    assert_bits_equal(s.view(np.uint32), sw.view(np.uint32), "scales")
+    assert_bits_equal(q, qw, "codes")
+    assert (q[3] == 127).all()
+
+
+@pytest.mark.parametrize("n", [4096, 12345])
+def test_per_tensor_quant_with_nan_and_inf(lib, ora, n):
+    banner(f"per-tensor quant with NaN n={n}")
+    x = f16(RNG.uniform(-1, 1, n) * 3)
+    x[[5, n - 2]] = [0x7E00, 0xFC01]
+    xb, qb, sb = dev(x), empty(n), empty(4)
+    ok(lib.cuda_quantize_per_tensor(qb.vp, sb.vp, xb.vp, n), "quant tensor")
+    qw, sw = ora.quant_tensor(x)
+    assert np.isfinite(sw[0])
+    assert_bits_equal(get(sb, np.float32, (1,)).view(np.uint32), sw.view(np.uint32), "scale")
+    assert_bits_equal(get(qb, np.int8, (n,)), qw, "codes")
+    x[7] = 0x7C00                              # and with an inf: scale inf
+    xb2, qb2, sb2 = dev(x), empty(n), empty(4)
+    ok(lib.cuda_quantize_per_tensor(qb2.vp, sb2.vp, xb2.vp, n), "quant tensor")
+    qw, sw = ora.quant_tensor(x)
+    assert np.isinf(sw[0])
+    assert_bits_equal(get(sb2, np.float32, (1,)).view(np.uint32), sw.view(np.uint32), "scale")
+    assert_bits_equal(get(qb2, np.int8, (n,)), qw, "codes")
+
+
+@pytest.mark.parametrize("K,N", [(128, 64), (100, 33)])
+def test_per_column_quant_with_nan_and_inf(lib, ora, K, N):
+    banner(f"per-column quant with NaN {K}x{N}")
+    x = np.ascontiguousarray(nonfinite_rows(N, K).T)   # the special cases down columns
+    xb, qb, sb = dev(x), empty(x.size), empty(4 * N)
+    ok(lib.cuda_quantize_weights(qb.vp, sb.vp, xb.vp, K, N), "quant cols")
+    qw, sw = ora.quant_cols(x)
+    assert_bits_equal(get(sb, np.float32, (N,)).view(np.uint32), sw.view(np.uint32), "scales")
+    assert_bits_equal(get(qb, np.int8, (K, N)), qw, "codes")
 
 
 @pytest.mark.parametrize("n", [4096, 1 << 20, 12345, 7])

@@ -396,6 +396,69 @@ def test_quant_invariants(ora):
     assert (np.abs(q * s[:, None].astype(np.float64) - v) <= s[:, None] / 2 * (1 + 1e-6)).all()
 
 
+def ref_nonfinite_codes(v, axis):
+    """The reference's rule restated with numpy's NaN-skipping routines: the
+    absmax is an fmaxf reduction from 0 (block_reduce_max, quantize.cu:24-50:
+    NaNs skipped, like np.fmax), scale = m / 127 (1 when 0), and the codes are
+    fmaxf(-127, fminf(127, rint(v / scale))) (quantize.cu:313): np.fmin / np.fmax
+    return the non-NaN operand exactly as C's fminf / fmaxf do."""
+    a = np.abs(v)
+    m = np.fmax.reduce(np.where(np.isnan(a), np.float32(0), a), axis=axis, keepdims=True).astype(np.float32)
+    s = (m / np.float32(127)).astype(np.float32)
+    s[s == 0] = 1
+    with np.errstate(invalid="ignore", divide="ignore"):
+        z = np.rint((v / s).astype(np.float32))
+    q = np.fmax(np.float32(-127), np.fmin(np.float32(127), z)).astype(np.int8)
+    return q, np.squeeze(s, axis=axis)
+
+
+def nonfinite_rows(rng, rows, cols):
+    x = f16(rng.standard_normal((rows, cols)) * rng.uniform(0.1, 10, (rows, 1)))
+    x[0, 3] = 0x7E00                     # one quiet NaN
+    x[1, :] = 0x7E00                     # all NaN: scale 1, every code +127
+    x[2, 5], x[2, 9] = 0x7C01, 0xFE00    # signalling and negative NaNs
+    x[3, 7] = 0x7C00                     # +inf: scale inf
+    x[4, 0], x[4, 1] = 0xFC00, 0x7E00    # -inf and a NaN
+    return x
+
+
+def test_quant_nan_and_inf_rows_follow_the_reference_rule(ora):
+    x = nonfinite_rows(RNG, 8, 96)
+    v = f16v(x)
+    q, s = ora.quant_rows(x)
+    qw, sw = ref_nonfinite_codes(v, 1)
+    assert (s.view(np.uint32) == sw.view(np.uint32)).all()
+    assert (q == qw).all()
+    # the cases spelled out: NaN elements +127, finite codes untouched by them
+    assert q[0, 3] == 127 and np.isfinite(s[0]) and s[0] == np.float32(np.abs(np.delete(v[0], 3)).max()) / 127
+    assert (q[1] == 127).all() and s[1] == 1
+    assert q[2, 5] == 127 and q[2, 9] == 127
+    assert np.isinf(s[3]) and q[3, 7] == 127 and (np.delete(q[3], 7) == 0).all()
+    assert np.isinf(s[4]) and q[4, 0] == 127 and q[4, 1] == 127
+    # per tensor and per column take the same rule
+    qt, st = ora.quant_tensor(x[0])
+    qtw, stw = ref_nonfinite_codes(v[0], 0)
+    assert st[0] == stw and (qt == qtw).all()
+    qc, sc = ora.quant_cols(np.ascontiguousarray(x.T))
+    qcw, scw = ref_nonfinite_codes(np.ascontiguousarray(v.T), 0)
+    assert (sc.view(np.uint32) == scw.view(np.uint32)).all() and (qc == qcw).all()
+
+
+def test_norm_quant_with_nan_and_inf_inputs(ora):
+    """A NaN in x makes every normed value NaN (scale 1, codes +127); an inf makes
+    ss = inf, r = 0, so finite values normalise to 0 and the inf to NaN (+127)."""
+    x = f16(RNG.standard_normal((3, 64)))
+    w = f16(1 + 0.02 * RNG.standard_normal(64))
+    x[0, 10] = 0x7E00
+    x[1, 20] = 0x7C00
+    q, s = ora.rmsnorm_quant(x, w, 1e-5)
+    assert s[0] == 1 and (q[0] == 127).all()
+    assert s[1] == 1 and q[1, 20] == 127 and (np.delete(q[1], 20) == 0).all()
+    y = ora.rmsnorm(x, w, 1e-5)
+    qw, sw = ref_nonfinite_codes(f16v(y), 1)
+    assert (q == qw).all() and (s == sw).all()
+
+
 def test_quant_per_tensor_reference_kat(ora):
     # tests/quantize_test.go:20-87: U(-1, 1), n = 4096, scale within 0.01 of max/127,
     # round-trip error below 0.01.
