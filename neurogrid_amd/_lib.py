@@ -91,6 +91,7 @@ SIGNATURES: dict[str, tuple] = {
     # matmul.h
     "cuda_gemm_fp16": (_i, [_vp, _cvp, _cvp, _i, _i, _i, C.c_bool, C.c_bool]),
     "cuda_gemm_int8": (_i, [_vp, _cvp, _cvp, _cvp, _i, _i, _i, C.c_bool]),
+    "ng_gemm_int8_noalloc": (_i, [_vp, _cvp, _cvp, _cvp, _i, _i, _i, C.c_bool]),
 }
 
 _LIB = None

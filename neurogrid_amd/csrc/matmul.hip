@@ -42,11 +42,20 @@
 
 #include <hipblaslt/hipblaslt.h>
 
+#include <atomic>
 #include <map>
 #include <mutex>
 #include <tuple>
 #include <utility>
 #include <vector>
+
+// Partial sums of the allocation-free entry point (ng_gemm_int8_noalloc): a
+// device array of fixed size that every GPU the library runs on holds until
+// the process ends. In host code `scratch` names a host-side stand-in, not
+// device memory: its device address is looked up once per device
+// (hipGetSymbolAddress, see scratch_ptr) and only that address is used.
+constexpr size_t kNoAllocScratchBytes = size_t(64) << 20;
+static __device__ __align__(256) float scratch[kNoAllocScratchBytes / sizeof(float)];
 
 namespace ng {
 namespace {
@@ -742,8 +751,12 @@ int gemm_lt(void* c, const void* a, const void* b, const void* q, const void* sc
     return 0;
 }
 
+// `scratch` (scratch_bytes long), when given, holds the partial sums in place
+// of this stream's buffer: nothing is allocated, and a call whose partial sums
+// do not fit is refused.
 template <int MT, int W, int G>
-int launch_split(uint16_t* c, const uint16_t* a, const int8_t* b, const float* scale, int M, int N, int K) {
+int launch_split(uint16_t* c, const uint16_t* a, const int8_t* b, const float* scale, int M, int N, int K,
+                 float* scratch, size_t scratch_bytes) {
     const int tiles = (N + 16 * W - 1) / (16 * W);
     const int nbatch = (K + kBatch - 1) / kBatch;
     // Enough slices of K for about 256 blocks (512 for K >= 8192; with groups
@@ -760,7 +773,14 @@ int launch_split(uint16_t* c, const uint16_t* a, const int8_t* b, const float* s
     const hipStream_t s = stream();
     float* part = nullptr;
     std::unique_lock<std::mutex> lock(g_mu, std::defer_lock);
-    if (S > 1) {
+    if (S > 1 && scratch != nullptr) {
+        const size_t need = static_cast<size_t>(S) * M * N * sizeof(float);
+        NG_REQUIRE(need <= scratch_bytes,
+                   "ng_gemm_int8_noalloc: M=%d K=%d N=%d splits K into %d slices whose partial sums need %zu "
+                   "bytes, more than the %zu-byte scratch; call cuda_gemm_int8 instead",
+                   M, K, N, S, need, scratch_bytes);
+        part = scratch;
+    } else if (S > 1) {
         int dev = 0;
         NG_HIP_CHECK(hipGetDevice(&dev));
         lock.lock();
@@ -792,7 +812,8 @@ int launch_split(uint16_t* c, const uint16_t* a, const int8_t* b, const float* s
 // M = 17 on and from M = 3 on with K or N of 8192 or more (at M = 4: 13.4 vs
 // 14.8 us for gate/up, 13.7 vs 15.5 us for down), otherwise the MFMA kernel
 // that reads A from L2 directly.
-int gemm_i8w(void* c, const void* a, const void* b, const void* scale, int M, int K, int N) {
+int gemm_i8w(void* c, const void* a, const void* b, const void* scale, int M, int K, int N,
+             float* scratch = nullptr, size_t scratch_bytes = 0) {
     auto* cp = static_cast<uint16_t*>(c);
     auto* ap = static_cast<const uint16_t*>(a);
     auto* bp = static_cast<const int8_t*>(b);
@@ -809,19 +830,20 @@ int gemm_i8w(void* c, const void* a, const void* b, const void* scale, int M, in
     const bool deep = K >= 8192;
     const bool wide = !deep && N >= 12288;
     if (M > 64)
-        return deep ? launch_split<8, 8, 1>(cp, ap, bp, sp, M, N, K)
-               : wide ? launch_split<8, 4, 2>(cp, ap, bp, sp, M, N, K)
-                      : launch_split<8, 4, 1>(cp, ap, bp, sp, M, N, K);
+        return deep ? launch_split<8, 8, 1>(cp, ap, bp, sp, M, N, K, scratch, scratch_bytes)
+               : wide ? launch_split<8, 4, 2>(cp, ap, bp, sp, M, N, K, scratch, scratch_bytes)
+                      : launch_split<8, 4, 1>(cp, ap, bp, sp, M, N, K, scratch, scratch_bytes);
     if (M > 32)
-        return deep ? launch_split<4, 8, 1>(cp, ap, bp, sp, M, N, K)
-               : wide ? launch_split<4, 4, 2>(cp, ap, bp, sp, M, N, K)
-                      : launch_split<4, 4, 1>(cp, ap, bp, sp, M, N, K);
+        return deep ? launch_split<4, 8, 1>(cp, ap, bp, sp, M, N, K, scratch, scratch_bytes)
+               : wide ? launch_split<4, 4, 2>(cp, ap, bp, sp, M, N, K, scratch, scratch_bytes)
+                      : launch_split<4, 4, 1>(cp, ap, bp, sp, M, N, K, scratch, scratch_bytes);
     if (M > 16)
-        return deep ? launch_split<2, 8, 1>(cp, ap, bp, sp, M, N, K)
-               : wide ? launch_split<2, 4, 2>(cp, ap, bp, sp, M, N, K)
-                      : launch_split<2, 4, 1>(cp, ap, bp, sp, M, N, K);
+        return deep ? launch_split<2, 8, 1>(cp, ap, bp, sp, M, N, K, scratch, scratch_bytes)
+               : wide ? launch_split<2, 4, 2>(cp, ap, bp, sp, M, N, K, scratch, scratch_bytes)
+                      : launch_split<2, 4, 1>(cp, ap, bp, sp, M, N, K, scratch, scratch_bytes);
     if (big)
-        return wide ? launch_split<1, 4, 2>(cp, ap, bp, sp, M, N, K) : launch_split<1, 4, 1>(cp, ap, bp, sp, M, N, K);
+        return wide ? launch_split<1, 4, 2>(cp, ap, bp, sp, M, N, K, scratch, scratch_bytes)
+                    : launch_split<1, 4, 1>(cp, ap, bp, sp, M, N, K, scratch, scratch_bytes);
     return launch_i8w<1, 1, 8, 4>(cp, ap, bp, sp, M, N, K);
 }
 
@@ -832,7 +854,32 @@ bool use_i8w(const void* a, const void* b, int M, int K, int N, bool transpose_b
     return K % kChunk == 0 || (M <= 4 && K % 16 == 0);
 }
 
+// Device address of `scratch` on device `dev`, looked up with that device
+// current on first use and kept per device (each device holds its own copy of
+// the array at its own address).
+constexpr int kMaxDevices = 64;
+std::atomic<float*> g_scratch[kMaxDevices];
+
+int scratch_ptr(int dev, float** out) {
+    NG_REQUIRE(dev >= 0 && dev < kMaxDevices, "ng_gemm_int8_noalloc: device %d out of range", dev);
+    float* p = g_scratch[dev].load(std::memory_order_acquire);
+    if (p == nullptr) {
+        void* addr = nullptr;
+        NG_HIP_CHECK(hipGetSymbolAddress(&addr, HIP_SYMBOL(scratch)));
+        NG_REQUIRE(addr != nullptr, "ng_gemm_int8_noalloc: no device address for the scratch array");
+        p = static_cast<float*>(addr);
+        g_scratch[dev].store(p, std::memory_order_release);
+    }
+    *out = p;
+    return 0;
+}
+
 }  // namespace
+
+int gemm_scratch_init(int dev) {
+    float* p = nullptr;
+    return scratch_ptr(dev, &p);
+}
 
 void gemm_release() {
     std::lock_guard<std::mutex> lock(g_mu);
@@ -853,6 +900,9 @@ void gemm_release() {
     g_retired.clear();
     for (auto& kv : g_handles) hipblasLtDestroy(kv.second);
     g_handles.clear();
+    // A device reset (cuda_shutdown) releases the module's device globals:
+    // look the scratch array up again after the next initialisation.
+    for (auto& p : g_scratch) p.store(nullptr, std::memory_order_release);
 }
 
 }  // namespace ng
@@ -872,4 +922,27 @@ extern "C" int cuda_gemm_int8(void* c, const void* a, const void* b, const void*
     NG_REQUIRE(M > 0 && K > 0 && N > 0, "cuda_gemm_int8: M=%d K=%d N=%d must be > 0", M, K, N);
     if (use_i8w(a, b, M, K, N, transpose_b)) return gemm_i8w(c, a, b, scale, M, K, N);
     return gemm_lt(c, a, nullptr, b, scale, M, K, N, false, transpose_b);
+}
+
+// The weight-streaming path of cuda_gemm_int8 with no allocation: its only
+// buffer, the split-K partial sums, lives in this library's fixed `scratch`
+// array of the current device. Same kernels, same launch shapes and so the
+// same bits as cuda_gemm_int8. Every call on a device shares that device's
+// array: calls that overlap on one GPU (other streams, other host threads)
+// race on it. The split kernel writes every partial sum before the reduction
+// reads it, so nothing needs clearing between calls.
+extern "C" int ng_gemm_int8_noalloc(void* c, const void* a, const void* b, const void* scale, int M, int K, int N,
+                                    bool transpose_b) {
+    NG_REQUIRE(c && a && b && scale, "ng_gemm_int8_noalloc: null pointer");
+    NG_REQUIRE(M > 0 && K > 0 && N > 0, "ng_gemm_int8_noalloc: M=%d K=%d N=%d must be > 0", M, K, N);
+    NG_REQUIRE(use_i8w(a, b, M, K, N, transpose_b),
+               "ng_gemm_int8_noalloc: M=%d K=%d N=%d transpose_b=%d is outside the weight-streaming path "
+               "(transpose_b, M <= %d, K %% 64 == 0 or K %% 16 == 0 with M <= 4, 16-byte aligned A and B), "
+               "which is the only one that runs without allocating; call cuda_gemm_int8 instead",
+               M, K, N, static_cast<int>(transpose_b), kMaxFusedM);
+    int dev = 0;
+    NG_HIP_CHECK(hipGetDevice(&dev));
+    float* part = nullptr;
+    if (scratch_ptr(dev, &part) != 0) return -1;
+    return gemm_i8w(c, a, b, scale, M, K, N, part, kNoAllocScratchBytes);
 }

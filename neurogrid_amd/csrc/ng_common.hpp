@@ -69,6 +69,12 @@ int device_cu_count();
 // device, which would otherwise leave them pointing at released memory.
 __attribute__((visibility("hidden"))) void gemm_release();
 
+// Looks up, with device `dev` current, the device address of the fixed
+// partial-sum array of ng_gemm_int8_noalloc (matmul.hip) and keeps it for
+// that device. cuda_init calls it; the entry point also does on its first
+// call on a device. Returns 0 or -1.
+__attribute__((visibility("hidden"))) int gemm_scratch_init(int dev);
+
 // RMSNorm of `rows` rows of H 16-bit elements through the row kernels
 // (norm.hip); launches on stream(), returns 0 or -1.
 template <typename T>

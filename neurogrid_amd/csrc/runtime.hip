@@ -97,7 +97,7 @@ extern "C" int cuda_init(int device_id) {
     void* dummy = nullptr;
     NG_HIP_CHECK(hipMalloc(&dummy, 1024));
     NG_HIP_CHECK(hipFree(dummy));
-    return 0;
+    return gemm_scratch_init(device_id);
 }
 
 extern "C" void cuda_shutdown(void) {
