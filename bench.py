@@ -31,7 +31,8 @@ kernel (SwiGLU); and the CPU oracle timed on the host cores on a bounded token
 sample of the same layer.
 
 Usage: python bench.py [--gpus 1] [--steps 50] [--warmup 5] [--no-cpu] [--no-extra]
-       python bench.py --pmc-pass   (short run for rocprofv3 --pmc: copy probe + layer kernels)
+       python bench.py --profile-pass  (eager launches of every kernel for rocprofv3: the kernel trace and
+                                        the --pmc FETCH_SIZE / WRITE_SIZE runs)
        python bench.py --gemm-only  (cuda_gemm_int8 timings only)
 """
 from __future__ import annotations
@@ -198,6 +199,67 @@ def layer_launches(L, cfg, s):
     ]
 
 
+def fused_launches(L, cfg, s):
+    """A layer in steady state with this library's fused entry points, four
+    launches: the residual add that ends the previous layer fused into this
+    layer's RMSNorm (cuda_add_rmsnorm), Q and K rotated in one launch
+    (ng_rope_qk_with_theta), add+RMSNorm, SwiGLU. Needs call-site changes in
+    the engine, so it is reported beside the headline."""
+    T, H, I, D = cfg.T, cfg.H, cfg.I, cfg.D
+    sh = s.shared
+    eps, theta = C.c_float(cfg.eps), C.c_float(cfg.theta)
+    bf = cfg.dtype == "bf16"
+    addn = L.ng_bf16_add_rmsnorm if bf else L.cuda_add_rmsnorm
+    rope_qk = L.ng_bf16_rope_qk_with_theta if bf else L.ng_rope_qk_with_theta
+    swig = L.ng_bf16_silu_mul if bf else L.cuda_silu_mul
+    return [
+        ("add_rmsnorm_in", lambda: addn(s.normed.vp, s.res_out.vp, s.down.vp, s.res.vp, sh["w_attn"].vp, T, H, eps)),
+        ("rope_qk", lambda: rope_qk(s.q.vp, s.q.vp, s.k.vp, s.k.vp, sh["pos"].ip, 1, T, cfg.nq, cfg.nkv, D, 0, theta)),
+        ("add_rmsnorm", lambda: addn(s.h2.vp, s.out.vp, s.attn.vp, s.res_out.vp, sh["w_ffn"].vp, T, H, eps)),
+        ("silu_mul", lambda: swig(s.act.vp, s.gate.vp, s.up.vp, T * I)),
+    ]
+
+
+def fused_bytes(cfg):
+    lb = W.layer_bytes(cfg)
+    return 2 * lb["add_rmsnorm"] + lb["rope_q"] + lb["rope_k"] - 4 * cfg.T + lb["silu_mul"]
+
+
+def engine_bf16_launches(L, cfg, s, hip, stream):
+    """The bf16 engine's own memory-bound sequence, unfused
+    (gpu/engine/layer.cu:1497-1615): copy residual <- input, RMSNorm, RoPE Q,
+    RoPE K, add, copy residual <- sum, RMSNorm in place, SiLU in place, mul in
+    place, residual add. The copies are device-to-device hipMemcpyAsync on the
+    launch stream, as the engine's cudaMemcpyAsync calls are."""
+    T, H, I, D = cfg.T, cfg.H, cfg.I, cfg.D
+    sh = s.shared
+    eps, theta = C.c_float(cfg.eps), C.c_float(cfg.theta)
+    nb = T * H * 2
+
+    def copy(dst, src):
+        return hip.h.hipMemcpyAsync(dst.vp, src.vp, nb, 3, stream)
+
+    return [
+        ("copy_residual", lambda: copy(s.res, s.x)),
+        ("rmsnorm", lambda: L.cuda_bf16_rmsnorm(s.normed.vp, s.x.vp, sh["w_attn"].vp, T, H, eps)),
+        ("rope_q", lambda: L.cuda_bf16_rope_with_theta(s.q.vp, s.q.vp, sh["pos"].ip, 1, T, cfg.nq, D, 0, theta)),
+        ("rope_k", lambda: L.cuda_bf16_rope_with_theta(s.k.vp, s.k.vp, sh["pos"].ip, 1, T, cfg.nkv, D, 0, theta)),
+        ("add", lambda: L.cuda_bf16_add(s.attn.vp, s.attn.vp, s.res.vp, T * H)),
+        ("copy_residual2", lambda: copy(s.res_out, s.attn)),
+        ("rmsnorm2", lambda: L.cuda_bf16_rmsnorm(s.attn.vp, s.attn.vp, sh["w_ffn"].vp, T, H, eps)),
+        ("silu", lambda: L.cuda_bf16_silu(s.gate.vp, s.gate.vp, T * I)),
+        ("mul", lambda: L.cuda_bf16_mul(s.gate.vp, s.gate.vp, s.up.vp, T * I)),
+        ("add_out", lambda: L.cuda_bf16_add(s.out.vp, s.down.vp, s.res_out.vp, T * H)),
+    ]
+
+
+def engine_bf16_bytes(cfg):
+    T, H, I, e = cfg.T, cfg.H, cfg.I, cfg.e
+    lb = W.layer_bytes(cfg)
+    return (2 * 2 * T * H * e + 2 * lb["rmsnorm"] + lb["rope_q"] + lb["rope_k"] + 2 * lb["add"]
+            + 2 * T * I * e + 3 * T * I * e)
+
+
 class Pool:
     """`n` copies of one buffer in one device allocation (slot j at offset
     j * slot bytes), all holding the same initial data, so that a kernel can be
@@ -296,27 +358,11 @@ def run_layer(L, hip, stream, cfg, steps, warmup, kernel_launches=24, kernel_rep
         nsets = min(32, max(2, -(-ROTATE_BYTES // LayerSet.nbytes(cfg))))
     sets = [LayerSet(d, cfg, shared) for _ in range(nsets)]
     del d
-    launches = [layer_launches(L, cfg, s) for s in sets]
-    names = [n for n, _ in launches[0]]
-
-    # Eager pass first: argument errors surface here, outside any capture.
-    for lset in launches:
-        for name, fn in lset:
-            if fn() != 0:
-                raise RuntimeError(f"{name} failed")
-    hip.sync()
-
-    # One graph of `warmup` steps, replayed once untimed, then one graph of
-    # exactly `steps` steps, replayed once between two events.
-    warm_graph = hip.capture(stream, [t for i in range(max(warmup, 1)) for t in launches[i % nsets]])
-    timed_graph = hip.capture(stream, [t for i in range(warmup, warmup + steps) for t in launches[i % nsets]])
-    warm_graph.launch(stream)
-    hip.sync()
-    t0 = time.perf_counter()
-    step_ms = time_graph(hip, stream, [timed_graph], 1, 0) / steps
-    wall_ms = (time.perf_counter() - t0) * 1e3 / steps
-    warm_graph.destroy()
-    timed_graph.destroy()
+    step_ms, wall_ms = time_steps(hip, stream, [layer_launches(L, cfg, s) for s in sets], steps, warmup)
+    seq = {"fused_step_ms": time_steps(hip, stream, [fused_launches(L, cfg, s) for s in sets], steps, warmup)[0]}
+    if cfg.dtype == "bf16":
+        seq["engine_bf16_step_ms"] = time_steps(
+            hip, stream, [engine_bf16_launches(L, cfg, s, hip, stream) for s in sets], steps, warmup)[0]
 
     for s in sets:
         s.free()
@@ -340,7 +386,44 @@ def run_layer(L, hip, stream, cfg, steps, warmup, kernel_launches=24, kernel_rep
     del d
     for b in shared.values():
         b.free()
-    return step_ms, wall_ms, per, nsets, slots
+    return step_ms, wall_ms, per, nsets, slots, seq
+
+
+def fused_layer_report(cfg, per, seq):
+    """The four-launch steady state (fused_launches): its graph step time,
+    and the sum of its kernels' per-kernel averages."""
+    b = fused_bytes(cfg)
+    us = seq["fused_step_ms"] * 1e3
+    us_sum = 2 * per["add_rmsnorm"] + per["rope_qk"] + per["silu_mul"]
+    return {"kernels": ["add_rmsnorm (residual add of the previous layer + RMSNorm)", "rope_qk", "add_rmsnorm",
+                        "silu_mul"],
+            "us_per_step": us, "us_per_layer": us_sum, "layer_bytes": b, "GBps": b / us / 1e3,
+            "frac": b / us / 1e3 / PEAK_GBPS,
+            "note": "us_per_step: graph replay of the four launches per step; us_per_layer: the sum of their "
+                    "per-kernel averages; the engine's six-kernel sequence is the headline"}
+
+
+def time_steps(hip, stream, launches, steps, warmup):
+    """Step time of a sequence: one graph of `warmup` steps replayed once
+    untimed, then one graph of exactly `steps` steps (cycling over the
+    rotating sets' launch lists) replayed once between two events. An eager
+    pass first makes argument errors surface outside any capture."""
+    for lset in launches:
+        for name, fn in lset:
+            if fn() != 0:
+                raise RuntimeError(f"{name} failed")
+    hip.sync()
+    n = len(launches)
+    warm_graph = hip.capture(stream, [t for i in range(max(warmup, 1)) for t in launches[i % n]])
+    timed_graph = hip.capture(stream, [t for i in range(warmup, warmup + steps) for t in launches[i % n]])
+    warm_graph.launch(stream)
+    hip.sync()
+    t0 = time.perf_counter()
+    step_ms = time_graph(hip, stream, [timed_graph], 1, 0) / steps
+    wall_ms = (time.perf_counter() - t0) * 1e3 / steps
+    warm_graph.destroy()
+    timed_graph.destroy()
+    return step_ms, wall_ms
 
 
 # ----------------------------------------------------------------------------- other kernels
@@ -393,6 +476,43 @@ def extra_kernels(L, hip, stream):
     out["gather_mistral7b_prefill"] = {"us": us, "GBps": b / us / 1e3, "frac": b / us / 1e3 / PEAK_GBPS,
                                        "bytes": b, "buffer_sets": f"{ntab} tables, {nids} id vectors",
                                        "note": "table [32000,4096] fp16 (262 MB), uniform ids"}
+    for p in (tabs, ids, outs):
+        p.free()
+
+    # Embedding gather at Mistral-Nemo (bf16, T = 2048): Zipf(1.1) ids over a
+    # [131072, 5120] table (1.34 GB); 4 table copies and 24 id vectors, so a
+    # launch finds no row of the previous one in the caches. Zipf ids repeat,
+    # so the hot rows come from the caches within a launch: FETCH_SIZE (the
+    # traffic summary) is below the algorithmic bytes.
+    nm = W.CONFIGS["mistral_nemo_bf16"]
+    rng = np.random.Generator(np.random.PCG64(1))
+    ntab, nids = 4, 24
+    tabs = Pool(hip, 2 * nm.vocab * nm.H, ntab)
+    for r0 in range(0, nm.vocab, 16384):            # fill slot 0 in pieces, then copy it
+        piece = W.round_to(rng.standard_normal((min(16384, nm.vocab - r0), nm.H), dtype=np.float32)
+                           * np.float32(0.02), "bf16")
+        hip.check(L.cuda_copy_int8_to_device(tabs.buf.offset(2 * r0 * nm.H), piece.ctypes.data, piece.nbytes),
+                  "upload")
+    del piece
+    for j in range(1, ntab):
+        hip.check(hip.h.hipMemcpyAsync(tabs.at(j), tabs.at(0), 2 * nm.vocab * nm.H, 3, None), "hipMemcpyAsync")
+    hip.sync()
+    ids = Pool(hip, 4 * nm.T, nids)
+    assert ids.slot == 4 * nm.T
+    zipf = np.stack([W.zipf_ids(rng, nm.T, nm.vocab, 1.1) for _ in range(nids)])
+    ids.buf.upload(zipf)
+    outs = Pool(hip, 2 * nm.T * nm.H, 8)
+    thunks = [("gather_zipf", (lambda j=j: L.cuda_gather_embeddings(outs.at(j), tabs.at(j), ipt(j), nm.H, nm.T)))
+              for j in range(nids)]
+    us = time_pool_kernel(hip, stream, thunks)
+    b = W.layer_bytes(cfg)["gather"]
+    distinct = float(np.mean([np.unique(z).size for z in zipf]))
+    out["gather_mistral_nemo_bf16_zipf"] = {
+        "us": us, "GBps": b / us / 1e3, "frac": b / us / 1e3 / PEAK_GBPS, "bytes": b,
+        "buffer_sets": f"{ntab} tables, {nids} id vectors",
+        "distinct_rows_per_launch": distinct,
+        "note": "table [131072,5120] bf16 (1.34 GB), Zipf(1.1) ids; GBps counts every row read once per token "
+                "(algorithmic bytes), though repeated ids are served from the caches"}
     for p in (tabs, ids, outs):
         p.free()
 
@@ -522,18 +642,19 @@ def gemm_extras(L, hip, stream):
 
 # ----------------------------------------------------------------------------- CPU baseline
 
-def cpu_baseline(cfg, budget_s=10.0):
-    """The CPU oracle (a C restatement of the reference semantics) running the
-    same layer kernel set on a token sample, OpenMP over the host threads, plus
-    one single-thread measurement."""
+def cpu_baseline(cfg, budget_s=10.0, sample_1t=256):
+    """The CPU oracle (oracle/ng_oracle.c, a C restatement of the reference
+    semantics, built -O3 -march=x86-64-v3 with OpenMP) running the same layer
+    kernel set on the same inputs: the full T on all host threads, and a
+    sample of `sample_1t` tokens on one thread (the full T would take about 5 s
+    per repetition there)."""
     from oracle import oracle as O
 
-    sample_T = 256
-    sub = W.LayerConfig(**{**cfg.__dict__, "T": sample_T, "key": cfg.key + "_cpu_sample"})
-    d = W.make_layer_inputs(sub, seed=0, with_table=False)
-    nbytes = sum(W.layer_bytes(sub)[k] for k in W.LAYER_KERNELS)
+    def inputs(T):
+        sub = W.LayerConfig(**{**cfg.__dict__, "T": T, "key": f"{cfg.key}_cpu_T{T}"})
+        return sub, W.make_layer_inputs(sub, seed=0, with_table=False)
 
-    def one():
+    def one(sub, d):
         O.rmsnorm(d["x"], d["w_attn"], sub.eps, sub.dtype)
         O.rope(d["q"], d["pos"], 0, sub.theta, sub.dtype)
         O.rope(d["k"], d["pos"], 0, sub.theta, sub.dtype)
@@ -541,52 +662,196 @@ def cpu_baseline(cfg, budget_s=10.0):
         O.elementwise("silu_mul", d["gate"], d["up"], dtype=sub.dtype)
         O.elementwise("add", d["x"], d["residual"], dtype=sub.dtype)
 
-    def measure(seconds):
-        one()
+    def measure(sub, d, seconds, min_reps=5):
+        one(sub, d)
         ts = []
         t_end = time.perf_counter() + seconds
-        while time.perf_counter() < t_end or len(ts) < 3:
+        while time.perf_counter() < t_end or len(ts) < min_reps:
             t = time.perf_counter()
-            one()
+            one(sub, d)
             ts.append(time.perf_counter() - t)
         return float(np.median(ts)), len(ts)
 
+    sub1, d1 = inputs(sample_1t)
     O.set_threads(1)
-    med1, n1 = measure(budget_s / 4)
+    med1, n1 = measure(sub1, d1, budget_s / 4, 3)
+    b1 = sum(W.layer_bytes(sub1)[k] for k in W.LAYER_KERNELS)
+    del d1
+    sub, d = inputs(cfg.T)
     O.set_threads(os.cpu_count() or 1)
     cores = O.get_threads()
-    med, n = measure(budget_s)
+    med, n = measure(sub, d, budget_s)
+    nbytes = sum(W.layer_bytes(sub)[k] for k in W.LAYER_KERNELS)
     return {"value": nbytes / med / 1e9, "unit": "GB/s", "cores": cores, "kind": "port",
-            "us_per_layer_sample": med * 1e6,
-            "value_1_thread": nbytes / med1 / 1e9, "us_per_layer_sample_1_thread": med1 * 1e6,
-            "sample": f"{cfg.key} layer kernel set on T={sample_T} tokens (of {cfg.T}); median of {n} reps in "
-                      f"{budget_s:.0f} s on {cores} OpenMP threads, and of {n1} reps on 1 thread"}
+            "us_per_layer": med * 1e6,
+            "value_1_thread": b1 / med1 / 1e9, "us_per_layer_sample_1_thread": med1 * 1e6,
+            "build": "gcc -O3 -march=x86-64-v3 -fopenmp -ffp-contract=off (portable x86-64-v3, not -march=native: "
+                     "the oracle is built in one container and run on the GPU box's host)",
+            "sample": f"{cfg.key} layer kernel set (rmsnorm, rope q, rope k, add+rmsnorm, silu_mul, add) on the "
+                      f"full T={cfg.T}: median of {n} reps on {cores} OpenMP threads; one thread on the first "
+                      f"{sample_1t} tokens: median of {n1} reps"}
 
 
-# ----------------------------------------------------------------------------- rocprofv3 --pmc pass
+# ----------------------------------------------------------------------------- rocprofv3 profiling pass
 
-def pmc_pass(L, hip, stream):
-    """A short program for rocprofv3 --pmc: a plain device-to-device copy of
-    known size (calibrates FETCH_SIZE / WRITE_SIZE), then one eager launch of
-    each layer kernel at Mistral-7B prefill shapes, each on a fresh set."""
+PROFILE_LAUNCHES = 5
+PROFILE_WARMUP = 20
+
+
+def profile_pass(L, hip, stream):
+    """The program the committed rocprofv3 summaries come from (--kernel-trace
+    --stats, and --pmc FETCH_SIZE / WRITE_SIZE in runs of their own). Every
+    launch is eager (no graph) and none uses hipBLASLt.
+
+    Calibration: a 256 MiB device-to-device copy (reads and writes 256 MiB),
+    and cuda_quantize_per_tensor over 128 Mi fp16 values, whose absmax kernel
+    reads 256 MiB and writes one word. Then, for each layer configuration, each
+    layer kernel (and ng_rope_qk_with_theta; for bf16 also the engine's
+    unfused RMSNorm in place, add, SiLU and mul) PROFILE_LAUNCHES times, each
+    launch on a buffer slot untouched for over 1 GB of other traffic; the
+    embedding gathers (Mistral-7B uniform ids, Mistral-Nemo Zipf ids); fused
+    RMSNorm + int8, residual add + RMSNorm + int8 and int8 dequant at the
+    quant configuration; QK LayerNorm + RoPE. Before each group a line
+    "[profile] <label> dispatches=<n>" goes to stderr: n is the number of this
+    library's kernel dispatches in the group, in order, so a summary can name
+    every dispatch of the trace."""
+
+    def group(label, thunks, per_call=1, warm=PROFILE_WARMUP):
+        # `warm` launches, then PROFILE_LAUNCHES measured ones, all enqueued
+        # without waiting, cycling over the buffer slots: the GPU stays busy
+        # (clocks up) and every launch finds a slot untouched since a full
+        # cycle of the others.
+        seq = [thunks[i % len(thunks)] for i in range(warm + PROFILE_LAUNCHES)]
+        log_profile(label, PROFILE_LAUNCHES * per_call, warm * per_call)
+        for fn in seq:
+            if fn() != 0:
+                raise RuntimeError(f"{label} failed")
+        hip.sync()
+
     nbytes = 256 << 20
     src, dst = DB(nbytes), DB(nbytes)
+    print("[profile] calib/copy_256MiB rocclr_copies=3", file=sys.stderr, flush=True)
     for _ in range(3):
         hip.check(hip.h.hipMemcpyAsync(dst.vp, src.vp, nbytes, 3, stream), "hipMemcpyAsync")
     hip.sync()
-    src.free()
-    dst.free()
+    sc = DB(4)
+    # fill (1 thread), absmax (reads 256 MiB), quantise, finalise: 4 dispatches per call
+    group("calib/quant_per_tensor_256MiB", [lambda: L.cuda_quantize_per_tensor(dst.vp, sc.vp, src.vp, nbytes // 2)],
+          per_call=4, warm=0)
+    for b in (src, dst, sc):
+        b.free()
+
+    for key in ("mistral7b_prefill", "mistral7b_decode", "llama2_13b_prefill", "mistral_nemo_bf16"):
+        cfg = W.CONFIGS[key]
+        d = W.make_layer_inputs(cfg, seed=0, with_table=False)
+        shared = {"w_attn": DB.from_array(d["w_attn"]), "w_ffn": DB.from_array(d["w_ffn"]),
+                  "pos": DB.from_array(d["pos"])}
+        for name, make in kernel_pools_for(L, hip, cfg, d, shared):
+            thunks, pools = make()
+            group(f"{key}/{name}", [fn for _, fn in thunks])
+            for p in pools:
+                p.free()
+        if cfg.dtype == "bf16":
+            for name, make in engine_bf16_pools_for(L, hip, cfg, d, shared):
+                thunks, pools = make()
+                group(f"{key}/engine_{name}", [fn for _, fn in thunks])
+                for p in pools:
+                    p.free()
+        for b in shared.values():
+            b.free()
+        del d
+
+    # embedding gathers
+    for key, ntab in (("mistral7b_prefill", 8), ("mistral_nemo_bf16", 4)):
+        cfg = W.CONFIGS[key]
+        rng = np.random.Generator(np.random.PCG64(2))
+        row_bytes = cfg.H * 2
+        tabs = Pool(hip, row_bytes * cfg.vocab, ntab)
+        for r0 in range(0, cfg.vocab, 16384):
+            n = min(16384, cfg.vocab - r0)
+            piece = W.round_to(rng.standard_normal((n, cfg.H), dtype=np.float32) * np.float32(0.02), cfg.dtype)
+            hip.check(L.cuda_copy_int8_to_device(tabs.buf.offset(r0 * row_bytes), piece.ctypes.data, piece.nbytes),
+                      "upload")
+        for j in range(1, ntab):
+            hip.check(hip.h.hipMemcpyAsync(tabs.at(j), tabs.at(0), row_bytes * cfg.vocab, 3, None), "hipMemcpyAsync")
+        hip.sync()
+        zipf = cfg.ids.startswith("zipf")
+        ids = np.stack([W.zipf_ids(rng, cfg.T, cfg.vocab, 1.1) if zipf else
+                        rng.integers(0, cfg.vocab, cfg.T).astype(np.int32) for _ in range(ntab)])
+        idb = DB.from_array(ids)
+        outs = Pool(hip, 2 * cfg.T * cfg.H, ntab)
+        group(f"{key}/gather_{'zipf' if zipf else 'uniform'}",
+              [(lambda j=j: L.cuda_gather_embeddings(outs.at(j), tabs.at(j), C.cast(idb.offset(4 * cfg.T * j),
+                                                                                    C.POINTER(C.c_int)),
+                                                     cfg.H, cfg.T)) for j in range(ntab)])
+        for b in (tabs, outs, idb):
+            b.free()
+
+    # quant configuration
+    q = W.make_quant_inputs(seed=0)
+    T, H, eps = W.QUANT_T, W.QUANT_H, C.c_float(1e-5)
+    n = pool_slots(W.quant_bytes()["rmsnorm_quant"])
+    xs, res, ro = Pool(hip, q["x"].nbytes, n, q["x"]), Pool(hip, q["x"].nbytes, n, q["x"]), Pool(hip, q["x"].nbytes, n)
+    codes, scl = Pool(hip, q["x"].size, n), Pool(hip, 4 * T, n)
+    wb = DB.from_array(q["w"])
+    group("quant/rmsnorm_quant", [(lambda j=j: L.ng_rmsnorm_quant_int8(codes.at(j), scl.at(j), xs.at(j), wb.vp, T, H,
+                                                                       eps)) for j in range(n)])
+    group("quant/add_rmsnorm_quant", [(lambda j=j: L.ng_add_rmsnorm_quant_int8(
+        codes.at(j), scl.at(j), ro.at(j), xs.at(j), res.at(j), wb.vp, T, H, eps)) for j in range(n)])
+    for p in (xs, res, ro, codes, scl):
+        p.free()
+    wb.free()
+    n = pool_slots(W.quant_bytes()["dequant"])
+    wq, wo = Pool(hip, q["wq"].nbytes, n, q["wq"]), Pool(hip, 2 * q["wq"].size, n)
+    ws = DB.from_array(q["wscale"])
+    group("quant/dequant", [(lambda j=j: L.cuda_dequantize_weights(wo.at(j), wq.at(j), ws.vp, W.QUANT_WN, W.QUANT_WK,
+                                                                   1)) for j in range(n)])
+    for p in (wq, wo):
+        p.free()
+    ws.free()
+
+    # QK LayerNorm + RoPE at Mistral-7B prefill shapes
     cfg = W.CONFIGS["mistral7b_prefill"]
     d = W.make_layer_inputs(cfg, seed=0, with_table=False)
-    shared = {"w_attn": DB.from_array(d["w_attn"]), "w_ffn": DB.from_array(d["w_ffn"]),
-              "pos": DB.from_array(d["pos"])}
-    sets = [LayerSet(d, cfg, shared) for _ in range(3)]
-    for s in sets:
-        for name, fn in layer_launches(L, cfg, s):
-            if fn() != 0:
-                raise RuntimeError(f"{name} failed")
-        hip.sync()
-    log(f"pmc pass done: copy {nbytes} B x3, layer kernels x{len(sets)}")
+    T, D, nq, nkv = cfg.T, cfg.D, cfg.nq, cfg.nkv
+    n = pool_slots(2 * (d["q"].nbytes + d["k"].nbytes))
+    qp, kp = Pool(hip, d["q"].nbytes, n, d["q"]), Pool(hip, d["k"].nbytes, n, d["k"])
+    wq, wk, pos = DB.from_array(d["w_attn"][:D]), DB.from_array(d["w_ffn"][:D]), DB.from_array(d["pos"])
+    group("mistral7b_prefill/qk_rmsnorm_rope", [(lambda j=j: L.ng_qk_rmsnorm_rope_with_theta(
+        qp.at(j), qp.at(j), kp.at(j), kp.at(j), wq.vp, wk.vp, pos.ip, 1, T, nq, nkv, D, eps, 0,
+        C.c_float(cfg.theta))) for j in range(n)])
+    for p in (qp, kp):
+        p.free()
+    for b in (wq, wk, pos):
+        b.free()
+    log("profile pass done")
+
+
+def log_profile(label, dispatches, warmup):
+    print(f"[profile] {label} warmup={warmup} dispatches={dispatches}", file=sys.stderr, flush=True)
+
+
+def engine_bf16_pools_for(L, hip, cfg, d, shared):
+    """The kernels of the bf16 engine's unfused sequence that the fused layer
+    does not launch (engine_bf16_launches), with buffer pools as in
+    kernel_pools_for: RMSNorm in place, add, SiLU in place, mul in place."""
+    T, H, I, e = cfg.T, cfg.H, cfg.I, cfg.e
+    eps = C.c_float(cfg.eps)
+    th, ti = T * H * e, T * I * e
+
+    def mk(name, footprint, specs, launch):
+        def make():
+            n = pool_slots(footprint)
+            pools = [Pool(hip, nbytes, n, init) for nbytes, init in specs]
+            thunks = [(name, (lambda j=j: launch(*[p.at(j) for p in pools]))) for j in range(n)]
+            return thunks, pools
+        return name, make
+
+    yield mk("rmsnorm_inplace", 2 * th, [(th, d["x"])],
+             lambda x: L.cuda_bf16_rmsnorm(x, x, shared["w_ffn"].vp, T, H, eps))
+    yield mk("add", 3 * th, [(th, d["x"]), (th, d["residual"])], lambda a, r: L.cuda_bf16_add(a, a, r, T * H))
+    yield mk("silu", 2 * ti, [(ti, d["gate"])], lambda g: L.cuda_bf16_silu(g, g, T * I))
+    yield mk("mul", 3 * ti, [(ti, d["gate"]), (ti, d["up"])], lambda g, u: L.cuda_bf16_mul(g, g, u, T * I))
 
 
 # ----------------------------------------------------------------------------- main
@@ -596,7 +861,7 @@ def load_traffic():
     rocprofv3 --pmc summary (FETCH_SIZE + WRITE_SIZE, calibrated on a copy)."""
     try:
         t = json.loads(TRAFFIC_FILE.read_text())
-        return t["silu_mul"]["hbm_bytes"]
+        return t["mistral7b_prefill/silu_mul"]["hbm_bytes"]
     except (OSError, KeyError, ValueError):
         return None
 
@@ -610,7 +875,8 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-extra", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
-    ap.add_argument("--pmc-pass", action="store_true")
+    ap.add_argument("--profile-pass", "--pmc-pass", dest="profile_pass", action="store_true",
+                    help="eager launches of every kernel for rocprofv3 (kernel trace and --pmc runs)")
     ap.add_argument("--gemm-only", action="store_true",
                     help="time only cuda_gemm_int8 at Mistral-7B's INT8 projections and print that JSON")
     args = ap.parse_args()
@@ -625,8 +891,8 @@ def main():
     hip = Hip()
     stream = hip.stream()
     L.ng_set_stream(stream)
-    if args.pmc_pass:
-        pmc_pass(L, hip, stream)
+    if args.profile_pass:
+        profile_pass(L, hip, stream)
         return
     if args.gemm_only:
         print(json.dumps({"gemm_int8": gemm_extras(L, hip, stream)}), flush=True)
@@ -634,7 +900,7 @@ def main():
 
     cfg = W.CONFIGS[args.config]
     log(f"layer {cfg.key}: {args.warmup} warmup + {args.steps} timed graph replays")
-    step_ms, wall_ms, per, nsets, slots = run_layer(L, hip, stream, cfg, args.steps, args.warmup)
+    step_ms, wall_ms, per, nsets, slots, seq = run_layer(L, hip, stream, cfg, args.steps, args.warmup)
     lb = W.layer_bytes(cfg)
     layer_bytes = sum(lb[k] for k in W.LAYER_KERNELS)
     kernels = {}
@@ -654,25 +920,31 @@ def main():
     # that ends layer L and the RMSNorm that starts layer L+1 are one
     # cuda_add_rmsnorm, and Q and K rotate in one launch. Needs call-site
     # changes in the engine, so it is reported beside the headline.
-    fl_bytes = 2 * lb["add_rmsnorm"] + qk_bytes + lb["silu_mul"]
-    fl_us = 2 * per["add_rmsnorm"] + per["rope_qk"] + per["silu_mul"]
-    fused_layer = {"kernels": ["add_rmsnorm (residual add of the previous layer + RMSNorm)", "rope_qk",
-                               "add_rmsnorm", "silu_mul"],
-                   "us_per_layer": fl_us, "layer_bytes": fl_bytes, "GBps": fl_bytes / fl_us / 1e3,
-                   "frac": fl_bytes / fl_us / 1e3 / PEAK_GBPS,
-                   "note": "sum of the per-kernel averages above; the engine's six-kernel sequence is the headline"}
+    fused_layer = fused_layer_report(cfg, per, seq)
 
     extra = {}
     if not args.no_extra:
         for key in ("mistral7b_decode", "llama2_13b_prefill", "mistral_nemo_bf16"):
             log(f"layer {key}")
             c2 = W.CONFIGS[key]
-            s2, _, p2, _, _ = run_layer(L, hip, stream, c2, 20, 3)
+            s2, _, p2, _, _, seq2 = run_layer(L, hip, stream, c2, 20, 3)
             lb2 = W.layer_bytes(c2)
             b2 = sum(lb2[k] for k in W.LAYER_KERNELS)
             u2 = sum(p2[k] for k in W.LAYER_KERNELS)
             extra[key] = {"us_per_layer": u2, "us_per_step": s2 * 1e3, "GBps": b2 / u2 / 1e3,
-                          "frac": b2 / u2 / 1e3 / PEAK_GBPS, "layer_bytes": b2, "per_kernel_us": p2}
+                          "frac": b2 / u2 / 1e3 / PEAK_GBPS, "layer_bytes": b2, "per_kernel_us": p2,
+                          "fused_layer_variant": fused_layer_report(c2, p2, seq2)}
+            if c2.dtype == "bf16":
+                eb = engine_bf16_bytes(c2)
+                eu = seq2["engine_bf16_step_ms"] * 1e3
+                extra[key]["engine_bf16_unfused"] = {
+                    "us_per_step": eu, "layer_bytes": eb,
+                    "sequence": ["copy residual", "rmsnorm", "rope_q", "rope_k", "add", "copy residual",
+                                 "rmsnorm (in place)", "silu (in place)", "mul (in place)", "add"],
+                    "note": "the bf16 engine's own sequence (layer.cu:1497-1615: two device copies, RMSNorm, "
+                            "RoPE Q and K, add, RMSNorm, SiLU, mul, add); us_per_step of this layer above uses "
+                            "the fused ng_bf16_add_rmsnorm and ng_bf16_silu_mul instead, which need the call-site "
+                            "change in INTEGRATION.md"}
         log("gather / rmsnorm+int8 / dequant")
         extra.update(extra_kernels(L, hip, stream))
 
@@ -680,6 +952,9 @@ def main():
     roof = {"kernel": "cuda_silu_mul (ng::ew_vec_kernel<_Float16, EW_SILU_MUL, 1>)", "bound": "hbm",
             "achieved": kernels[dom]["GBps"], "peak": PEAK_GBPS, "unit": "GB/s",
             "frac": kernels[dom]["GBps"] / PEAK_GBPS, "traffic": load_traffic(),
+            "traffic_source": f"{TRAFFIC_FILE.relative_to(ROOT)}: FETCH_SIZE and WRITE_SIZE per dispatch from "
+                              "rocprofv3 --pmc runs of bench.py --profile-pass, scaled by a 256 MiB copy; read "
+                              "from the committed profile, not measured by this run",
             "algorithmic_bytes_per_launch": lb[dom], "avg_launch_us": kernels[dom]["us"]}
 
     cpu = None
