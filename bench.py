@@ -389,6 +389,24 @@ def run_layer(L, hip, stream, cfg, steps, warmup, kernel_launches=24, kernel_rep
     return step_ms, wall_ms, per, nsets, slots, seq
 
 
+def copy_times(hip, stream, byte_counts, launches=24, reps=4):
+    """Average duration (us) of a plain device-to-device hipMemcpyAsync that
+    moves b bytes (reads b / 2, writes b / 2), for each b in byte_counts,
+    timed as the kernels are: back-to-back in one graph over a pool of
+    buffers. The HBM rate a streaming kernel of that size can reach."""
+    out = {}
+    for b in sorted(set(int(x) for x in byte_counts)):
+        half = b // 2
+        n = pool_slots(b)
+        src, dst = Pool(hip, half, n), Pool(hip, half, n)
+        thunks = [("copy", (lambda j=j: hip.h.hipMemcpyAsync(dst.at(j), src.at(j), half, 3, stream)))
+                  for j in range(n)]
+        out[b] = time_pool_kernel(hip, stream, thunks, launches, reps)
+        src.free()
+        dst.free()
+    return out
+
+
 def fused_layer_report(cfg, per, seq):
     """The four-launch steady state (fused_launches): its graph step time,
     and the sum of its kernels' per-kernel averages."""
@@ -505,7 +523,7 @@ def extra_kernels(L, hip, stream):
     thunks = [("gather_zipf", (lambda j=j: L.cuda_gather_embeddings(outs.at(j), tabs.at(j), ipt(j), nm.H, nm.T)))
               for j in range(nids)]
     us = time_pool_kernel(hip, stream, thunks)
-    b = W.layer_bytes(cfg)["gather"]
+    b = W.layer_bytes(nm)["gather"]
     distinct = float(np.mean([np.unique(z).size for z in zipf]))
     out["gather_mistral_nemo_bf16_zipf"] = {
         "us": us, "GBps": b / us / 1e3, "frac": b / us / 1e3 / PEAK_GBPS, "bytes": b,
@@ -583,18 +601,22 @@ def extra_kernels(L, hip, stream):
     return out
 
 
+PREFILL_M = (512, 4096)
+
+
 def gemm_extras(L, hip, stream):
     """cuda_gemm_int8 at the INT8 projections of one Mistral-7B layer
     (layer.cu:487-501,551,575: B int8 [N, K] with per-row scales), for M = 1
     and 64 tokens, against the reference's composition without its cudaMalloc /
     cudaFree (cuda_dequantize_weights into an fp16 buffer, then
-    cuda_gemm_fp16). Weight pools keep the codes cache-cold. Also q_proj at
-    prefill (M = 4096), where cuda_gemm_int8 dequantizes and calls hipBLASLt."""
+    cuda_gemm_fp16). Weight pools keep the codes cache-cold. Also every
+    projection at prefill sizes (PREFILL_M tokens), where cuda_gemm_int8 runs
+    the fused prefill MFMA kernel, against the same composition."""
     rng = np.random.Generator(np.random.PCG64(0))
     H, I = 4096, 14336
     shapes = {"q_proj": (H, H), "k_proj": (H, 1024), "gate_proj": (H, I), "down_proj": (I, H)}
     per_layer = {"q_proj": 2, "k_proj": 2, "gate_proj": 2, "down_proj": 1}   # q+o, k+v, gate+up, down
-    out, layer = {}, {1: [0.0, 0.0], 64: [0.0, 0.0]}
+    out, layer, prefill = {}, {1: [0.0, 0.0], 64: [0.0, 0.0]}, {}
     for name, (K, N) in shapes.items():
         wq = rng.integers(-128, 128, (N, K)).astype(np.int8)
         n = pool_slots(N * K)
@@ -621,21 +643,35 @@ def gemm_extras(L, hip, stream):
             layer[M][1] += per_layer[name] * usc
             cp.free()
             ab.free()
-        if name == "q_proj":
-            M = 4096
+        for M in PREFILL_M:
             ab = DB.from_array(W.round_to(rng.standard_normal((M, K), dtype=np.float32), "f16"))
             cb = DB(2 * M * N)
             us = time_kernel(hip, stream, [lambda: L.cuda_gemm_int8(cb.vp, ab.vp, wp.at(0), sc.vp, M, K, N, True)],
                              launches=8, reps=2)
-            out["q_proj_M4096"] = {"us": us, "TFLOPs": 2 * M * N * K / us / 1e6,
-                                   "note": "dequantize to fp16 + hipBLASLt fp16 GEMM"}
+
+            def comp(M=M, ab=ab, cb=cb):
+                rc = L.cuda_dequantize_weights(deq.vp, wp.at(0), sc.vp, N, K, 1)
+                return rc or L.cuda_gemm_fp16(cb.vp, ab.vp, deq.vp, M, K, N, False, True)
+
+            try:
+                usc = time_kernel(hip, stream, [comp], launches=8, reps=2)
+            except RuntimeError as e:   # hipBLASLt refuses some shapes (status 6 at K = 14336)
+                usc = None
+                print(f"[bench] composed {name} M={M}: {e}", file=sys.stderr, flush=True)
+            out[f"{name}_M{M}"] = {"us": us, "TFLOPs": 2 * M * N * K / us / 1e6, "composed_us": usc,
+                                   "composed_TFLOPs": usc and 2 * M * N * K / usc / 1e6,
+                                   "note": "fused int8 prefill MFMA kernel; composed = dequantize to fp16 + "
+                                           "hipBLASLt fp16 GEMM"}
+            prefill.setdefault(M, [0.0, 0.0])
+            prefill[M][0] += per_layer[name] * us
+            prefill[M][1] += per_layer[name] * (usc or float("nan"))
             ab.free()
             cb.free()
         wp.free()
         sc.free()
         deq.free()
-    for M, (u, c) in layer.items():
-        out[f"mistral7b_layer_M{M}"] = {"us": u, "composed_us": c,
+    for M, (u, c) in list(layer.items()) + list(prefill.items()):
+        out[f"mistral7b_layer_M{M}"] = {"us": u, "composed_us": None if c != c else c,
                                         "note": "q, k, v, o, gate, up, down projections of one layer"}
     return out
 
@@ -903,11 +939,12 @@ def main():
     step_ms, wall_ms, per, nsets, slots, seq = run_layer(L, hip, stream, cfg, args.steps, args.warmup)
     lb = W.layer_bytes(cfg)
     layer_bytes = sum(lb[k] for k in W.LAYER_KERNELS)
+    copy_us = copy_times(hip, stream, [lb[k] for k in W.LAYER_KERNELS])
     kernels = {}
     for k in W.LAYER_KERNELS:
         us = per[k]
         kernels[k] = {"us": us, "GBps": lb[k] / us / 1e3, "frac": lb[k] / us / 1e3 / PEAK_GBPS, "bytes": lb[k],
-                      "buffer_sets": slots[k]}
+                      "buffer_sets": slots[k], "copy_us": copy_us[lb[k]], "vs_copy": copy_us[lb[k]] / us}
     us_layer = sum(kernels[k]["us"] for k in W.LAYER_KERNELS)
     log(f"layer done: {us_layer:.1f} us summed kernel time, {step_ms * 1e3:.1f} us per step")
     qk_bytes = lb["rope_q"] + lb["rope_k"] - 4 * cfg.T
@@ -931,8 +968,10 @@ def main():
             lb2 = W.layer_bytes(c2)
             b2 = sum(lb2[k] for k in W.LAYER_KERNELS)
             u2 = sum(p2[k] for k in W.LAYER_KERNELS)
+            cu2 = copy_times(hip, stream, [lb2[k] for k in W.LAYER_KERNELS])
             extra[key] = {"us_per_layer": u2, "us_per_step": s2 * 1e3, "GBps": b2 / u2 / 1e3,
                           "frac": b2 / u2 / 1e3 / PEAK_GBPS, "layer_bytes": b2, "per_kernel_us": p2,
+                          "per_kernel_copy_us": {k: cu2[lb2[k]] for k in W.LAYER_KERNELS},
                           "fused_layer_variant": fused_layer_report(c2, p2, seq2)}
             if c2.dtype == "bf16":
                 eb = engine_bf16_bytes(c2)
@@ -947,6 +986,10 @@ def main():
                             "change in INTEGRATION.md"}
         log("gather / rmsnorm+int8 / dequant")
         extra.update(extra_kernels(L, hip, stream))
+        sized = [v for v in extra.values() if isinstance(v, dict) and "bytes" in v and "us" in v]
+        xc = copy_times(hip, stream, [v["bytes"] for v in sized])
+        for v in sized:
+            v["copy_us"], v["vs_copy"] = xc[v["bytes"]], xc[v["bytes"]] / v["us"]
 
     dom = "silu_mul"
     roof = {"kernel": "cuda_silu_mul (ng::ew_vec_kernel<_Float16, EW_SILU_MUL, 1>)", "bound": "hbm",
@@ -986,6 +1029,8 @@ def main():
         "host_wall_ms_per_step": wall_ms,
         "layer_bytes": layer_bytes,
         "per_kernel": kernels,
+        "copy_note": "copy_us: a plain device-to-device hipMemcpyAsync moving the kernel's algorithmic bytes "
+                     "(half read, half written), timed the same way; vs_copy = copy_us / us",
         "extra": extra,
         "roofline": roof,
         "cpu_baseline": cpu,

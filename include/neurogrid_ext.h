@@ -108,13 +108,13 @@ int cuda_dequantize_weights(void* output, const void* input, const void* scales,
 int ng_gather_embeddings_checked(void* output, const void* embed_table, const int* d_token_ids,
                                  int hidden_size, int num_tokens, int vocab_size, int* d_error_count);
 
-/* cuda_gemm_int8's weight-streaming path without any allocation. No
- * counterpart in the reference: it is for callers that cannot allocate device
- * memory (code under HIP graph capture, tight serving loops, harnesses that
- * forbid hipMalloc). Arguments and results as cuda_gemm_int8 (the same
- * kernels, bit for bit), for the shapes that path takes: transpose_b,
- * M <= 128, K % 64 == 0 (K % 16 == 0 for M <= 4), 16-byte aligned A and B;
- * other shapes return -1. The split-K partial sums live in a fixed 64 MiB
+/* cuda_gemm_int8's fused int8 paths (weight streaming for M <= 128, prefill
+ * above) without any allocation. No counterpart in the reference: it is for
+ * callers that cannot allocate device memory (code under HIP graph capture,
+ * tight serving loops, harnesses that forbid hipMalloc). Arguments and
+ * results as cuda_gemm_int8 (the same kernels, bit for bit), for the shapes
+ * those paths take: transpose_b, K % 16 == 0 (K % 64 == 0 for 4 < M <= 128),
+ * 16-byte aligned A and B; other shapes return -1. The split-K partial sums live in a fixed 64 MiB
  * device array that each GPU the library runs on holds until the process
  * ends; a shape whose partial sums exceed it returns -1. Calls that overlap
  * on one GPU share that array and race. */

@@ -608,6 +608,193 @@ __global__ __launch_bounds__(256) void split_reduce_kernel(uint16_t* __restrict_
 }
 
 
+// ---- prefill variant (M > 128) ----------------------------------------------
+// Many rows of A: the product is bound by the matrix cores, not by reading
+// the weights. A block computes a BM x BN tile of C (BM = 16 TM WM rows of A,
+// BN = 16 TN WN rows of B) with WM x WN waves, each a TM x TN grid of 16x16
+// MFMA tiles, over a slice of K in steps of 64:
+//   * the A tile (fp16) and the B tile go through LDS; the B codes are
+//     converted to exact fp16 integers once, on their way into LDS, so a code
+//     is converted once per block that uses it and the matrix cores read fp16;
+//   * two LDS buffers: the loads of step kt + 1 are issued before step kt is
+//     multiplied, then stored into the other buffer; one barrier per step;
+//   * rows of 64 k are 128 bytes; piece q (16 bytes) of row r sits at
+//     q xor ((r / 2) mod 8), so that the 16 lanes of an MFMA operand read
+//     (rows r0 .. r0 + 15, one piece) hit 16 different 16-byte slots of the
+//     256 bytes the banks serve per clock;
+//   * A and B are read through buffer resources based at the block's first
+//     row: 32-bit offsets, and rows past M (or N) read zeros;
+//   * tiles are handed out XCD by XCD: consecutive block ids go to different
+//     XCDs, so block b takes tile (b mod 8) * (tiles / 8) + b / 8, and the
+//     tiles of one XCD (and of its L2) are neighbours, grouped kPfGroupM rows
+//     of tiles at a time so that they share rows of A and of B;
+//   * with S > 1 the K steps are split into S slices (slice-major over the
+//     tiles); each block stores its fp32 sums in `part` [S][M][N] and
+//     split_reduce_kernel adds the slices in slice order.
+// Sums in fp32 in MFMA order; scale[n] multiplies the sum, as on the
+// streaming paths. Launch shapes, measured on MI355X with random data
+// (q_proj 4096 x 4096 at M = 4096: 16 waves of 64 x 64 on a 256 x 256 tile,
+// 127 us, against 162 us for 4 waves on 128 x 128 and 169 us for 4 waves of
+// 128 x 128 on 256 x 256, whose fragment loads the compiler serialises
+// behind each group of MFMAs): 256 x 256 with 16 waves and no K slices when
+// that gives 192 tiles or more, otherwise 128 x 128 with 4 waves and enough
+// K slices for about 512 blocks.
+constexpr int kPfBK = 64;
+constexpr int kPfGroupM = 8;
+constexpr int kPfBlocks = 512;
+
+__device__ __forceinline__ int pf_slot(int row, int q) { return row * 8 + (q ^ ((row >> 1) & 7)); }
+
+template <int TM, int TN, int WM, int WN>
+__global__ __launch_bounds__(WM * WN * kWave, 1) void gemm_i8w_prefill_kernel(
+    uint16_t* __restrict__ c, const uint16_t* __restrict__ a, const int8_t* __restrict__ b,
+    const float* __restrict__ scale, float* __restrict__ part, int M, int N, int K, int tiles_m, int tiles_n,
+    int S, int cps) {
+    constexpr int kThreads = WM * WN * kWave;
+    constexpr int BM = WM * TM * 16, BN = WN * TN * 16;
+    constexpr int kAP = BM * 8 / kThreads;  // 16-byte pieces (8 k) of A per thread per step
+    constexpr int kBP = BN * 4 / kThreads;  // 16-code pieces of B per thread per step
+    static_assert(BM * 8 % kThreads == 0 && BN * 4 % kThreads == 0, "tile pieces must divide among the threads");
+    static_assert((kThreads / 8) % 16 == 0 && (kThreads / 4) % 16 == 0, "row strides must keep the swizzle");
+    __shared__ __align__(16) u32x4 lds_a[2][BM * 8];
+    __shared__ __align__(16) u32x4 lds_b[2][BN * 8];
+
+    const int ntiles = tiles_m * tiles_n;
+    int t = blockIdx.x;
+    if ((ntiles * S) % 8 == 0) t = (t % 8) * (ntiles * S / 8) + t / 8;
+    const int sl = t / ntiles;
+    t -= sl * ntiles;
+    const int per_group = kPfGroupM * tiles_n;
+    const int grp0 = (t / per_group) * kPfGroupM;
+    const int gm = min(kPfGroupM, tiles_m - grp0);
+    const int tm = grp0 + (t % per_group) % gm;
+    const int tn = (t % per_group) / gm;
+    const int m0 = tm * BM, n0 = tn * BN;
+
+    const int tid = threadIdx.x;
+    const int lane = tid & (kWave - 1);
+    const int wave = __builtin_amdgcn_readfirstlane(tid / kWave);
+    const int wm = wave / WN, wn = wave % WN;
+
+    const __amdgpu_buffer_rsrc_t rsa = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<uint16_t*>(a + static_cast<size_t>(m0) * K), 0,
+        static_cast<int>(min(static_cast<long long>(M - m0) * K * 2, 0x7fffffffll)), 0x00020000);
+    const __amdgpu_buffer_rsrc_t rsb = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<int8_t*>(b + static_cast<size_t>(n0) * K), 0,
+        static_cast<int>(min(static_cast<long long>(N - n0) * K, 0x7fffffffll)), 0x00020000);
+    // Thread tid loads A pieces (row tid / 8 + j kThreads / 8, piece tid % 8)
+    // and B pieces (row tid / 4 + j kThreads / 4, codes 16 (tid % 4) ..).
+    const int aq = tid & 7, bp = tid & 3;
+    const uint32_t aoff0 = static_cast<uint32_t>((tid >> 3) * K * 2 + 16 * aq);
+    const uint32_t boff0 = static_cast<uint32_t>((tid >> 2) * K + 16 * bp);
+    const uint32_t astride = static_cast<uint32_t>((kThreads / 8) * K * 2);
+    const uint32_t bstride = static_cast<uint32_t>((kThreads / 4) * K);
+    const int aslot0 = pf_slot(tid >> 3, aq);
+    const int bslot0 = pf_slot(tid >> 2, 2 * bp), bslot1 = pf_slot(tid >> 2, 2 * bp + 1);
+
+    f32x4 acc[TM][TN];
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+        for (int jn = 0; jn < TN; ++jn) acc[i][jn] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+
+    const int nk = (K + kPfBK - 1) / kPfBK;
+    const int c0 = sl * cps, c1 = min(nk, c0 + cps);
+    u32x4 ra[kAP], rb[kBP];
+    // Loads of step kt. In a last step that runs past K (K % 64 != 0) the
+    // pieces past K are zeroed in both operands, so that they add nothing (an
+    // inf times a zero would be NaN).
+    auto load = [&](int kt) {
+        const int k0 = kt * kPfBK;
+#pragma unroll
+        for (int j = 0; j < kAP; ++j) ra[j] = __builtin_amdgcn_raw_buffer_load_b128(rsa, aoff0 + j * astride, 2 * k0, 0);
+#pragma unroll
+        for (int j = 0; j < kBP; ++j) rb[j] = __builtin_amdgcn_raw_buffer_load_b128(rsb, boff0 + j * bstride, k0, 0);
+        if (k0 + kPfBK > K) {
+            if (k0 + 8 * aq >= K) {
+#pragma unroll
+                for (int j = 0; j < kAP; ++j) ra[j] = u32x4{0u, 0u, 0u, 0u};
+            }
+            if (k0 + 16 * bp >= K) {
+#pragma unroll
+                for (int j = 0; j < kBP; ++j) rb[j] = u32x4{0u, 0u, 0u, 0u};
+            }
+        }
+    };
+    auto stage = [&](int buf) {
+#pragma unroll
+        for (int j = 0; j < kAP; ++j) lds_a[buf][aslot0 + j * (kThreads / 8) * 8] = ra[j];
+#pragma unroll
+        for (int j = 0; j < kBP; ++j) {
+            f16x8 lo, hi;
+            codes16_to_operands(rb[j], lo, hi);
+            lds_b[buf][bslot0 + j * (kThreads / 4) * 8] = __builtin_bit_cast(u32x4, lo);
+            lds_b[buf][bslot1 + j * (kThreads / 4) * 8] = __builtin_bit_cast(u32x4, hi);
+        }
+    };
+    const int ar0 = wm * TM * 16 + (lane & 15);
+    const int br0 = wn * TN * 16 + (lane & 15);
+    auto frags = [&](int buf, int s2, u32x4 (&af)[TM], u32x4 (&bf)[TN]) {
+        const int q = 4 * s2 + (lane >> 4);
+#pragma unroll
+        for (int i = 0; i < TM; ++i) af[i] = lds_a[buf][pf_slot(ar0 + 16 * i, q)];
+#pragma unroll
+        for (int jn = 0; jn < TN; ++jn) bf[jn] = lds_b[buf][pf_slot(br0 + 16 * jn, q)];
+    };
+    auto mma = [&](const u32x4 (&af)[TM], const u32x4 (&bf)[TN]) {
+#pragma unroll
+        for (int i = 0; i < TM; ++i)
+#pragma unroll
+            for (int jn = 0; jn < TN; ++jn)
+                acc[i][jn] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, af[i]),
+                                                                    __builtin_bit_cast(f16x8, bf[jn]), acc[i][jn],
+                                                                    0, 0, 0);
+    };
+
+    if (c0 < c1) {
+        load(c0);
+        stage(0);
+        __syncthreads();
+        for (int kt = c0; kt < c1; ++kt) {
+            const int buf = (kt - c0) & 1;
+            if (kt + 1 < c1) load(kt + 1);
+            u32x4 af0[TM], bf0[TN], af1[TM], bf1[TN];
+            frags(buf, 0, af0, bf0);
+            frags(buf, 1, af1, bf1);
+            mma(af0, bf0);
+            mma(af1, bf1);
+            if (kt + 1 < c1) stage(buf ^ 1);
+            __syncthreads();
+        }
+    }
+
+    const int mb = m0 + wm * TM * 16 + 4 * (lane >> 4);
+#pragma unroll
+    for (int jn = 0; jn < TN; ++jn) {
+        const int n = n0 + wn * TN * 16 + 16 * jn + (lane & 15);
+        if (n >= N) continue;
+        if (S == 1) {
+            const float sc = scale[n];
+#pragma unroll
+            for (int i = 0; i < TM; ++i)
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    const int m = mb + 16 * i + e;
+                    if (m < M) c[static_cast<size_t>(m) * N + n] = from_f32<f16>(acc[i][jn][e] * sc);
+                }
+        } else {
+            float* mine = part + static_cast<size_t>(sl) * M * N;
+#pragma unroll
+            for (int i = 0; i < TM; ++i)
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    const int m = mb + 16 * i + e;
+                    if (m < M) mine[static_cast<size_t>(m) * N + n] = acc[i][jn][e];
+                }
+        }
+    }
+}
+
 // ---- hipBLASLt path ----------------------------------------------------------
 constexpr size_t kLtWorkspace = size_t(32) << 20;
 
@@ -751,9 +938,44 @@ int gemm_lt(void* c, const void* a, const void* b, const void* q, const void* sc
     return 0;
 }
 
-// `scratch` (scratch_bytes long), when given, holds the partial sums in place
-// of this stream's buffer: nothing is allocated, and a call whose partial sums
-// do not fit is refused.
+// The fp32 partial-sum buffer [S][M][N] of a split-K launch: `scratch` when
+// the caller brings one (refused when too small), else this (device,
+// stream)'s buffer, grown on demand with `lock` (g_mu) taken; the caller
+// keeps the lock until both kernels are enqueued, so that calls from other
+// host threads on the same stream cannot slip a launch between them.
+int partial_buffer(hipStream_t s, int S, int M, int N, int K, float* scratch, size_t scratch_bytes,
+                   std::unique_lock<std::mutex>& lock, float** out) {
+    const size_t need = static_cast<size_t>(S) * M * N * sizeof(float);
+    if (scratch != nullptr) {
+        NG_REQUIRE(need <= scratch_bytes,
+                   "ng_gemm_int8_noalloc: M=%d K=%d N=%d splits K into %d slices whose partial sums need %zu "
+                   "bytes, more than the %zu-byte scratch; call cuda_gemm_int8 instead",
+                   M, K, N, S, need, scratch_bytes);
+        *out = scratch;
+        return 0;
+    }
+    int dev = 0;
+    NG_HIP_CHECK(hipGetDevice(&dev));
+    lock.lock();
+    StreamBuffers* sb = &g_buffers[{dev, s}];
+    if (grow(s, &sb->part, &sb->part_bytes, need) != 0) return -1;
+    *out = static_cast<float*>(sb->part);
+    return 0;
+}
+
+// C = fp16(scale[n] * sum of the S slices of part), slices added in order.
+int launch_reduce(hipStream_t s, uint16_t* c, const float* part, const float* scale, int M, int N, int S) {
+    const size_t mn = static_cast<size_t>(M) * N;
+    if (N % 4 == 0 && aligned16(scale) && aligned8(c))
+        split_reduce_kernel<true><<<dim3(static_cast<unsigned>((mn / 4 + 255) / 256)), dim3(256), 0, s>>>(
+            c, part, scale, M, N, S);
+    else
+        split_reduce_kernel<false><<<dim3(static_cast<unsigned>((mn + 255) / 256)), dim3(256), 0, s>>>(
+            c, part, scale, M, N, S);
+    NG_CHECK_LAUNCH("cuda_gemm_int8");
+    return 0;
+}
+
 template <int MT, int W, int G>
 int launch_split(uint16_t* c, const uint16_t* a, const int8_t* b, const float* scale, int M, int N, int K,
                  float* scratch, size_t scratch_bytes) {
@@ -773,36 +995,11 @@ int launch_split(uint16_t* c, const uint16_t* a, const int8_t* b, const float* s
     const hipStream_t s = stream();
     float* part = nullptr;
     std::unique_lock<std::mutex> lock(g_mu, std::defer_lock);
-    if (S > 1 && scratch != nullptr) {
-        const size_t need = static_cast<size_t>(S) * M * N * sizeof(float);
-        NG_REQUIRE(need <= scratch_bytes,
-                   "ng_gemm_int8_noalloc: M=%d K=%d N=%d splits K into %d slices whose partial sums need %zu "
-                   "bytes, more than the %zu-byte scratch; call cuda_gemm_int8 instead",
-                   M, K, N, S, need, scratch_bytes);
-        part = scratch;
-    } else if (S > 1) {
-        int dev = 0;
-        NG_HIP_CHECK(hipGetDevice(&dev));
-        lock.lock();
-        StreamBuffers* sb = &g_buffers[{dev, s}];
-        if (grow(s, &sb->part, &sb->part_bytes, static_cast<size_t>(S) * M * N * sizeof(float)) != 0)
-            return -1;
-        part = static_cast<float*>(sb->part);
-    }
+    if (S > 1 && partial_buffer(s, S, M, N, K, scratch, scratch_bytes, lock, &part) != 0) return -1;
     gemm_i8w_split_kernel<MT, W, G><<<dim3(static_cast<unsigned>(tiles * S)), dim3(G * W * kWave), 0, s>>>(
         c, a, b, scale, part, M, N, K, S, tiles, cps);
     NG_CHECK_LAUNCH("cuda_gemm_int8");
-    if (S > 1) {
-        const size_t mn = static_cast<size_t>(M) * N;
-        if (N % 4 == 0 && aligned16(scale) && aligned8(c))
-            split_reduce_kernel<true><<<dim3(static_cast<unsigned>((mn / 4 + 255) / 256)), dim3(256), 0, s>>>(
-                c, part, scale, M, N, S);
-        else
-            split_reduce_kernel<false><<<dim3(static_cast<unsigned>((mn + 255) / 256)), dim3(256), 0, s>>>(
-                c, part, scale, M, N, S);
-        NG_CHECK_LAUNCH("cuda_gemm_int8");
-    }
-    return 0;
+    return S > 1 ? launch_reduce(s, c, part, scale, M, N, S) : 0;
 }
 
 // Kernel and tile shape by M, K and N, from sweeps on MI355X over K x N in
@@ -845,6 +1042,49 @@ int gemm_i8w(void* c, const void* a, const void* b, const void* scale, int M, in
         return wide ? launch_split<1, 4, 2>(cp, ap, bp, sp, M, N, K, scratch, scratch_bytes)
                     : launch_split<1, 4, 1>(cp, ap, bp, sp, M, N, K, scratch, scratch_bytes);
     return launch_i8w<1, 1, 8, 4>(cp, ap, bp, sp, M, N, K);
+}
+
+// The prefill kernel takes transpose_b, K % 16 == 0 and 16-byte aligned A and B.
+bool use_prefill(const void* a, const void* b, int M, int K, int N, bool transpose_b) {
+    return transpose_b && K % 16 == 0 && aligned16(a) && aligned16(b) &&
+           static_cast<long long>(M) * K * 2 < (1ll << 31) && static_cast<long long>(N) * K < (1ll << 31);
+}
+
+template <int TM, int TN, int WM, int WN>
+int launch_prefill(uint16_t* c, const uint16_t* a, const int8_t* b, const float* scale, int M, int N, int K,
+                   float* scratch, size_t scratch_bytes) {
+    constexpr int BM = WM * TM * 16, BN = WN * TN * 16;
+    const int tiles_m = (M + BM - 1) / BM, tiles_n = (N + BN - 1) / BN;
+    const int tiles = tiles_m * tiles_n;
+    const int nk = (K + kPfBK - 1) / kPfBK;
+    // K slices for about kPfBlocks blocks, at most 8, each of 4 steps or
+    // more; none for 256 x 256 tiles, which are only chosen when there are
+    // enough of them to fill the CUs.
+    int S = BM * BN >= 65536 ? 1 : max(1, min((kPfBlocks + tiles - 1) / tiles, min(8, nk / 4)));
+    const int cps = (nk + S - 1) / S;
+    S = (nk + cps - 1) / cps;
+    const hipStream_t s = stream();
+    float* part = nullptr;
+    std::unique_lock<std::mutex> lock(g_mu, std::defer_lock);
+    if (S > 1 && partial_buffer(s, S, M, N, K, scratch, scratch_bytes, lock, &part) != 0) return -1;
+    gemm_i8w_prefill_kernel<TM, TN, WM, WN><<<dim3(static_cast<unsigned>(tiles * S)), dim3(WM * WN * kWave), 0, s>>>(
+        c, a, b, scale, part, M, N, K, tiles_m, tiles_n, S, cps);
+    NG_CHECK_LAUNCH("cuda_gemm_int8");
+    return S > 1 ? launch_reduce(s, c, part, scale, M, N, S) : 0;
+}
+
+// Tile shape by the number of tiles (see the prefill kernel): 256 x 256
+// when that gives at least 192 tiles (three quarters of the CUs), otherwise
+// 128 x 128 with K slices.
+int gemm_prefill(void* c, const void* a, const void* b, const void* scale, int M, int K, int N,
+                 float* scratch = nullptr, size_t scratch_bytes = 0) {
+    auto* cp = static_cast<uint16_t*>(c);
+    auto* ap = static_cast<const uint16_t*>(a);
+    auto* bp = static_cast<const int8_t*>(b);
+    auto* sp = static_cast<const float*>(scale);
+    const long long tiles256 = static_cast<long long>((M + 255) / 256) * ((N + 255) / 256);
+    if (tiles256 >= 192) return launch_prefill<4, 4, 4, 4>(cp, ap, bp, sp, M, N, K, scratch, scratch_bytes);
+    return launch_prefill<4, 4, 2, 2>(cp, ap, bp, sp, M, N, K, scratch, scratch_bytes);
 }
 
 // The weight-streaming path takes transpose_b, M <= kMaxFusedM, 16-byte aligned
@@ -921,6 +1161,7 @@ extern "C" int cuda_gemm_int8(void* c, const void* a, const void* b, const void*
     NG_REQUIRE(c && a && b && scale, "cuda_gemm_int8: null pointer");
     NG_REQUIRE(M > 0 && K > 0 && N > 0, "cuda_gemm_int8: M=%d K=%d N=%d must be > 0", M, K, N);
     if (use_i8w(a, b, M, K, N, transpose_b)) return gemm_i8w(c, a, b, scale, M, K, N);
+    if (use_prefill(a, b, M, K, N, transpose_b)) return gemm_prefill(c, a, b, scale, M, K, N);
     return gemm_lt(c, a, nullptr, b, scale, M, K, N, false, transpose_b);
 }
 
@@ -935,14 +1176,15 @@ extern "C" int ng_gemm_int8_noalloc(void* c, const void* a, const void* b, const
                                     bool transpose_b) {
     NG_REQUIRE(c && a && b && scale, "ng_gemm_int8_noalloc: null pointer");
     NG_REQUIRE(M > 0 && K > 0 && N > 0, "ng_gemm_int8_noalloc: M=%d K=%d N=%d must be > 0", M, K, N);
-    NG_REQUIRE(use_i8w(a, b, M, K, N, transpose_b),
-               "ng_gemm_int8_noalloc: M=%d K=%d N=%d transpose_b=%d is outside the weight-streaming path "
-               "(transpose_b, M <= %d, K %% 64 == 0 or K %% 16 == 0 with M <= 4, 16-byte aligned A and B), "
-               "which is the only one that runs without allocating; call cuda_gemm_int8 instead",
-               M, K, N, static_cast<int>(transpose_b), kMaxFusedM);
+    const bool stream_path = use_i8w(a, b, M, K, N, transpose_b);
+    NG_REQUIRE(stream_path || use_prefill(a, b, M, K, N, transpose_b),
+               "ng_gemm_int8_noalloc: M=%d K=%d N=%d transpose_b=%d is outside the paths that run without "
+               "allocating (transpose_b, K %% 16 == 0 (K %% 64 == 0 for 4 < M <= %d), 16-byte aligned A and B); "
+               "call cuda_gemm_int8 instead", M, K, N, static_cast<int>(transpose_b), kMaxFusedM);
     int dev = 0;
     NG_HIP_CHECK(hipGetDevice(&dev));
     float* part = nullptr;
     if (scratch_ptr(dev, &part) != 0) return -1;
-    return gemm_i8w(c, a, b, scale, M, K, N, part, kNoAllocScratchBytes);
+    if (stream_path) return gemm_i8w(c, a, b, scale, M, K, N, part, kNoAllocScratchBytes);
+    return gemm_prefill(c, a, b, scale, M, K, N, part, kNoAllocScratchBytes);
 }

@@ -96,7 +96,7 @@ def test_argument_errors_return_minus_one_without_touching_the_gpu(capfd):
     assert L.cuda_gemm_int8(p, p, p, p, 4, 0, 16, True) == -1
     assert L.cuda_gemm_fp16(p, None, p, 4, 64, 16, False, False) == -1
     assert L.ng_gemm_int8_noalloc(p, p, None, p, 4, 64, 16, True) == -1
-    assert L.ng_gemm_int8_noalloc(p, p, p, p, 129, 64, 16, True) == -1     # outside the streaming path
+    assert L.ng_gemm_int8_noalloc(p, p, p, p, 129, 72, 16, True) == -1     # K % 16 != 0: hipBLASLt path
     assert L.ng_gemm_int8_noalloc(p, p, p, p, 4, 64, 16, False) == -1
     err = capfd.readouterr().err
     assert "neurogrid-amd:" in err and "null pointer" in err

@@ -160,15 +160,16 @@ def _ops():
     add("cuda_dequantize_weights_col", {"y": (E2, (GK, GN))},
         lambda L, i, o: L.cuda_dequantize_weights(o["y"].vp, i["wq_kn"].vp, i["wsc"].vp, GK, GN, 0))
     # GEMMs: GEMV (M <= 4), small-M MFMA, split-K at three tile heights, the
-    # library path (M > 128 and transpose_b false), and the fp16 GEMM.
+    # prefill kernel with two K slices (M > 128), the library path
+    # (transpose_b false), and the fp16 GEMM.
     for m in (1, 3, 16, 40, 64, 100):
         add(f"cuda_gemm_int8_M{m}", {"y": (E2, (m, GN))},
             lambda L, i, o, m=m: L.cuda_gemm_int8(o["y"].vp, i[f"a{m}"].vp, i["wq"].vp, i["wsc"].vp, m, GK, GN, True))
     # N >= 12288: one slice of K, two wave groups per block
     add("cuda_gemm_int8_M40_wide", {"y": (E2, (40, GNW))},
         lambda L, i, o: L.cuda_gemm_int8(o["y"].vp, i["a40"].vp, i["wq_wide"].vp, i["wsc_wide"].vp, 40, GK, GNW, True))
-    add("cuda_gemm_int8_M200_library", {"y": (E2, (200, GN))},
-        lambda L, i, o: L.cuda_gemm_int8(o["y"].vp, i["a200"].vp, i["wq"].vp, i["wsc"].vp, 200, GK, GN, True), False)
+    add("cuda_gemm_int8_M200_prefill", {"y": (E2, (200, GN))},
+        lambda L, i, o: L.cuda_gemm_int8(o["y"].vp, i["a200"].vp, i["wq"].vp, i["wsc"].vp, 200, GK, GN, True))
     add("cuda_gemm_int8_kn_library", {"y": (E2, (16, GN))},
         lambda L, i, o: L.cuda_gemm_int8(o["y"].vp, i["a16"].vp, i["wq_kn"].vp, i["wsc"].vp, 16, GK, GN, False),
         False)

@@ -158,11 +158,44 @@ def test_int8_weight_streaming_inf_activations(lib, M, K, N):
     assert (got[~nan_w] == want[~nan_w]).all(), "signed infinities differ"
 
 
-# The dequantize + hipBLASLt path: B [K, N] with per-column scales, M > 128 or
-# K not a multiple of 64.
+# The prefill kernel (transpose_b, M > 128, K % 16 == 0): ragged M and N,
+# K with a partial last step of 128 (K % 128 = 64, 16), full model shapes.
+PREFILL = [(129, 4096, 1024), (256, 4096, 4096), (4096, 4096, 1024), (200, 4160, 1000), (300, 1040, 384),
+           (4100, 1024, 300), (130, 14336, 256), (1000, 4096, 14336), (2049, 2048, 2056), (640, 16, 64)]
+
+
+@pytest.mark.parametrize("M,K,N", PREFILL)
+def test_int8_prefill_bit_exact(lib, M, K, N):
+    banner(f"gemm_int8 prefill exact M={M} K={K} N={N}")
+    a = exact_activations(M, K)
+    q = codes((N, K))
+    scale = RNG.uniform(1e-3, 1e-2, N).astype(np.float16).astype(np.float32)
+    got = gemm_int8(lib, a, q, scale, M, K, N, True)
+    S = f16val(a) @ q.astype(np.float64).T
+    want = (S.astype(np.float32) * scale[None, :]).astype(np.float16).view(np.uint16)
+    assert_bits_equal(got, want, "C")
+
+
+@pytest.mark.parametrize("M,K,N", [(4096, 4096, 4096), (512, 14336, 1024), (300, 1040, 4100)])
+def test_int8_prefill_random(lib, ora, M, K, N):
+    banner(f"gemm_int8 prefill random M={M} K={K} N={N}")
+    a = f16bits(RNG.standard_normal((M, K)))
+    q = codes((N, K))
+    scale = RNG.uniform(1e-3, 1e-2, N).astype(np.float32)
+    got = gemm_int8(lib, a, q, scale, M, K, N, True)
+    assert_within_bound(got, a, q, scale, True, "C", ora)
+
+
+@pytest.mark.parametrize("M,K,N", [(256, 4160, 512), (129, 1040, 300), (1024, 4096, 1024)])
+def test_int8_prefill_inf_activations(lib, M, K, N):
+    test_int8_weight_streaming_inf_activations(lib, M, K, N)
+
+
+# The dequantize + hipBLASLt path: B [K, N] with per-column scales, or
+# transpose_b with K not a multiple of 16 (of 64 for 4 < M <= 128).
 LIBRARY = [
-    (4, 256, 128, False), (129, 4096, 1024, True), (256, 1024, 512, False), (7, 200, 96, True),
-    (512, 4096, 4096, True), (33, 1024, 4096, False),
+    (4, 256, 128, False), (129, 4104, 1024, True), (256, 1024, 512, False), (7, 200, 96, True),
+    (512, 4104, 4096, True), (33, 1024, 4096, False),
 ]
 
 
@@ -179,7 +212,7 @@ def test_int8_dequant_library_bit_exact(lib, M, K, N, tb):
     assert_bits_equal(got, S.astype(np.float16).view(np.uint16), "C")
 
 
-@pytest.mark.parametrize("M,K,N,tb", [(129, 4096, 1024, True), (16, 1024, 512, False), (100, 960, 200, True)])
+@pytest.mark.parametrize("M,K,N,tb", [(129, 4104, 1024, True), (16, 1024, 512, False), (100, 960, 200, True)])
 def test_int8_dequant_library_random(lib, ora, M, K, N, tb):
     banner(f"gemm_int8 library random M={M} K={K} N={N} tb={tb}")
     a = f16bits(RNG.standard_normal((M, K)))
@@ -190,8 +223,8 @@ def test_int8_dequant_library_random(lib, ora, M, K, N, tb):
 
 
 def test_int8_paths_agree(lib, ora):
-    """The same product through both paths (M <= 128 streams, M = 129 goes
-    through the library): rows shared by the two calls agree to the bound."""
+    """The same product through both kernel families (M <= 128 streams the
+    weights, M = 129 takes the prefill kernel): both within the bound."""
     banner("gemm_int8 both paths")
     K, N = 4096, 2048
     a = f16bits(RNG.standard_normal((129, K)))
@@ -199,11 +232,11 @@ def test_int8_paths_agree(lib, ora):
     scale = RNG.uniform(1e-3, 1e-2, N).astype(np.float32)
     big = gemm_int8(lib, a, q, scale, 129, K, N, True)
     small = gemm_int8(lib, a[:128], q, scale, 128, K, N, True)
-    assert_within_bound(big[:128], a[:128], q, scale, True, "library", ora)
+    assert_within_bound(big[:128], a[:128], q, scale, True, "prefill", ora)
     assert_within_bound(small, a[:128], q, scale, True, "streaming", ora)
 
 
-@pytest.mark.parametrize("M", [16, 64])
+@pytest.mark.parametrize("M", [16, 64, 300, 2048])
 def test_int8_streaming_is_deterministic(lib, M):
     banner(f"gemm_int8 streaming repeat M={M}")
     K, N = 4096, 4096

@@ -1,12 +1,12 @@
-"""ng_gemm_int8_noalloc: cuda_gemm_int8's weight-streaming path with its
-split-K partial sums in the library's fixed device array instead of an
-allocated buffer.
+"""ng_gemm_int8_noalloc: cuda_gemm_int8's weight-streaming (M <= 128) and
+prefill (M > 128) paths with their split-K partial sums in the library's
+fixed device array instead of an allocated buffer.
 
 Checked through the C ABI against cuda_gemm_int8 itself (the same kernels and
 launch shapes, so the bar is bit-exact): two calls in a row, the second with a
 smaller input, so that the second reads none of the first call's leftovers;
 then shapes covering every kernel family, and device memory unchanged across
-calls. Shapes outside the streaming path are refused on the host.
+calls. Shapes that only the hipBLASLt path takes are refused on the host.
 """
 from __future__ import annotations
 
@@ -55,8 +55,11 @@ def test_noalloc_two_calls_second_smaller(lib):
 
 # GEMV (M <= 4), the small-M MFMA kernel, the split kernel with 1 to 8 slices
 # (4 and 8 waves), and two wave groups per block (N >= 12288 at K < 8192).
+# The prefill kernel with 1 to 8 slices of K, both tile shapes, ragged M and N.
 SHAPES = [(1, 4096, 4096), (4, 2064, 33), (8, 4096, 4096), (12, 1088, 4096), (33, 4096, 1024),
-          (64, 4096, 14336), (128, 14336, 4096), (100, 8256, 384), (128, 4096, 1024), (3, 4096, 12300)]
+          (64, 4096, 14336), (128, 14336, 4096), (100, 8256, 384), (128, 4096, 1024), (3, 4096, 12300),
+          (129, 256, 64), (200, 4096, 1000), (512, 4096, 4096), (300, 14336, 4096), (1024, 4096, 14336),
+          (3072, 4096, 4096)]
 
 
 @pytest.mark.parametrize("M,K,N", SHAPES)
@@ -70,7 +73,7 @@ def test_noalloc_allocates_nothing(lib):
     """Device memory in use is the same before and after a run of calls with
     shapes not seen before (the library's own buffers would grow)."""
     banner("ng_gemm_int8_noalloc device memory unchanged")
-    shapes = [(96, 14336, 4096), (48, 8192, 8192), (2, 1024, 512)]
+    shapes = [(96, 14336, 4096), (48, 8192, 8192), (2, 1024, 512), (384, 4096, 4096), (2000, 1024, 8000)]
     bufs = []
     for M, K, N in shapes:
         ab, qb, sb = inputs(M, K, N)
@@ -87,10 +90,10 @@ def test_noalloc_allocates_nothing(lib):
 
 
 def test_noalloc_refuses_other_paths(lib, capfd):
-    banner("ng_gemm_int8_noalloc refuses shapes outside the streaming path")
+    banner("ng_gemm_int8_noalloc refuses shapes that only the hipBLASLt path takes")
     ab, qb, sb = inputs(129, 256, 64)
     cb = empty(2 * 129 * 64)
-    assert lib.ng_gemm_int8_noalloc(cb.vp, ab.vp, qb.vp, sb.vp, 129, 256, 64, True) == -1   # M > 128
+    assert lib.ng_gemm_int8_noalloc(cb.vp, ab.vp, qb.vp, sb.vp, 129, 200, 64, True) == -1   # M > 128, K % 16 != 0
     assert lib.ng_gemm_int8_noalloc(cb.vp, ab.vp, qb.vp, sb.vp, 4, 256, 64, False) == -1    # not transpose_b
     assert lib.ng_gemm_int8_noalloc(cb.vp, ab.vp, qb.vp, sb.vp, 8, 200, 64, True) == -1     # K % 64 != 0
     assert "call cuda_gemm_int8 instead" in capfd.readouterr().err
