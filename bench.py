@@ -58,7 +58,7 @@ PEAK_GBPS = 8000.0  # MI355X HBM3E, AMD published
 METRIC = "fused-kernel HBM GB/s (% of peak) + µs/layer at Mistral-7B shapes"
 ROTATE_BYTES = 1536 << 20  # layer-step rotation: > 6x the 256 MB Infinity Cache
 POOL_BYTES = 1 << 30       # per-kernel pools: bytes touched between reuses of a buffer
-TRAFFIC_FILE = ROOT / "profiles" / "traffic_mistral7b_prefill.json"
+TRAFFIC_FILE = ROOT / "profiles" / "memory_bound_kernels_hbm_traffic.json"
 
 
 class Hip:
