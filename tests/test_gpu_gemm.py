@@ -160,8 +160,11 @@ def test_int8_weight_streaming_inf_activations(lib, M, K, N):
 
 # The prefill kernel (transpose_b, M > 128, K % 16 == 0): ragged M and N,
 # K with a partial last step of 128 (K % 128 = 64, 16), full model shapes.
+# 256 x 256 tiles from 192 of them on: 1000 x 14336, 777 x 16000 (ragged in M
+# and N), 3072 x 4096, 1000 x 4112 x 12300 (K % 64 = 16).
 PREFILL = [(129, 4096, 1024), (256, 4096, 4096), (4096, 4096, 1024), (200, 4160, 1000), (300, 1040, 384),
-           (4100, 1024, 300), (130, 14336, 256), (1000, 4096, 14336), (2049, 2048, 2056), (640, 16, 64)]
+           (4100, 1024, 300), (130, 14336, 256), (1000, 4096, 14336), (2049, 2048, 2056), (640, 16, 64),
+           (777, 1024, 16000), (3072, 4096, 4096), (1000, 4112, 12300)]
 
 
 @pytest.mark.parametrize("M,K,N", PREFILL)
@@ -176,7 +179,7 @@ def test_int8_prefill_bit_exact(lib, M, K, N):
     assert_bits_equal(got, want, "C")
 
 
-@pytest.mark.parametrize("M,K,N", [(4096, 4096, 4096), (512, 14336, 1024), (300, 1040, 4100)])
+@pytest.mark.parametrize("M,K,N", [(4096, 4096, 4096), (512, 14336, 1024), (300, 1040, 4100), (2048, 14336, 4096)])
 def test_int8_prefill_random(lib, ora, M, K, N):
     banner(f"gemm_int8 prefill random M={M} K={K} N={N}")
     a = f16bits(RNG.standard_normal((M, K)))
@@ -186,7 +189,7 @@ def test_int8_prefill_random(lib, ora, M, K, N):
     assert_within_bound(got, a, q, scale, True, "C", ora)
 
 
-@pytest.mark.parametrize("M,K,N", [(256, 4160, 512), (129, 1040, 300), (1024, 4096, 1024)])
+@pytest.mark.parametrize("M,K,N", [(256, 4160, 512), (129, 1040, 300), (1024, 4096, 1024), (777, 1024, 16000)])
 def test_int8_prefill_inf_activations(lib, M, K, N):
     test_int8_weight_streaming_inf_activations(lib, M, K, N)
 
