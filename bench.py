@@ -383,6 +383,14 @@ def run_layer(L, hip, stream, cfg, steps, warmup, kernel_launches=24, kernel_rep
         g.destroy()
         for p in pools:
             p.free()
+    if cfg.dtype == "bf16":
+        eng = {}
+        for name, make in engine_bf16_pools_for(L, hip, cfg, d, shared):
+            thunks, pools = make()
+            eng[name] = time_pool_kernel(hip, stream, thunks, kernel_launches, kernel_reps)
+            for p in pools:
+                p.free()
+        seq["engine_bf16_kernels_us"] = eng
     del d
     for b in shared.values():
         b.free()
@@ -870,7 +878,8 @@ def log_profile(label, dispatches, warmup):
 def engine_bf16_pools_for(L, hip, cfg, d, shared):
     """The kernels of the bf16 engine's unfused sequence that the fused layer
     does not launch (engine_bf16_launches), with buffer pools as in
-    kernel_pools_for: RMSNorm in place, add, SiLU in place, mul in place."""
+    kernel_pools_for: RMSNorm in place, add, SiLU in place, mul in place, and
+    the dtype conversions the bf16 layer runs around attention."""
     T, H, I, e = cfg.T, cfg.H, cfg.I, cfg.e
     eps = C.c_float(cfg.eps)
     th, ti = T * H * e, T * I * e
@@ -888,6 +897,21 @@ def engine_bf16_pools_for(L, hip, cfg, d, shared):
     yield mk("add", 3 * th, [(th, d["x"]), (th, d["residual"])], lambda a, r: L.cuda_bf16_add(a, a, r, T * H))
     yield mk("silu", 2 * ti, [(ti, d["gate"])], lambda g: L.cuda_bf16_silu(g, g, T * I))
     yield mk("mul", 3 * ti, [(ti, d["gate"]), (ti, d["up"])], lambda g, u: L.cuda_bf16_mul(g, g, u, T * I))
+    # The conversions around attention (layer.cu:1537-1543,1574): Q, K (V is
+    # the same shape as K) bf16 -> fp16, and the attention output fp16 -> bf16.
+    nq, nk = T * cfg.nq * cfg.D, T * cfg.nkv * cfg.D
+    xh = (d["x"].astype(np.uint32) << 16).view(np.float32).astype(np.float16).view(np.uint16)
+    yield mk("cvt_q", 4 * nq, [(2 * nq, d["q"]), (2 * nq, None)], lambda q, o: L.cuda_bf16_to_fp16(o, q, nq))
+    yield mk("cvt_k", 4 * nk, [(2 * nk, d["k"]), (2 * nk, None)], lambda k, o: L.cuda_bf16_to_fp16(o, k, nk))
+    yield mk("cvt_attn_out", 2 * th, [(th, xh), (th, None)], lambda x, o: L.cuda_fp16_to_bf16(o, x, T * H))
+
+
+def engine_bf16_kernel_bytes(cfg):
+    """Algorithmic bytes of engine_bf16_pools_for's kernels."""
+    T, H, I, e = cfg.T, cfg.H, cfg.I, cfg.e
+    return {"rmsnorm_inplace": 2 * T * H * e + H * e, "add": 3 * T * H * e, "silu": 2 * T * I * e,
+            "mul": 3 * T * I * e, "cvt_q": 4 * T * cfg.nq * cfg.D, "cvt_k": 4 * T * cfg.nkv * cfg.D,
+            "cvt_attn_out": 4 * T * H}
 
 
 # ----------------------------------------------------------------------------- main
@@ -976,8 +1000,11 @@ def main():
             if c2.dtype == "bf16":
                 eb = engine_bf16_bytes(c2)
                 eu = seq2["engine_bf16_step_ms"] * 1e3
+                ebk = engine_bf16_kernel_bytes(c2)
                 extra[key]["engine_bf16_unfused"] = {
                     "us_per_step": eu, "layer_bytes": eb,
+                    "kernels": {k: {"us": u, "bytes": ebk[k], "frac": ebk[k] / u / 1e3 / PEAK_GBPS}
+                                for k, u in seq2["engine_bf16_kernels_us"].items()},
                     "sequence": ["copy residual", "rmsnorm", "rope_q", "rope_k", "add", "copy residual",
                                  "rmsnorm (in place)", "silu (in place)", "mul (in place)", "add"],
                     "note": "the bf16 engine's own sequence (layer.cu:1497-1615: two device copies, RMSNorm, "

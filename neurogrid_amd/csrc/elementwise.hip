@@ -176,34 +176,51 @@ __device__ __forceinline__ void cvt_store1(void* out, size_t i, float v) {
     else static_cast<uint16_t*>(out)[i] = from_f32<bf16>(v);
 }
 
+// One 8-element vector per thread, one-wave workgroups, as the element-wise
+// kernels (timed the same as a grid-stride loop over 64 workgroups per CU).
 template <int K>
-__global__ __launch_bounds__(kEwThreads) void cvt_kernel(void* out, const void* in, size_t n, int vec) {
+__global__ __launch_bounds__(kEwThreads) void cvt_vec_kernel(void* out, const void* in, size_t nvec) {
+    const size_t i = static_cast<size_t>(blockIdx.x) * kEwThreads + threadIdx.x;
+    if (i >= nvec) return;
+    float f[8];
+    cvt_load8<K>(in, i * 8, f);
+    cvt_store8<K>(out, i * 8, f);
+}
+
+// Elements [start, n) one per thread per step (the tail, or unaligned buffers).
+template <int K>
+__global__ __launch_bounds__(kEwThreads) void cvt_scalar_kernel(void* out, const void* in, size_t start, size_t n) {
     const size_t stride = static_cast<size_t>(gridDim.x) * kEwThreads;
-    const size_t t0 = static_cast<size_t>(blockIdx.x) * kEwThreads + threadIdx.x;
-    if (vec) {
-        const size_t nvec = n / 8;
-        for (size_t i = t0; i < nvec; i += stride) {
-            float f[8];
-            cvt_load8<K>(in, i * 8, f);
-            cvt_store8<K>(out, i * 8, f);
-        }
-        for (size_t i = nvec * 8 + t0; i < n; i += stride) cvt_store1<K>(out, i, cvt_load1<K>(in, i));
-    } else {
-        for (size_t i = t0; i < n; i += stride) cvt_store1<K>(out, i, cvt_load1<K>(in, i));
-    }
+    for (size_t i = start + static_cast<size_t>(blockIdx.x) * kEwThreads + threadIdx.x; i < n; i += stride)
+        cvt_store1<K>(out, i, cvt_load1<K>(in, i));
+}
+
+// Grid for one thread per unit, or for a grid-stride loop over a tail.
+static unsigned ew_blocks(size_t units, size_t cap) {
+    size_t blocks = (units + kEwThreads - 1) / kEwThreads;
+    if (blocks < 1) blocks = 1;
+    if (blocks > cap) blocks = cap;
+    return static_cast<unsigned>(blocks);
 }
 
 template <int K>
 static int launch_cvt(const char* name, void* out, const void* in, size_t n) {
     NG_REQUIRE(out && in, "%s: null pointer", name);
     NG_REQUIRE(n > 0, "%s: num_elements must be > 0", name);
-    const int vec = aligned16(out) && aligned16(in);
-    size_t blocks = (n / 8 + kEwThreads - 1) / kEwThreads;
-    if (blocks < 1) blocks = 1;
-    const size_t cap = static_cast<size_t>(device_cu_count()) * 64;  // 64 one-wave workgroups per CU
-    if (blocks > cap) blocks = cap;
-    cvt_kernel<K><<<dim3(static_cast<unsigned>(blocks)), dim3(kEwThreads), 0, stream()>>>(out, in, n, vec);
-    NG_CHECK_LAUNCH(name);
+    size_t done = 0;
+    if (aligned16(out) && aligned16(in)) {
+        const size_t nvec = n / 8;
+        NG_REQUIRE(nvec / kEwThreads < 0xffffffffull, "%s: tensor too large", name);
+        if (nvec > 0) {
+            cvt_vec_kernel<K><<<dim3(ew_blocks(nvec, ~0u)), dim3(kEwThreads), 0, stream()>>>(out, in, nvec);
+            NG_CHECK_LAUNCH(name);
+        }
+        done = nvec * 8;
+    }
+    if (done < n) {
+        cvt_scalar_kernel<K><<<dim3(ew_blocks(n - done, 65536)), dim3(kEwThreads), 0, stream()>>>(out, in, done, n);
+        NG_CHECK_LAUNCH(name);
+    }
     return 0;
 }
 
@@ -227,23 +244,21 @@ __device__ __forceinline__ uint32_t bf16_to_f16_trunc(uint32_t b) {
     return sign | mag;
 }
 
-__global__ __launch_bounds__(kEwThreads) void bf16_to_f16_trunc_kernel(uint16_t* out, const uint16_t* in, size_t n,
-                                                                       int vec) {
-    const size_t stride = static_cast<size_t>(gridDim.x) * kEwThreads;
-    const size_t t0 = static_cast<size_t>(blockIdx.x) * kEwThreads + threadIdx.x;
-    size_t done = 0;
-    if (vec) {
-        const size_t nvec = n / 8;
-        for (size_t i = t0; i < nvec; i += stride) {
-            u32x4 v = ld16_stream(in + i * 8);
+__global__ __launch_bounds__(kEwThreads) void bf16_to_f16_trunc_vec_kernel(uint16_t* out, const uint16_t* in,
+                                                                           size_t nvec) {
+    const size_t i = static_cast<size_t>(blockIdx.x) * kEwThreads + threadIdx.x;
+    if (i >= nvec) return;
+    u32x4 v = ld16_stream(in + i * 8);
 #pragma unroll
-            for (int j = 0; j < 4; ++j)
-                v[j] = bf16_to_f16_trunc(v[j] & 0xffffu) | (bf16_to_f16_trunc(v[j] >> 16) << 16);
-            st16_stream(out + i * 8, v);
-        }
-        done = nvec * 8;
-    }
-    for (size_t i = done + t0; i < n; i += stride) out[i] = static_cast<uint16_t>(bf16_to_f16_trunc(in[i]));
+    for (int j = 0; j < 4; ++j) v[j] = bf16_to_f16_trunc(v[j] & 0xffffu) | (bf16_to_f16_trunc(v[j] >> 16) << 16);
+    st16_stream(out + i * 8, v);
+}
+
+__global__ __launch_bounds__(kEwThreads) void bf16_to_f16_trunc_scalar_kernel(uint16_t* out, const uint16_t* in,
+                                                                              size_t start, size_t n) {
+    const size_t stride = static_cast<size_t>(gridDim.x) * kEwThreads;
+    for (size_t i = start + static_cast<size_t>(blockIdx.x) * kEwThreads + threadIdx.x; i < n; i += stride)
+        out[i] = static_cast<uint16_t>(bf16_to_f16_trunc(in[i]));
 }
 
 }  // namespace ng
@@ -298,13 +313,21 @@ extern "C" int ng_fp16_to_fp32(void* output, const void* input, size_t n) {
 extern "C" int ng_bf16_to_fp16_truncate(void* output, const void* input, size_t n) {
     NG_REQUIRE(output && input, "ng_bf16_to_fp16_truncate: null pointer");
     NG_REQUIRE(n > 0, "ng_bf16_to_fp16_truncate: num_elements must be > 0");
-    const int vec = aligned16(output) && aligned16(input);
-    size_t blocks = (n / 8 + kEwThreads - 1) / kEwThreads;
-    if (blocks < 1) blocks = 1;
-    const size_t cap = static_cast<size_t>(device_cu_count()) * 64;  // 64 one-wave workgroups per CU
-    if (blocks > cap) blocks = cap;
-    bf16_to_f16_trunc_kernel<<<dim3(static_cast<unsigned>(blocks)), dim3(kEwThreads), 0, stream()>>>(
-        static_cast<uint16_t*>(output), static_cast<const uint16_t*>(input), n, vec);
+    auto* o = static_cast<uint16_t*>(output);
+    const auto* x = static_cast<const uint16_t*>(input);
+    size_t done = 0;
+    if (aligned16(output) && aligned16(input)) {
+        const size_t nvec = n / 8;
+        NG_REQUIRE(nvec / kEwThreads < 0xffffffffull, "ng_bf16_to_fp16_truncate: tensor too large");
+        if (nvec > 0) {
+            bf16_to_f16_trunc_vec_kernel<<<dim3(ew_blocks(nvec, ~0u)), dim3(kEwThreads), 0, stream()>>>(o, x, nvec);
+            NG_CHECK_LAUNCH("ng_bf16_to_fp16_truncate");
+        }
+        done = nvec * 8;
+    }
+    if (done < n)
+        bf16_to_f16_trunc_scalar_kernel<<<dim3(ew_blocks(n - done, 65536)), dim3(kEwThreads), 0, stream()>>>(
+            o, x, done, n);
     NG_CHECK_LAUNCH("ng_bf16_to_fp16_truncate");
     return 0;
 }

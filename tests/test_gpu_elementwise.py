@@ -93,7 +93,7 @@ def test_scale_bit_exact(lib, ora):
     assert_bits_equal(get(ob, np.uint16, (n,)), ora.elementwise("scale", a, s=np.float32(0.125 + 1e-3)), "scale")
 
 
-@pytest.mark.parametrize("n", [1, 8, 1000, 1 << 20])
+@pytest.mark.parametrize("n", [1, 8, 1000, 8 * 777 + 5, 1 << 20])
 def test_converters_exact(lib, ora, n):
     banner(f"converters n={n}")
     x = (RNG.standard_normal(n) * 10.0 ** RNG.integers(-6, 6, n)).astype(np.float32)
