@@ -897,11 +897,13 @@ def engine_bf16_pools_for(L, hip, cfg, d, shared):
     yield mk("add", 3 * th, [(th, d["x"]), (th, d["residual"])], lambda a, r: L.cuda_bf16_add(a, a, r, T * H))
     yield mk("silu", 2 * ti, [(ti, d["gate"])], lambda g: L.cuda_bf16_silu(g, g, T * I))
     yield mk("mul", 3 * ti, [(ti, d["gate"]), (ti, d["up"])], lambda g, u: L.cuda_bf16_mul(g, g, u, T * I))
-    # The conversions around attention (layer.cu:1537-1543,1574): Q, K (V is
-    # the same shape as K) bf16 -> fp16, and the attention output fp16 -> bf16.
-    nq, nk = T * cfg.nq * cfg.D, T * cfg.nkv * cfg.D
+    # The conversions around attention, with the element counts the engine
+    # passes (layer.cu:1537-1543,1574): Q (num_tokens x hidden_size) and K (V is
+    # the same) bf16 -> fp16, and the attention output (num_tokens x
+    # hidden_size) fp16 -> bf16.
+    nk = T * cfg.nkv * cfg.D
     xh = (d["x"].astype(np.uint32) << 16).view(np.float32).astype(np.float16).view(np.uint16)
-    yield mk("cvt_q", 4 * nq, [(2 * nq, d["q"]), (2 * nq, None)], lambda q, o: L.cuda_bf16_to_fp16(o, q, nq))
+    yield mk("cvt_q", 2 * th, [(th, d["x"]), (th, None)], lambda q, o: L.cuda_bf16_to_fp16(o, q, T * H))
     yield mk("cvt_k", 4 * nk, [(2 * nk, d["k"]), (2 * nk, None)], lambda k, o: L.cuda_bf16_to_fp16(o, k, nk))
     yield mk("cvt_attn_out", 2 * th, [(th, xh), (th, None)], lambda x, o: L.cuda_fp16_to_bf16(o, x, T * H))
 
@@ -910,7 +912,7 @@ def engine_bf16_kernel_bytes(cfg):
     """Algorithmic bytes of engine_bf16_pools_for's kernels."""
     T, H, I, e = cfg.T, cfg.H, cfg.I, cfg.e
     return {"rmsnorm_inplace": 2 * T * H * e + H * e, "add": 3 * T * H * e, "silu": 2 * T * I * e,
-            "mul": 3 * T * I * e, "cvt_q": 4 * T * cfg.nq * cfg.D, "cvt_k": 4 * T * cfg.nkv * cfg.D,
+            "mul": 3 * T * I * e, "cvt_q": 4 * T * H, "cvt_k": 4 * T * cfg.nkv * cfg.D,
             "cvt_attn_out": 4 * T * H}
 
 

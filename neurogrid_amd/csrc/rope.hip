@@ -146,6 +146,7 @@ struct RopeWaveArgs {
     const void* w1;    // per-head RMSNorm weights [D] of the first / second tensor (QKNORM)
     const void* w2;
     float eps;
+    int dev_store;     // 1: device-scope stores (small in-place updates), 0: non-temporal
     float inv_freq[kRopeMaxHalf];
 };
 
@@ -219,6 +220,10 @@ __global__ __launch_bounds__(kRopeThreads) void rope_wave_kernel(RopeWaveArgs a)
     uint16_t* out1 = static_cast<uint16_t*>(a.out) + static_cast<size_t>(t) * a.nh * a.D;
     const uint16_t* in2 = static_cast<const uint16_t*>(a.in2) + static_cast<size_t>(t) * a.nh2 * a.D;
     uint16_t* out2 = static_cast<uint16_t*>(a.out2) + static_cast<size_t>(t) * a.nh2 * a.D;
+    auto store = [&](uint16_t* p, u32x4 v) {
+        if (a.dev_store) st16_device(p, v);
+        else st16_stream(p, v);
+    };
 
     // Pass k of this wave is head pass g * HPL + k of the token: passes
     // [0, npass1) cover the first tensor, the rest the second. A pass (or a
@@ -274,8 +279,8 @@ __global__ __launch_bounds__(kRopeThreads) void rope_wave_kernel(RopeWaveArgs a)
         for (int k = 0; k < HPL; ++k) {
             if (!ok[k]) continue;
             uint16_t* dst = sec[k] ? out2 : out1;
-            st16_stream(dst + off[k], v1[k]);
-            if (STYLE == 0) st16_stream(dst + off[k] + half, v2[k]);
+            store(dst + off[k], v1[k]);
+            if (STYLE == 0) store(dst + off[k] + half, v2[k]);
         }
         return;
     }
@@ -315,8 +320,8 @@ __global__ __launch_bounds__(kRopeThreads) void rope_wave_kernel(RopeWaveArgs a)
             }
             if (ok[k]) {
                 uint16_t* dst = sec[k] ? out2 : out1;
-                st16_stream(dst + off[k], pack8<T>(y1));
-                st16_stream(dst + off[k] + half, pack8<T>(y2));
+                store(dst + off[k], pack8<T>(y1));
+                store(dst + off[k] + half, pack8<T>(y2));
             }
         } else {
             float x[8], y[8];
@@ -326,7 +331,7 @@ __global__ __launch_bounds__(kRopeThreads) void rope_wave_kernel(RopeWaveArgs a)
                 y[2 * e] = x[2 * e] * c[e] - x[2 * e + 1] * sn[e];
                 y[2 * e + 1] = x[2 * e] * sn[e] + x[2 * e + 1] * c[e];
             }
-            if (ok[k]) st16_stream((sec[k] ? out2 : out1) + off[k], pack8<T>(y));
+            if (ok[k]) store((sec[k] ? out2 : out1) + off[k], pack8<T>(y));
         }
     }
 }
@@ -397,6 +402,12 @@ static int launch_rope_wave(const char* name, void* out, const void* in, void* o
     w.nh = nh;
     w.nh2 = nh2;
     w.D = head_dim;
+    // In-place updates of tensors up to 8 MiB: device-scope stores. Measured
+    // on MI355X against non-temporal ones: K at Mistral-7B prefill (8 MiB)
+    // 4.49 vs 4.66 us, at Mistral-Nemo (4 MiB) 3.16 vs 3.59 us, Q at decode
+    // 2.48 vs 2.66 us; from 16 MiB on (Mistral-Nemo's Q) no faster.
+    const long long bytes = 2ll * tokens * (nh + nh2) * head_dim;
+    w.dev_store = out == in && (nh2 == 0 || out2 == in2) && bytes <= (8ll << 20);
     const int lph = style == 0 ? head_dim / 16 : head_dim / 8;
     w.lph_log2 = __builtin_ctz(static_cast<unsigned>(lph));
     const int hpp = kWave / lph;
