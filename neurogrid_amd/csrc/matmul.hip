@@ -364,7 +364,8 @@ constexpr int kBatch = 128;  // k per batch
 template <int MT, int W, int G>
 __global__ __launch_bounds__(G * W * kWave) void gemm_i8w_split_kernel(
     uint16_t* __restrict__ c, const uint16_t* __restrict__ a, const int8_t* __restrict__ b,
-    const float* __restrict__ scale, float* __restrict__ part, int M, int N, int K, int S, int tiles, int cps) {
+    const float* __restrict__ scale, float* __restrict__ part, int M, int N, int K, int S, int tiles, int cps,
+    int TT) {
     // A batch of A in LDS. From 4 tiles of A on: 256 bytes per row, 16-byte
     // piece q of row m stored at piece q xor (m mod 16), so the MFMA reads
     // (16 rows, one piece each per lane group) are conflict-free; padded rows
@@ -382,8 +383,26 @@ __global__ __launch_bounds__(G * W * kWave) void gemm_i8w_split_kernel(
     __shared__ __align__(16) uint8_t lds_a[2][G][16 * MT * kRowBytes];
     __shared__ __align__(16) u32x4 lds_b[G * W][2 * kWave];
 
-    const int sl = blockIdx.x % S;
-    const int tile = blockIdx.x / S;
+    // With TT > 1 token tiles, block b takes rows 16 MT ty .. of A for unit u
+    // (a tile and slice), with the TT blocks of a unit on one XCD (ids u + 8 j
+    // apart), so that they read its rows of B from one L2.
+    int unit = blockIdx.x, ty = 0;
+    if (TT > 1) {
+        const int i = blockIdx.x / 8;
+        ty = i % TT;
+        unit = (i / TT) * 8 + blockIdx.x % 8;
+        if (unit >= tiles * S) return;
+    }
+    const int Mall = M;
+    {
+        const int m0 = 16 * MT * ty;
+        a += static_cast<size_t>(m0) * K;
+        c += static_cast<size_t>(m0) * N;
+        part += static_cast<size_t>(m0) * N;
+        M = min(16 * MT, M - m0);
+    }
+    const int sl = unit % S;
+    const int tile = unit / S;
 
     const int tid = threadIdx.x;
     const int lane = tid & (kWave - 1);
@@ -558,7 +577,7 @@ __global__ __launch_bounds__(G * W * kWave) void gemm_i8w_split_kernel(
         return;
     }
     if (n < N) {
-        float* mine = part + static_cast<size_t>(sl) * M * N;
+        float* mine = part + static_cast<size_t>(sl) * Mall * N;
 #pragma unroll
         for (int t = 0; t < MT; ++t)
 #pragma unroll
@@ -978,14 +997,14 @@ int launch_reduce(hipStream_t s, uint16_t* c, const float* part, const float* sc
 
 template <int MT, int W, int G>
 int launch_split(uint16_t* c, const uint16_t* a, const int8_t* b, const float* scale, int M, int N, int K,
-                 float* scratch, size_t scratch_bytes) {
+                 float* scratch, size_t scratch_bytes, int TT = 1) {
     const int tiles = (N + 16 * W - 1) / (16 * W);
     const int nbatch = (K + kBatch - 1) / kBatch;
     // Enough slices of K for about 256 blocks (512 for K >= 8192; with groups
     // in the block, 192 blocks of twice the waves), at most 8, each of at
     // least two turns, none empty.
     const int target = G > 1 ? 192 : K >= 8192 ? 512 : 256;
-    int S = (target + tiles - 1) / tiles;
+    int S = (target + tiles * TT - 1) / (tiles * TT);
     S = max(1, min(S, min(8, nbatch / (2 * G))));
     const int cps = (nbatch + S - 1) / S;
     S = (nbatch + cps - 1) / cps;
@@ -996,8 +1015,10 @@ int launch_split(uint16_t* c, const uint16_t* a, const int8_t* b, const float* s
     float* part = nullptr;
     std::unique_lock<std::mutex> lock(g_mu, std::defer_lock);
     if (S > 1 && partial_buffer(s, S, M, N, K, scratch, scratch_bytes, lock, &part) != 0) return -1;
-    gemm_i8w_split_kernel<MT, W, G><<<dim3(static_cast<unsigned>(tiles * S)), dim3(G * W * kWave), 0, s>>>(
-        c, a, b, scale, part, M, N, K, S, tiles, cps);
+    const int units = tiles * S;
+    const int blocks = TT > 1 ? (units + 7) / 8 * 8 * TT : units;
+    gemm_i8w_split_kernel<MT, W, G><<<dim3(static_cast<unsigned>(blocks)), dim3(G * W * kWave), 0, s>>>(
+        c, a, b, scale, part, M, N, K, S, tiles, cps, TT);
     NG_CHECK_LAUNCH("cuda_gemm_int8");
     return S > 1 ? launch_reduce(s, c, part, scale, M, N, S) : 0;
 }
@@ -1007,8 +1028,9 @@ int launch_split(uint16_t* c, const uint16_t* a, const int8_t* b, const float* s
 // the GEMV kernel up to M = 4 (8 rows of B per block for M <= 2, 4 for M = 3,
 // 4: 23-33% faster than the MFMA kernels at M = 1), the split kernel from
 // M = 17 on and from M = 3 on with K or N of 8192 or more (at M = 4: 13.4 vs
-// 14.8 us for gate/up, 13.7 vs 15.5 us for down), otherwise the MFMA kernel
-// that reads A from L2 directly.
+// 14.8 us for gate/up, 13.7 vs 15.5 us for down), with token tiles of 32 rows
+// of A for N <= 2048 from M = 33 on, otherwise the MFMA kernel that reads A
+// from L2 directly.
 int gemm_i8w(void* c, const void* a, const void* b, const void* scale, int M, int K, int N,
              float* scratch = nullptr, size_t scratch_bytes = 0) {
     auto* cp = static_cast<uint16_t*>(c);
@@ -1026,6 +1048,12 @@ int gemm_i8w(void* c, const void* a, const void* b, const void* scale, int M, in
     // between two groups of 4 waves per block.
     const bool deep = K >= 8192;
     const bool wide = !deep && N >= 12288;
+    // Few rows of B (k/v: N = 1024 gives 16 tiles): blocks of 32 rows of A
+    // each (token tiles sharing B through one XCD's L2) instead of one block
+    // for all of A: 7-16% faster at M = 64-128 (k/v: 9.0 vs 10.5 us at
+    // M = 96); for larger N, and with 16-row token tiles, slower.
+    if (!deep && N <= 2048 && M > 32)
+        return launch_split<2, 4, 1>(cp, ap, bp, sp, M, N, K, scratch, scratch_bytes, (M + 31) / 32);
     if (M > 64)
         return deep ? launch_split<8, 8, 1>(cp, ap, bp, sp, M, N, K, scratch, scratch_bytes)
                : wide ? launch_split<8, 4, 2>(cp, ap, bp, sp, M, N, K, scratch, scratch_bytes)

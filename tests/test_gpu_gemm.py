@@ -103,6 +103,8 @@ FUSED = [
     # N >= 12288 at K < 8192: two wave groups per block at every tile height, odd batch counts, a half batch
     (128, 4096, 14336), (80, 4160, 12288), (20, 1088, 13000), (33, 2048, 12290), (9, 192, 12288),
     (3, 64, 12288), (4, 128, 12300), (70, 64, 12288),
+    # N <= 2048 at K < 8192 with M > 32: token tiles of 32 rows of A as separate blocks
+    (96, 4096, 1000), (128, 4096, 2048), (33, 1024, 64), (127, 4160, 1030),
 ]
 
 
@@ -130,7 +132,8 @@ def test_int8_weight_streaming_random(lib, ora, M, K, N):
 
 
 INF_SHAPES = [(1, 1040, 100), (2, 14352, 64), (4, 2064, 33), (8, 4160, 512), (12, 1088, 4096), (64, 4096, 4096),
-              (33, 8256, 384), (80, 4160, 12288), (3, 4096, 12300), (20, 1088, 13000), (128, 14336, 4096)]
+              (33, 8256, 384), (80, 4160, 12288), (3, 4096, 12300), (20, 1088, 13000), (128, 14336, 4096),
+              (100, 4160, 1000)]
 
 
 @pytest.mark.parametrize("M,K,N", INF_SHAPES)
