@@ -698,36 +698,42 @@ def cpu_baseline(cfg, budget_s=10.0, sample_1t=256):
         sub = W.LayerConfig(**{**cfg.__dict__, "T": T, "key": f"{cfg.key}_cpu_T{T}"})
         return sub, W.make_layer_inputs(sub, seed=0, with_table=False)
 
-    def one(sub, d):
-        O.rmsnorm(d["x"], d["w_attn"], sub.eps, sub.dtype)
-        O.rope(d["q"], d["pos"], 0, sub.theta, sub.dtype)
-        O.rope(d["k"], d["pos"], 0, sub.theta, sub.dtype)
-        O.add_rmsnorm(d["x"], d["residual"], d["w_ffn"], sub.eps, sub.dtype)
-        O.elementwise("silu_mul", d["gate"], d["up"], dtype=sub.dtype)
-        O.elementwise("add", d["x"], d["residual"], dtype=sub.dtype)
+    def ops(sub, d):
+        return [("rmsnorm", lambda: O.rmsnorm(d["x"], d["w_attn"], sub.eps, sub.dtype)),
+                ("rope_q", lambda: O.rope(d["q"], d["pos"], 0, sub.theta, sub.dtype)),
+                ("rope_k", lambda: O.rope(d["k"], d["pos"], 0, sub.theta, sub.dtype)),
+                ("add_rmsnorm", lambda: O.add_rmsnorm(d["x"], d["residual"], d["w_ffn"], sub.eps, sub.dtype)),
+                ("silu_mul", lambda: O.elementwise("silu_mul", d["gate"], d["up"], dtype=sub.dtype)),
+                ("add", lambda: O.elementwise("add", d["x"], d["residual"], dtype=sub.dtype))]
 
     def measure(sub, d, seconds, min_reps=5):
-        one(sub, d)
-        ts = []
+        """Median layer time and per-kernel medians (s) over repetitions of the six."""
+        steps = ops(sub, d)
+        for _, f in steps:
+            f()
+        ts, per = [], {k: [] for k, _ in steps}
         t_end = time.perf_counter() + seconds
         while time.perf_counter() < t_end or len(ts) < min_reps:
-            t = time.perf_counter()
-            one(sub, d)
-            ts.append(time.perf_counter() - t)
-        return float(np.median(ts)), len(ts)
+            t0 = time.perf_counter()
+            for k, f in steps:
+                t = time.perf_counter()
+                f()
+                per[k].append(time.perf_counter() - t)
+            ts.append(time.perf_counter() - t0)
+        return float(np.median(ts)), len(ts), {k: float(np.median(v)) for k, v in per.items()}
 
     sub1, d1 = inputs(sample_1t)
     O.set_threads(1)
-    med1, n1 = measure(sub1, d1, budget_s / 4, 3)
+    med1, n1, _ = measure(sub1, d1, budget_s / 4, 3)
     b1 = sum(W.layer_bytes(sub1)[k] for k in W.LAYER_KERNELS)
     del d1
     sub, d = inputs(cfg.T)
     O.set_threads(os.cpu_count() or 1)
     cores = O.get_threads()
-    med, n = measure(sub, d, budget_s)
+    med, n, per = measure(sub, d, budget_s)
     nbytes = sum(W.layer_bytes(sub)[k] for k in W.LAYER_KERNELS)
     return {"value": nbytes / med / 1e9, "unit": "GB/s", "cores": cores, "kind": "port",
-            "us_per_layer": med * 1e6,
+            "us_per_layer": med * 1e6, "per_kernel_us": {k: v * 1e6 for k, v in per.items()},
             "value_1_thread": b1 / med1 / 1e9, "us_per_layer_sample_1_thread": med1 * 1e6,
             "build": "gcc -O3 -march=x86-64-v3 -fopenmp -ffp-contract=off (portable x86-64-v3, not -march=native: "
                      "the oracle is built in one container and run on the GPU box's host)",
