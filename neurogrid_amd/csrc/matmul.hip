@@ -23,7 +23,12 @@
 //       L2, waves split K within the block;
 //   otherwise, up to M = 128: gemm_i8w_split_kernel, matrix cores, A staged
 //       in LDS, K split between wave groups of a block and between blocks
-//       (slices whose sums a second kernel adds).
+//       (slices whose sums a second kernel adds), A cut into token tiles
+//       for few rows of B.
+// Above 128 rows of A (prefill) the product is bound by the matrix cores:
+// gemm_i8w_prefill_kernel, a tiled GEMM whose B tiles are converted on their
+// way into LDS (see the prefill section). B stored [K, N] goes through the
+// reference's composition (dequantize, then hipBLASLt).
 // MFMA layout: v_mfma_f32_16x16x32_f16 multiplies a 16 x 32 tile of A (rows
 // m) by a 32 x 16 tile of B^T (columns n). Lane l supplies row (l % 16) of
 // each operand and 8 values of k; the accumulator lane l holds rows
