@@ -103,6 +103,38 @@ def build_library(jobs: int | None = None, verbose: bool = False) -> Path:
     return out
 
 
+# The C++ host mirror of the reference's Go bindings (host/neurogrid_gpu.cpp)
+# and its test program (tests/host/host_test.cpp): plain host code, built with
+# g++ against libgpu_engine.so and found beside it through $ORIGIN.
+CXX = os.environ.get("CXX", "g++")
+HOST_LIB = "libneurogrid_host.so"
+HOST_TEST = "host_test"
+HOST_FLAGS = ["-O2", "-std=c++17", "-Wall", "-Wextra", "-Werror",
+              f"-I{ROOT / 'include'}", f"-I{PKG / 'host'}"]
+
+
+def build_host(verbose: bool = False) -> tuple[Path, Path]:
+    """Compile libneurogrid_host.so and the host_test program into lib/."""
+    if not (LIBDIR / LIBNAME).exists():
+        raise RuntimeError(f"{LIBDIR / LIBNAME} is not built; build_library() first")
+    rpath = "-Wl,-rpath,$ORIGIN"
+    lib = LIBDIR / HOST_LIB
+    test = LIBDIR / HOST_TEST
+    steps = [
+        (lib, [CXX, *HOST_FLAGS, "-fPIC", "-shared", "-o", f"{lib}.tmp", str(PKG / "host" / "neurogrid_gpu.cpp"),
+               f"-L{LIBDIR}", "-lgpu_engine", rpath]),
+        (test, [CXX, *HOST_FLAGS, "-pthread", "-o", f"{test}.tmp", str(ROOT / "tests" / "host" / "host_test.cpp"),
+                f"-L{LIBDIR}", "-lneurogrid_host", "-lgpu_engine", rpath]),
+    ]
+    for out, cmd in steps:
+        if verbose:
+            print(" ".join(cmd), flush=True)
+        _run(cmd)
+        os.replace(f"{out}.tmp", out)
+    return lib, test
+
+
 if __name__ == "__main__":
     path = build_library(verbose="-v" in sys.argv)
     print(path)
+    print(*build_host(verbose="-v" in sys.argv))
