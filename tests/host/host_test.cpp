@@ -6,14 +6,15 @@
 // Sources: tests/kernels_test.go:19-274 (RMSNorm, SiLU, RoPE, Add),
 // tests/quantize_test.go:20-280, tests/matmul_test.go:20-260 (GEMMFP16,
 // GEMMINT8, GEMMTranspose), tests/cgo_test.go:16-313 (init/shutdown, error
-// handling, call overhead, concurrent calls) and
-// tests/e2e/real_inference_test.go:218-279 (embedding lookup). The Go suites
+// handling, call overhead, concurrent calls), tests/golden_test.go:24-201
+// (RMSNorm and SiLU golden vectors) and tests/e2e/real_inference_test.go:
+// 218-279 (embedding lookup). The Go suites
 // draw from math/rand seed 42, which is not reproduced here; a seeded
 // std::mt19937 stream serves these tolerance checks equally.
 //
-// Usage: host_test [--list] [name...]. Runs every test (or the named ones) in
-// order, prints RUN / PASS / FAIL lines, and exits with the number of
-// failures. --list prints the names and touches no GPU.
+// Usage: host_test [--list] [--golden DIR] [name...]. Runs every test (or
+// the named ones) in order, prints RUN / PASS / FAIL lines, and exits with the
+// number of failures. --list prints the names and touches no GPU.
 #include <algorithm>
 #include <atomic>
 #include <chrono>
@@ -27,6 +28,8 @@
 #include <string>
 #include <thread>
 #include <vector>
+
+#include <unistd.h>
 
 #include "neurogrid_gpu.hpp"
 
@@ -101,6 +104,41 @@ std::vector<float> CpuMatmul(const std::vector<float>& a, const std::vector<floa
             c[static_cast<size_t>(i) * N + j] = s;
         }
     return c;
+}
+
+// The reference's golden vectors (written by its scripts/generate_golden.py,
+// committed under tests/golden/reference_kernels/ as raw little-endian fp32),
+// found relative to this program (neurogrid_amd/lib/host_test) or given with
+// --golden DIR.
+std::string g_golden_dir;
+
+std::vector<float> LoadGolden(const char* name) {
+    const std::string path = g_golden_dir + "/" + name;
+    FILE* f = std::fopen(path.c_str(), "rb");
+    CHECK(f != nullptr, "cannot open %s", path.c_str());
+    std::vector<float> v;
+    float x;
+    while (std::fread(&x, sizeof(float), 1, f) == 1) v.push_back(x);
+    std::fclose(f);
+    CHECK(!v.empty(), "%s is empty", path.c_str());
+    return v;
+}
+
+// Max, mean and count above `tol` of |got - want|.
+struct DiffStats {
+    double max = 0, mean = 0;
+    size_t over = 0;
+};
+DiffStats Diff(const std::vector<float>& got, const std::vector<float>& want, double tol) {
+    DiffStats d;
+    for (size_t i = 0; i < want.size(); ++i) {
+        const double e = std::fabs(static_cast<double>(got[i]) - want[i]);
+        d.max = std::max(d.max, e);
+        d.mean += e;
+        d.over += e > tol;
+    }
+    d.mean /= static_cast<double>(want.size());
+    return d;
 }
 
 // ------------------------------------------------------------------ tests
@@ -313,6 +351,43 @@ void TestEmbeddingLookup() {
     for (int i = 0; i < 2 * H; ++i)
         CHECK(static_cast<uint8_t>(got[i]) == (off + i) % 256, "byte %d: %d, want %zu", i,
               static_cast<uint8_t>(got[i]), (off + i) % 256);
+}
+
+// golden_test.go:24-117: RMSNorm of the golden [1, 1, 4096] input with eps
+// 1e-6 against the golden output: max |d| < 5e-3, mean < 1e-4, fewer than 1%
+// of elements off by more than 1e-3.
+void TestRMSNormGolden() {
+    const std::vector<float> x = LoadGolden("rmsnorm_input.bin"), w = LoadGolden("rmsnorm_weight.bin"),
+                             want = LoadGolden("rmsnorm_output.bin");
+    const int64_t H = static_cast<int64_t>(w.size());
+    CHECK(x.size() == w.size() && want.size() == w.size(), "golden sizes %zu %zu %zu", x.size(), w.size(),
+          want.size());
+    Owned in({1, 1, H}, ng::Dtype::FP16), wt({H}, ng::Dtype::FP16), out({1, 1, H}, ng::Dtype::FP16);
+    NoError(ng::CopyToDevice(in.get(), x), "CopyToDevice");
+    NoError(ng::CopyToDevice(wt.get(), w), "CopyToDevice");
+    NoError(ng::RMSNorm(out.get(), in.get(), wt.get(), 1e-6f), "RMSNorm");
+    std::vector<float> got(H);
+    NoError(ng::CopyToHost(got, out.get()), "CopyToHost");
+    const DiffStats d = Diff(got, want, 1e-3);
+    std::printf("  max_diff %.3e, avg_diff %.3e, errors %zu/%lld\n", d.max, d.mean, d.over,
+                static_cast<long long>(H));
+    CHECK(d.max < 5e-3 && d.mean < 1e-4 && d.over < static_cast<size_t>(H) / 100, "outside the golden tolerance");
+}
+
+// golden_test.go:122-201: SiLU of the golden 11008 inputs: max |d| < 5e-3,
+// mean < 1e-4, fewer than 1% of elements off by more than 1e-3.
+void TestSiLUGolden() {
+    const std::vector<float> x = LoadGolden("silu_input.bin"), want = LoadGolden("silu_output.bin");
+    CHECK(x.size() == want.size(), "golden sizes %zu %zu", x.size(), want.size());
+    const int64_t n = static_cast<int64_t>(x.size());
+    Owned in({n}, ng::Dtype::FP16), out({n}, ng::Dtype::FP16);
+    NoError(ng::CopyToDevice(in.get(), x), "CopyToDevice");
+    NoError(ng::SiLU(out.get(), in.get()), "SiLU");
+    std::vector<float> got(n);
+    NoError(ng::CopyToHost(got, out.get()), "CopyToHost");
+    const DiffStats d = Diff(got, want, 1e-3);
+    std::printf("  max_diff %.3e, avg_diff %.3e, errors %zu/%lld\n", d.max, d.mean, d.over, static_cast<long long>(n));
+    CHECK(d.max < 5e-3 && d.mean < 1e-4 && d.over < static_cast<size_t>(n) / 100, "outside the golden tolerance");
 }
 
 // The bf16 wrappers (gpu.go:1329-1354; the Go suites hold no test of them):
@@ -551,6 +626,8 @@ const Case kCases[] = {
     {"TestDeviceInfo", TestDeviceInfo},
     {"TestRMSNorm", TestRMSNorm},
     {"TestSiLU", TestSiLU},
+    {"TestRMSNormGolden", TestRMSNormGolden},
+    {"TestSiLUGolden", TestSiLUGolden},
     {"TestRoPE", TestRoPE},
     {"TestAddKernel", TestAddKernel},
     {"TestQuantizePerTensor", TestQuantizePerTensor},
@@ -573,10 +650,23 @@ const Case kCases[] = {
 
 int main(int argc, char** argv) {
     std::vector<std::string> want;
+    {
+        // Default golden directory: tests/golden/reference_kernels beside this
+        // program's neurogrid_amd/lib/.
+        char exe[4096];
+        const ssize_t len = readlink("/proc/self/exe", exe, sizeof(exe) - 1);
+        std::string dir = len > 0 ? std::string(exe, static_cast<size_t>(len)) : std::string(argv[0]);
+        dir = dir.substr(0, dir.find_last_of('/') == std::string::npos ? 0 : dir.find_last_of('/'));
+        g_golden_dir = dir + "/../../tests/golden/reference_kernels";
+    }
     for (int i = 1; i < argc; ++i) {
         if (std::strcmp(argv[i], "--list") == 0) {
             for (const Case& c : kCases) std::printf("%s\n", c.name);
             return 0;
+        }
+        if (std::strcmp(argv[i], "--golden") == 0 && i + 1 < argc) {
+            g_golden_dir = argv[++i];
+            continue;
         }
         want.emplace_back(argv[i]);
     }

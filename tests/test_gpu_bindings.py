@@ -4,8 +4,10 @@ drive the gfx950 library through the same wrapper calls and shape rules.
 
 Sources: tests/kernels_test.go:19-274, tests/quantize_test.go:20-280,
 tests/matmul_test.go:96-179 (GEMMINT8), tests/cgo_test.go:244-313 (call
-overhead, concurrent calls), tests/e2e/real_inference_test.go:218-279
-(embedding lookup), and the device plumbing they use. The Go suites draw from Go's math/rand seed 42, which
+overhead, concurrent calls), tests/golden_test.go:24-201 (RMSNorm and SiLU
+against the reference's golden vectors, tests/golden/reference_kernels/),
+tests/e2e/real_inference_test.go:218-279 (embedding lookup), and the device
+plumbing they use. The Go suites draw from Go's math/rand seed 42, which
 cannot be reproduced here; any seeded stream is equivalent for these
 tolerance checks, so numpy PCG64 seed 42 is used.
 """
@@ -14,6 +16,7 @@ from __future__ import annotations
 import math
 import threading
 import time
+from pathlib import Path
 
 import numpy as np
 import pytest
@@ -63,6 +66,51 @@ def test_rmsnorm_ramp(gpu):
     rel = np.abs(res[nz] - exp[nz]) / np.abs(exp[nz])
     assert (rel > 0.002).sum() < 10
     for t in (inp, w, out):
+        B.FreeTensor(t)
+
+
+GOLD = Path(__file__).resolve().parent / "golden" / "reference_kernels"
+
+
+def golden_stats(got, want, tol=1e-3):
+    d = np.abs(got.astype(np.float64) - want)
+    return d.max(), d.mean(), int((d > tol).sum())
+
+
+def test_rmsnorm_golden(gpu):
+    """TestRMSNormGolden (golden_test.go:24-117): the reference's golden
+    [1, 1, 4096] vectors, eps 1e-6; max |d| < 5e-3, mean < 1e-4, under 1% of
+    elements off by more than 1e-3."""
+    banner("bindings TestRMSNormGolden")
+    x, w, want = (np.fromfile(GOLD / f"rmsnorm_{n}.bin", dtype="<f4") for n in ("input", "weight", "output"))
+    H = w.size
+    inp, wt, out = alloc([1, 1, H], B.Dtype.FP16), alloc([H], B.Dtype.FP16), alloc([1, 1, H], B.Dtype.FP16)
+    B.CopyToDevice(inp, x)
+    B.CopyToDevice(wt, w)
+    B.RMSNorm(out, inp, wt, 1e-6)
+    got = np.empty(H, np.float32)
+    B.CopyToHost(got, out)
+    mx, mean, over = golden_stats(got, want)
+    print(f"max_diff {mx:.3e} avg_diff {mean:.3e} errors {over}/{H}")
+    assert mx < 5e-3 and mean < 1e-4 and over < 0.01 * H
+    for t in (inp, wt, out):
+        B.FreeTensor(t)
+
+
+def test_silu_golden(gpu):
+    """TestSiLUGolden (golden_test.go:122-201): the reference's 11008 golden
+    inputs; max |d| < 5e-3, mean < 1e-4, under 1% off by more than 1e-3."""
+    banner("bindings TestSiLUGolden")
+    x, want = (np.fromfile(GOLD / f"silu_{n}.bin", dtype="<f4") for n in ("input", "output"))
+    inp, out = alloc([x.size], B.Dtype.FP16), alloc([x.size], B.Dtype.FP16)
+    B.CopyToDevice(inp, x)
+    B.SiLU(out, inp)
+    got = np.empty(x.size, np.float32)
+    B.CopyToHost(got, out)
+    mx, mean, over = golden_stats(got, want)
+    print(f"max_diff {mx:.3e} avg_diff {mean:.3e} errors {over}/{x.size}")
+    assert mx < 5e-3 and mean < 1e-4 and over < 0.01 * x.size
+    for t in (inp, out):
         B.FreeTensor(t)
 
 

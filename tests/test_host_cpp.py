@@ -22,10 +22,10 @@ HOST_TEST = LIB / "host_test"
 HEADER = ROOT / "neurogrid_amd" / "host" / "neurogrid_gpu.hpp"
 
 # The Go tests restated (tests/kernels_test.go, quantize_test.go,
-# matmul_test.go, cgo_test.go, e2e/real_inference_test.go) plus checks of
+# matmul_test.go, cgo_test.go, golden_test.go, e2e/real_inference_test.go) plus checks of
 # the copy rounding, the bf16 wrappers and concurrent GEMMINT8 calls.
 EXPECTED = [
-    "TestDeviceInfo", "TestRMSNorm", "TestSiLU", "TestRoPE", "TestAddKernel",
+    "TestDeviceInfo", "TestRMSNorm", "TestSiLU", "TestRMSNormGolden", "TestSiLUGolden", "TestRoPE", "TestAddKernel",
     "TestQuantizePerTensor", "TestDequantizePerTensor", "TestQuantizeWeights",
     "TestCopyFP16RoundToNearestEven", "TestEmbeddingLookup", "TestBF16Conversion",
     "TestCGOErrorHandling",
