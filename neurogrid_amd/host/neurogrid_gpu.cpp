@@ -1,8 +1,9 @@
 // neurogrid_gpu.cpp - the C++ restatement of gpu/bindings/gpu.go's wrappers
 // for the per-layer kernel path (see neurogrid_gpu.hpp). Each function cites
 // the Go wrapper it follows; the error text is the one that wrapper formats.
-// Two checks are added where the Go code would index an empty or short slice
-// and panic: CopyToHostINT8's buffer size and RoPE's empty position list.
+// Where the Go code would index an empty or short slice and panic (a
+// position list that is empty, a shape with too few dimensions for the
+// wrapper's shape rule), these functions return an error instead.
 #include "neurogrid_gpu.hpp"
 
 #include <cstdarg>
@@ -24,6 +25,12 @@ Error Errorf(const char* fmt, ...) {
     std::vsnprintf(buf, sizeof(buf), fmt, ap);
     va_end(ap);
     return Error(buf);
+}
+
+// A shape with fewer than `rank` dimensions, which the Go wrapper would index
+// out of range.
+Error ShapeError(const char* what, const Tensor* t, size_t rank) {
+    return Errorf("%s: tensor has %zu dimensions, needs at least %zu", what, t->Shape.size(), rank);
 }
 
 }  // namespace
@@ -184,7 +191,9 @@ Error RMSNorm(Tensor* output, const Tensor* input, const Tensor* weight, float e
     if (output == nullptr || input == nullptr || weight == nullptr) return Error("nil tensor");
     if (output->Data == nullptr || input->Data == nullptr || weight->Data == nullptr)
         return Error("tensor not allocated");
+    if (input->Shape.empty()) return ShapeError("RMSNorm", input, 1);
     const int64_t hidden = input->Shape.back();
+    if (hidden <= 0) return Errorf("RMSNorm: hidden size %lld must be positive", static_cast<long long>(hidden));
     const int64_t tokens = input->NumElements() / hidden;
     const int r = cuda_rmsnorm(output->Data, input->Data, weight->Data, static_cast<int>(tokens),
                                static_cast<int>(hidden), eps);
@@ -233,6 +242,8 @@ Error RoPE(Tensor* output, const Tensor* input, const std::vector<int32_t>& posi
 
 Error GEMMFP16(Tensor* c, const Tensor* a, const Tensor* b, bool transposeA, bool transposeB) {  // gpu.go:358-392
     if (c == nullptr || a == nullptr || b == nullptr) return Error("nil tensor");
+    if (a->Shape.size() < 2) return ShapeError("GEMM FP16", a, 2);
+    if (b->Shape.size() < 2) return ShapeError("GEMM FP16", b, 2);
     const int64_t M = transposeA ? a->Shape[1] : a->Shape[0];
     const int64_t K = transposeA ? a->Shape[0] : a->Shape[1];
     const int64_t N = transposeB ? b->Shape[0] : b->Shape[1];
@@ -244,6 +255,8 @@ Error GEMMFP16(Tensor* c, const Tensor* a, const Tensor* b, bool transposeA, boo
 
 Error GEMMINT8(Tensor* c, const Tensor* a, const Tensor* b, const Tensor* scale, bool transposeB) {  // gpu.go:395-424
     if (c == nullptr || a == nullptr || b == nullptr || scale == nullptr) return Error("nil tensor");
+    if (a->Shape.size() < 2) return ShapeError("GEMM INT8", a, 2);
+    if (b->Shape.size() < 2) return ShapeError("GEMM INT8", b, 2);
     const int64_t M = a->Shape[0], K = a->Shape[1];
     const int64_t N = transposeB ? b->Shape[0] : b->Shape[1];
     const int r = cuda_gemm_int8(c->Data, a->Data, b->Data, scale->Data, static_cast<int>(M), static_cast<int>(K),
@@ -270,6 +283,7 @@ Error DequantizePerTensor(Tensor* output, const Tensor* input, const Tensor* sca
 
 Error QuantizeWeights(Tensor* output, Tensor* scales, const Tensor* input) {  // gpu.go:463-482
     if (output == nullptr || scales == nullptr || input == nullptr) return Error("nil tensor");
+    if (input->Shape.size() < 2) return ShapeError("quantize weights", input, 2);
     const int r = cuda_quantize_weights(output->Data, scales->Data, input->Data, static_cast<int>(input->Shape[0]),
                                         static_cast<int>(input->Shape[1]));
     if (r != 0) return Errorf("quantize weights failed: %d", r);

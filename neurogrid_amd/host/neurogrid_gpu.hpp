@@ -8,7 +8,9 @@
 // [batch, seq, heads, headDim], GEMM dimensions from the operands' shapes),
 // and the same error text. A Go `error` becomes an `Error` whose message is
 // the one gpu.go formats; an empty Error is nil. Functions that return
-// (value, error) in Go take an out-parameter and return the Error.
+// (value, error) in Go take an out-parameter and return the Error. Where a Go
+// wrapper would panic (a shape with too few dimensions for its shape rule, an
+// empty position list), the C++ one returns an Error.
 //
 // Wrappers restated (gpu/bindings/gpu.go): HasCUDA :64, InitGPU :73,
 // ShutdownGPU :82, GetDeviceCount :87, SetDevice :97, GetDeviceInfo :106,

@@ -451,6 +451,18 @@ void TestCGOErrorHandling() {
     // An error the library reports is formatted with its code: the kernel
     // rejects a null pointer with -1.
     WantError(ng::SiLU(&unalloc, t.get()), "SiLU failed: -1", "SiLU(null output)");
+    // Shapes the wrappers' shape rules cannot read (Go would index out of
+    // range and panic) come back as errors.
+    ng::Tensor flat = t.t, scalarless = t.t;
+    scalarless.Shape.clear();
+    WantError(ng::RMSNorm(t.get(), &scalarless, t.get(), 1e-6f), "RMSNorm: tensor has 0 dimensions",
+              "RMSNorm(no dimensions)");
+    WantError(ng::GEMMINT8(t.get(), &flat, t.get(), t.get(), true), "GEMM INT8: tensor has 1 dimensions",
+              "GEMMINT8(1-d A)");
+    WantError(ng::GEMMFP16(t.get(), t.get(), &flat, false, false), "GEMM FP16: tensor has 1 dimensions",
+              "GEMMFP16(1-d B)");
+    WantError(ng::QuantizeWeights(t.get(), t.get(), &flat), "quantize weights: tensor has 1 dimensions",
+              "QuantizeWeights(1-d)");
 }
 
 void GemmFP16Case(bool transposeA) {
