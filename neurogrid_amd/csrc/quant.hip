@@ -36,6 +36,8 @@ __global__ void fill_u32_kernel(uint32_t* p, size_t n, uint32_t v) {
 }
 
 // ---- per tensor --------------------------------------------------------------
+constexpr int kAbsLoads = 4;
+
 __global__ __launch_bounds__(kQThreads) void tensor_absmax_kernel(uint32_t* mx_out, const uint16_t* x, size_t n,
                                                                   int vec) {
     __shared__ uint32_t s_max[kQThreads / kWave];
@@ -43,18 +45,30 @@ __global__ __launch_bounds__(kQThreads) void tensor_absmax_kernel(uint32_t* mx_o
     const size_t t0 = static_cast<size_t>(blockIdx.x) * kQThreads + threadIdx.x;
     uint32_t m = 0;
     size_t done = 0;
-    if (vec) {
-        const size_t nvec = n / 8;
-        for (size_t i = t0; i < nvec; i += stride) {
-            const u32x4 v = ld16_stream(x + i * 8);
+    auto fold = [&m](const u32x4 v) {
 #pragma unroll
-            for (int k = 0; k < 4; ++k) {
-                const uint32_t lo = absbits_nonan<f16>(static_cast<uint16_t>(v[k]));
-                const uint32_t hi = absbits_nonan<f16>(static_cast<uint16_t>(v[k] >> 16));
-                m = m > lo ? m : lo;
-                m = m > hi ? m : hi;
-            }
+        for (int k = 0; k < 4; ++k) {
+            const uint32_t lo = absbits_nonan<f16>(static_cast<uint16_t>(v[k]));
+            const uint32_t hi = absbits_nonan<f16>(static_cast<uint16_t>(v[k] >> 16));
+            m = m > lo ? m : lo;
+            m = m > hi ? m : hi;
         }
+    };
+    if (vec) {
+        // kAbsLoads vectors per thread per pass, all requested before any is
+        // folded: with one at a time each wave kept a single load in flight.
+        // Measured on MI355X for 2^27 elements: the whole per-tensor call
+        // 124.5 us against 129.8 us (8 loads: 125.7 us).
+        const size_t nvec = n / 8;
+        size_t i = t0;
+        for (; i + (kAbsLoads - 1) * stride < nvec; i += kAbsLoads * stride) {
+            u32x4 v[kAbsLoads];
+#pragma unroll
+            for (int u = 0; u < kAbsLoads; ++u) v[u] = ld16_stream(x + (i + u * stride) * 8);
+#pragma unroll
+            for (int u = 0; u < kAbsLoads; ++u) fold(v[u]);
+        }
+        for (; i < nvec; i += stride) fold(ld16_stream(x + i * 8));
         done = nvec * 8;
     }
     for (size_t i = done + t0; i < n; i += stride) {
