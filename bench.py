@@ -555,6 +555,15 @@ def extra_kernels(L, hip, stream):
     us = time_pool_kernel(hip, stream, thunks)
     out["rmsnorm_quant_int8"] = {"us": us, "GBps": b / us / 1e3, "frac": b / us / 1e3 / PEAK_GBPS, "bytes": b,
                                  "buffer_sets": n}
+    # Per-token int8 alone (cuda_quantize_weights_per_row with the tokens as
+    # rows), on the same activations.
+    b = qb["quant_per_token"]
+    thunks = [("quant_per_token", (lambda j=j: L.cuda_quantize_weights_per_row(codes.at(j), scl.at(j), xs.at(j),
+                                                                               W.QUANT_T, W.QUANT_H)))
+              for j in range(n)]
+    us = time_pool_kernel(hip, stream, thunks)
+    out["quantize_per_token_int8"] = {"us": us, "GBps": b / us / 1e3, "frac": b / us / 1e3 / PEAK_GBPS, "bytes": b,
+                                      "buffer_sets": n}
     for p in (xs, codes, scl):
         p.free()
     wb.free()
@@ -848,6 +857,8 @@ def profile_pass(L, hip, stream):
                                                                        eps)) for j in range(n)])
     group("quant/add_rmsnorm_quant", [(lambda j=j: L.ng_add_rmsnorm_quant_int8(
         codes.at(j), scl.at(j), ro.at(j), xs.at(j), res.at(j), wb.vp, T, H, eps)) for j in range(n)])
+    group("quant/quant_per_token", [(lambda j=j: L.cuda_quantize_weights_per_row(codes.at(j), scl.at(j), xs.at(j), T,
+                                                                                 H)) for j in range(n)])
     for p in (xs, res, ro, codes, scl):
         p.free()
     wb.free()

@@ -166,5 +166,6 @@ LAYER_KERNELS = ("rmsnorm", "rope_q", "rope_k", "add_rmsnorm", "silu_mul", "add"
 def quant_bytes(T: int = QUANT_T, H: int = QUANT_H, wn: int = QUANT_WN, wk: int = QUANT_WK) -> dict[str, int]:
     return {
         "rmsnorm_quant": T * H * 2 + T * H + 4 * T + H * 2,
+        "quant_per_token": T * H * 2 + T * H + 4 * T,
         "dequant": wn * wk + 4 * wn + 2 * wn * wk,
     }
