@@ -204,7 +204,7 @@ def fused_launches(L, cfg, s):
     launches: the residual add that ends the previous layer fused into this
     layer's RMSNorm (cuda_add_rmsnorm), Q and K rotated in one launch
     (ng_rope_qk_with_theta), add+RMSNorm, SwiGLU. Needs call-site changes in
-    the engine, so it is reported beside the headline."""
+    the engine (layer.cu:986-1057), so it is reported beside the headline."""
     T, H, I, D = cfg.T, cfg.H, cfg.I, cfg.D
     sh = s.shared
     eps, theta = C.c_float(cfg.eps), C.c_float(cfg.theta)
@@ -1028,8 +1028,8 @@ def main():
                                  "rmsnorm (in place)", "silu (in place)", "mul (in place)", "add"],
                     "note": "the bf16 engine's own sequence (layer.cu:1497-1615: two device copies, RMSNorm, "
                             "RoPE Q and K, add, RMSNorm, SiLU, mul, add); us_per_step of this layer above uses "
-                            "the fused ng_bf16_add_rmsnorm and ng_bf16_silu_mul instead, which need the call-site "
-                            "change in INTEGRATION.md"}
+                            "the fused ng_bf16_add_rmsnorm and ng_bf16_silu_mul instead, which need a call-site "
+                            "change in the engine (layer.cu:1584-1607)"}
         log("gather / rmsnorm+int8 / dequant")
         extra.update(extra_kernels(L, hip, stream))
         sized = [v for v in extra.values() if isinstance(v, dict) and "bytes" in v and "us" in v]
