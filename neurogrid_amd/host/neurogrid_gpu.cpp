@@ -3,7 +3,9 @@
 // the Go wrapper it follows; the error text is the one that wrapper formats.
 // Where the Go code would index an empty or short slice and panic (a
 // position list that is empty, a shape with too few dimensions for the
-// wrapper's shape rule), these functions return an error instead.
+// wrapper's shape rule), or hand the kernel a tensor smaller than the call
+// reads or writes through it (a device access past the allocation), these
+// functions return an error instead.
 #include "neurogrid_gpu.hpp"
 
 #include <cstdarg>
@@ -31,6 +33,12 @@ Error Errorf(const char* fmt, ...) {
 // out of range.
 Error ShapeError(const char* what, const Tensor* t, size_t rank) {
     return Errorf("%s: tensor has %zu dimensions, needs at least %zu", what, t->Shape.size(), rank);
+}
+
+// A tensor (or position list) with fewer elements than the call touches.
+Error SizeError(const char* what, const char* operand, int64_t have, int64_t need) {
+    return Errorf("%s: %s has %lld elements, the call needs %lld", what, operand, static_cast<long long>(have),
+                  static_cast<long long>(need));
 }
 
 }  // namespace
@@ -195,6 +203,9 @@ Error RMSNorm(Tensor* output, const Tensor* input, const Tensor* weight, float e
     const int64_t hidden = input->Shape.back();
     if (hidden <= 0) return Errorf("RMSNorm: hidden size %lld must be positive", static_cast<long long>(hidden));
     const int64_t tokens = input->NumElements() / hidden;
+    if (weight->NumElements() < hidden) return SizeError("RMSNorm", "weight", weight->NumElements(), hidden);
+    if (output->NumElements() < input->NumElements())
+        return SizeError("RMSNorm", "output", output->NumElements(), input->NumElements());
     const int r = cuda_rmsnorm(output->Data, input->Data, weight->Data, static_cast<int>(tokens),
                                static_cast<int>(hidden), eps);
     if (r != 0) return Errorf("RMSNorm failed: %d", r);
@@ -203,6 +214,8 @@ Error RMSNorm(Tensor* output, const Tensor* input, const Tensor* weight, float e
 
 Error SiLU(Tensor* output, const Tensor* input) {  // gpu.go:282-296
     if (output == nullptr || input == nullptr) return Error("nil tensor");
+    if (output->NumElements() < input->NumElements())
+        return SizeError("SiLU", "output", output->NumElements(), input->NumElements());
     const int r = cuda_silu(output->Data, input->Data, static_cast<size_t>(input->NumElements()));
     if (r != 0) return Errorf("SiLU failed: %d", r);
     return Error();
@@ -210,6 +223,8 @@ Error SiLU(Tensor* output, const Tensor* input) {  // gpu.go:282-296
 
 Error Add(Tensor* c, const Tensor* a, const Tensor* b) {  // gpu.go:299-314
     if (c == nullptr || a == nullptr || b == nullptr) return Error("nil tensor");
+    if (b->NumElements() < a->NumElements()) return SizeError("Add", "b", b->NumElements(), a->NumElements());
+    if (c->NumElements() < a->NumElements()) return SizeError("Add", "c", c->NumElements(), a->NumElements());
     const int r = cuda_add(c->Data, a->Data, b->Data, static_cast<size_t>(a->NumElements()));
     if (r != 0) return Errorf("Add failed: %d", r);
     return Error();
@@ -225,6 +240,12 @@ Error RoPE(Tensor* output, const Tensor* input, const std::vector<int32_t>& posi
     const int batch = static_cast<int>(input->Shape[0]);
     const int seq = static_cast<int>(input->Shape[1]);
     const int heads = static_cast<int>(input->Shape[2]);
+    const int64_t tokens = static_cast<int64_t>(batch) * seq;
+    const int64_t touched = tokens * heads * headDim;
+    if (static_cast<int64_t>(positions.size()) < tokens)
+        return SizeError("RoPE", "positions", static_cast<int64_t>(positions.size()), tokens);
+    if (input->NumElements() < touched) return SizeError("RoPE", "input", input->NumElements(), touched);
+    if (output->NumElements() < touched) return SizeError("RoPE", "output", output->NumElements(), touched);
     const size_t bytes = positions.size() * sizeof(int32_t);
     void* dpos = nullptr;
     if (cuda_malloc(&dpos, bytes) != 0) return Error("failed to allocate positions on GPU");
@@ -247,6 +268,9 @@ Error GEMMFP16(Tensor* c, const Tensor* a, const Tensor* b, bool transposeA, boo
     const int64_t M = transposeA ? a->Shape[1] : a->Shape[0];
     const int64_t K = transposeA ? a->Shape[0] : a->Shape[1];
     const int64_t N = transposeB ? b->Shape[0] : b->Shape[1];
+    if (a->NumElements() < M * K) return SizeError("GEMM FP16", "a", a->NumElements(), M * K);
+    if (b->NumElements() < K * N) return SizeError("GEMM FP16", "b", b->NumElements(), K * N);
+    if (c->NumElements() < M * N) return SizeError("GEMM FP16", "c", c->NumElements(), M * N);
     const int r = cuda_gemm_fp16(c->Data, a->Data, b->Data, static_cast<int>(M), static_cast<int>(K),
                                  static_cast<int>(N), transposeA, transposeB);
     if (r != 0) return Errorf("GEMM FP16 failed: %d", r);
@@ -259,6 +283,9 @@ Error GEMMINT8(Tensor* c, const Tensor* a, const Tensor* b, const Tensor* scale,
     if (b->Shape.size() < 2) return ShapeError("GEMM INT8", b, 2);
     const int64_t M = a->Shape[0], K = a->Shape[1];
     const int64_t N = transposeB ? b->Shape[0] : b->Shape[1];
+    if (b->NumElements() < K * N) return SizeError("GEMM INT8", "b", b->NumElements(), K * N);
+    if (c->NumElements() < M * N) return SizeError("GEMM INT8", "c", c->NumElements(), M * N);
+    if (scale->NumElements() < N) return SizeError("GEMM INT8", "scale", scale->NumElements(), N);
     const int r = cuda_gemm_int8(c->Data, a->Data, b->Data, scale->Data, static_cast<int>(M), static_cast<int>(K),
                                  static_cast<int>(N), transposeB);
     if (r != 0) return Errorf("GEMM INT8 failed: %d", r);
@@ -267,6 +294,8 @@ Error GEMMINT8(Tensor* c, const Tensor* a, const Tensor* b, const Tensor* scale,
 
 Error QuantizePerTensor(Tensor* output, Tensor* scale, const Tensor* input) {  // gpu.go:427-442
     if (output == nullptr || scale == nullptr || input == nullptr) return Error("nil tensor");
+    if (output->NumElements() < input->NumElements())
+        return SizeError("quantize", "output", output->NumElements(), input->NumElements());
     const int r = cuda_quantize_per_tensor(output->Data, scale->Data, input->Data,
                                            static_cast<size_t>(input->NumElements()));
     if (r != 0) return Errorf("quantize failed: %d", r);
@@ -275,6 +304,8 @@ Error QuantizePerTensor(Tensor* output, Tensor* scale, const Tensor* input) {  /
 
 Error DequantizePerTensor(Tensor* output, const Tensor* input, const Tensor* scale) {  // gpu.go:445-460
     if (output == nullptr || input == nullptr || scale == nullptr) return Error("nil tensor");
+    if (output->NumElements() < input->NumElements())
+        return SizeError("dequantize", "output", output->NumElements(), input->NumElements());
     const int r = cuda_dequantize_per_tensor(output->Data, input->Data, scale->Data,
                                              static_cast<size_t>(input->NumElements()));
     if (r != 0) return Errorf("dequantize failed: %d", r);
@@ -284,6 +315,10 @@ Error DequantizePerTensor(Tensor* output, const Tensor* input, const Tensor* sca
 Error QuantizeWeights(Tensor* output, Tensor* scales, const Tensor* input) {  // gpu.go:463-482
     if (output == nullptr || scales == nullptr || input == nullptr) return Error("nil tensor");
     if (input->Shape.size() < 2) return ShapeError("quantize weights", input, 2);
+    if (output->NumElements() < input->NumElements())
+        return SizeError("quantize weights", "output", output->NumElements(), input->NumElements());
+    if (scales->NumElements() < input->Shape[1])
+        return SizeError("quantize weights", "scales", scales->NumElements(), input->Shape[1]);
     const int r = cuda_quantize_weights(output->Data, scales->Data, input->Data, static_cast<int>(input->Shape[0]),
                                         static_cast<int>(input->Shape[1]));
     if (r != 0) return Errorf("quantize weights failed: %d", r);

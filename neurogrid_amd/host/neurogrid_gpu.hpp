@@ -10,7 +10,8 @@
 // the one gpu.go formats; an empty Error is nil. Functions that return
 // (value, error) in Go take an out-parameter and return the Error. Where a Go
 // wrapper would panic (a shape with too few dimensions for its shape rule, an
-// empty position list), the C++ one returns an Error.
+// empty position list) or pass the kernel a tensor smaller than the call
+// touches, the C++ one returns an Error before any launch.
 //
 // Wrappers restated (gpu/bindings/gpu.go): HasCUDA :64, InitGPU :73,
 // ShutdownGPU :82, GetDeviceCount :87, SetDevice :97, GetDeviceInfo :106,

@@ -463,6 +463,20 @@ void TestCGOErrorHandling() {
               "GEMMFP16(1-d B)");
     WantError(ng::QuantizeWeights(t.get(), t.get(), &flat), "quantize weights: tensor has 1 dimensions",
               "QuantizeWeights(1-d)");
+    // Tensors smaller than the call touches are refused before any launch.
+    Owned q4({1, 2, 4, 64}, ng::Dtype::FP16), big({1024}, ng::Dtype::FP16);
+    WantError(ng::RoPE(q4.get(), q4.get(), {0}, 64), "RoPE: positions has 1 elements, the call needs 2",
+              "RoPE(short positions)");
+    WantError(ng::RoPE(q4.get(), q4.get(), {0, 1}, 128), "RoPE: input has 512 elements, the call needs 1024",
+              "RoPE(head_dim past the tensor)");
+    WantError(ng::SiLU(t.get(), big.get()), "SiLU: output has 4 elements, the call needs 1024", "SiLU(short output)");
+    WantError(ng::Add(big.get(), big.get(), t.get()), "Add: b has 4 elements, the call needs 1024", "Add(short b)");
+    Owned a8({2, 64}, ng::Dtype::FP16), b8({16, 32}, ng::Dtype::INT8), c8({2, 16}, ng::Dtype::FP16),
+        s8({16}, ng::Dtype::FP32);
+    WantError(ng::GEMMINT8(c8.get(), a8.get(), b8.get(), s8.get(), true),
+              "GEMM INT8: b has 512 elements, the call needs 1024", "GEMMINT8(K of B short)");
+    WantError(ng::RMSNorm(big.get(), big.get(), t.get(), 1e-6f), "RMSNorm: weight has 4 elements, the call needs 1024",
+              "RMSNorm(short weight)");
 }
 
 void GemmFP16Case(bool transposeA) {
