@@ -204,8 +204,9 @@ __device__ __forceinline__ void head_rmsnorm(u32x4 (&x)[NV], const u32x4 (&w)[NV
                                el_mul<T, 1>(w[n][i], el_mul<T, 1>(x[n][i], r)));
 }
 
-template <typename T, int STYLE, int HPL, bool QKNORM, bool ROT = true>
+template <typename T, int STYLE, int HPL, bool QKNORM, bool ROT = true, bool EARLY = false>
 __global__ __launch_bounds__(kRopeThreads) void rope_wave_kernel(RopeWaveArgs a) {
+    static_assert(!EARLY || (ROT && !QKNORM), "early angles are for plain RoPE");
     const int lane = threadIdx.x & 63;
     // The wave index is uniform. With QK-norm, saying so makes the position
     // load a scalar load, which does not wait behind the head loads; plain
@@ -240,9 +241,14 @@ __global__ __launch_bounds__(kRopeThreads) void rope_wave_kernel(RopeWaveArgs a)
     // computed early, and 12.4-12.8 us with the stores held until every head
     // is in, or with one of the two round trips after the heads left): each
     // wave's two round trips between its last load and its first store keep
-    // the grid's writes behind its reads.
+    // the grid's writes behind its reads. Small tensors (EARLY: up to 8 MiB,
+    // one pass per wave) are bound by latency instead, and plain RoPE loads
+    // the position (a vector load) and the frequencies ahead of the heads
+    // too: Q at T = 64 2.19 us against 2.50, at T = 256 2.35 against 2.78.
     float f0 = 0.0f, f1 = 0.0f;
-    if (ROT && QKNORM) {
+    int praw = 0;
+    if (ROT && (QKNORM || EARLY)) {
+        if (EARLY) praw = a.pos[t];
         f0 = a.inv_freq[lane < half ? lane : 0];
         if (half > kWave) f1 = a.inv_freq[lane + kWave < half ? lane + kWave : 0];
     }
@@ -268,12 +274,13 @@ __global__ __launch_bounds__(kRopeThreads) void rope_wave_kernel(RopeWaveArgs a)
     __builtin_amdgcn_sched_barrier(0);
 
     float s0 = 0.0f, c0 = 1.0f, s1 = 0.0f, c1 = 1.0f;
-    auto angles = [&] {
-        const float p = static_cast<float>(__builtin_amdgcn_readfirstlane(a.pos[t]));
+    auto angles = [&](int pos) {
+        const float p = static_cast<float>(__builtin_amdgcn_readfirstlane(pos));
         sincosf(p * f0, &s0, &c0);
         if (half > kWave) sincosf(p * f1, &s1, &c1);
     };
-    if (ROT && QKNORM) angles();
+    if (ROT && QKNORM) angles(a.pos[t]);
+    if (EARLY) angles(praw);
 
     if (QKNORM) {
         // Per-head RMSNorm of each pass before it is rotated (weights of the
@@ -315,7 +322,7 @@ __global__ __launch_bounds__(kRopeThreads) void rope_wave_kernel(RopeWaveArgs a)
         return;
     }
 
-    if (!QKNORM) {
+    if (!QKNORM && !EARLY) {
         const float p = static_cast<float>(__builtin_amdgcn_readfirstlane(a.pos[t]));
         sincosf(p * a.inv_freq[lane < half ? lane : 0], &s0, &c0);
         if (half > kWave) sincosf(p * a.inv_freq[lane + kWave < half ? lane + kWave : 0], &s1, &c1);
@@ -475,6 +482,13 @@ static int launch_rope_wave(const char* name, void* out, const void* in, void* o
             else go(rope_wave_kernel<T, 1, HPL, false>);                                    \
         }                                                                                   \
         break;
+    // Up to 8 MiB with one pass per wave, plain RoPE takes the variant that
+    // loads the position and the frequencies ahead of the heads.
+    if (hpl == 1 && rotate && !qknorm && bytes <= (8ll << 20)) {
+        if (style == 0) go(rope_wave_kernel<T, 0, 1, false, true, true>);
+        else go(rope_wave_kernel<T, 1, 1, false, true, true>);
+        return 0;
+    }
     switch (hpl) {
         NG_ROPE_WAVE(1) NG_ROPE_WAVE(2) NG_ROPE_WAVE(3) NG_ROPE_WAVE(4)
         NG_ROPE_WAVE(5) NG_ROPE_WAVE(6) NG_ROPE_WAVE(7) NG_ROPE_WAVE(8)
