@@ -358,8 +358,17 @@ __global__ __launch_bounds__(64) void add_rms_rows_kernel(RowArgs a, int rows) {
             rv[j][k] = ld16_stream(RS + off + vc[k] * 8);
         }
     }
+    // The weight row is read by every wave. With four rows per wave it is
+    // loaded once the first row's statistic is known: issued with the row
+    // loads, these loads of the same few lines slowed them (measured on
+    // MI355X at T = H = 4096, in place: 22.0 us against 22.75 us), as in plain
+    // RMSNorm. With two rows per wave (H = 5120) loading it up front is faster
+    // (T = 2048, bf16: 14.55 us against 15.05 us).
+    constexpr bool kWeightsLate = R >= 4;
+    if (!kWeightsLate) {
 #pragma unroll
-    for (int k = 0; k < V; ++k) wv[k] = ld16(wr + vc[k] * 8);
+        for (int k = 0; k < V; ++k) wv[k] = ld16(wr + vc[k] * 8);
+    }
     __builtin_amdgcn_sched_barrier(0);
 
 #pragma unroll
@@ -389,6 +398,10 @@ __global__ __launch_bounds__(64) void add_rms_rows_kernel(RowArgs a, int rows) {
         // Summation tree height: 2 V per accumulator, 2 to join them, 6 across the wave.
         if (!ss_fast_resolve(S, 2 * V + 8, ss)) exact_row_ss_wave<T, true>(X + off, RS + off, a.nvec, lane, ss);
         const float r = 1.0f / __builtin_sqrtf(ss / static_cast<float>(a.H) + a.eps);
+        if (kWeightsLate && j == 0) {
+#pragma unroll
+            for (int k = 0; k < V; ++k) wv[k] = ld16(wr + vc[k] * 8);
+        }
         uint16_t* ro = static_cast<uint16_t*>(a.res_out) + off;
         uint16_t* yr = static_cast<uint16_t*>(a.y) + off;
 #pragma unroll
