@@ -89,6 +89,20 @@ def _ptr(t: Tensor) -> C.c_void_p:
     return C.c_void_p(t.data)
 
 
+# Where a Go wrapper would index past a short shape (a panic) or hand the
+# kernel a tensor smaller than the call touches (a device access past the
+# allocation), these wrappers raise before any call into the library, with
+# the text of the C++ wrappers (neurogrid_amd/host/neurogrid_gpu.cpp).
+def _rank(what: str, t: Tensor, rank: int) -> None:
+    if len(t.shape) < rank:
+        raise GPUError(f"{what}: tensor has {len(t.shape)} dimensions, needs at least {rank}")
+
+
+def _need(what: str, operand: str, have: int, need: int) -> None:
+    if have < need:
+        raise GPUError(f"{what}: {operand} has {have} elements, the call needs {need}")
+
+
 # ---------------------------------------------------------------- device management
 
 def HasCUDA() -> bool:
@@ -227,8 +241,13 @@ def RMSNorm(output: Tensor, input: Tensor, weight: Tensor, eps: float) -> None:
         raise GPUError("nil tensor")
     if output.data is None or input.data is None or weight.data is None:
         raise GPUError("tensor not allocated")
+    _rank("RMSNorm", input, 1)
     hidden = input.shape[-1]
+    if hidden <= 0:
+        raise GPUError(f"RMSNorm: hidden size {hidden} must be positive")
     tokens = input.num_elements() // hidden
+    _need("RMSNorm", "weight", weight.num_elements(), hidden)
+    _need("RMSNorm", "output", output.num_elements(), input.num_elements())
     r = _lib().cuda_rmsnorm(_ptr(output), _ptr(input), _ptr(weight), tokens, hidden, C.c_float(eps))
     if r != 0:
         raise GPUError(f"RMSNorm failed: {r}")
@@ -237,6 +256,7 @@ def RMSNorm(output: Tensor, input: Tensor, weight: Tensor, eps: float) -> None:
 def SiLU(output: Tensor, input: Tensor) -> None:
     if output is None or input is None:
         raise GPUError("nil tensor")
+    _need("SiLU", "output", output.num_elements(), input.num_elements())
     r = _lib().cuda_silu(_ptr(output), _ptr(input), input.num_elements())
     if r != 0:
         raise GPUError(f"SiLU failed: {r}")
@@ -245,6 +265,8 @@ def SiLU(output: Tensor, input: Tensor) -> None:
 def Add(c: Tensor, a: Tensor, b: Tensor) -> None:
     if c is None or a is None or b is None:
         raise GPUError("nil tensor")
+    _need("Add", "b", b.num_elements(), a.num_elements())
+    _need("Add", "c", c.num_elements(), a.num_elements())
     r = _lib().cuda_add(_ptr(c), _ptr(a), _ptr(b), a.num_elements())
     if r != 0:
         raise GPUError(f"Add failed: {r}")
@@ -260,6 +282,10 @@ def RoPE(output: Tensor, input: Tensor, positions, head_dim: int) -> None:
         raise GPUError("input must have 4 dimensions: [batch, seq, heads, head_dim]")
     batch, seq, heads = input.shape[0], input.shape[1], input.shape[2]
     pos = np.ascontiguousarray(positions, dtype=np.int32)
+    touched = batch * seq * heads * head_dim
+    _need("RoPE", "positions", pos.size, batch * seq)
+    _need("RoPE", "input", input.num_elements(), touched)
+    _need("RoPE", "output", output.num_elements(), touched)
     lib = _lib()
     dpos = C.c_void_p()
     if lib.cuda_malloc(C.byref(dpos), pos.nbytes) != 0:
@@ -281,8 +307,13 @@ def GEMMFP16(c: Tensor, a: Tensor, b: Tensor, transposeA: bool, transposeB: bool
     """gpu.go:357-391: M, K from a's shape (swapped when transposeA), N from b's."""
     if c is None or a is None or b is None:
         raise GPUError("nil tensor")
+    _rank("GEMM FP16", a, 2)
+    _rank("GEMM FP16", b, 2)
     M, K = (a.shape[1], a.shape[0]) if transposeA else (a.shape[0], a.shape[1])
     N = b.shape[0] if transposeB else b.shape[1]
+    _need("GEMM FP16", "a", a.num_elements(), M * K)
+    _need("GEMM FP16", "b", b.num_elements(), K * N)
+    _need("GEMM FP16", "c", c.num_elements(), M * N)
     r = _lib().cuda_gemm_fp16(_ptr(c), _ptr(a), _ptr(b), M, K, N, bool(transposeA), bool(transposeB))
     if r != 0:
         raise GPUError(f"GEMM FP16 failed: {r}")
@@ -292,8 +323,13 @@ def GEMMINT8(c: Tensor, a: Tensor, b: Tensor, scale: Tensor, transposeB: bool) -
     """gpu.go:395-424: M, K from a; N = b.shape[0] when transposeB (B [N, K]), else b.shape[1]."""
     if c is None or a is None or b is None or scale is None:
         raise GPUError("nil tensor")
+    _rank("GEMM INT8", a, 2)
+    _rank("GEMM INT8", b, 2)
     M, K = a.shape[0], a.shape[1]
     N = b.shape[0] if transposeB else b.shape[1]
+    _need("GEMM INT8", "b", b.num_elements(), K * N)
+    _need("GEMM INT8", "c", c.num_elements(), M * N)
+    _need("GEMM INT8", "scale", scale.num_elements(), N)
     r = _lib().cuda_gemm_int8(_ptr(c), _ptr(a), _ptr(b), _ptr(scale), M, K, N, bool(transposeB))
     if r != 0:
         raise GPUError(f"GEMM INT8 failed: {r}")
@@ -302,6 +338,7 @@ def GEMMINT8(c: Tensor, a: Tensor, b: Tensor, scale: Tensor, transposeB: bool) -
 def QuantizePerTensor(output: Tensor, scale: Tensor, input: Tensor) -> None:
     if output is None or scale is None or input is None:
         raise GPUError("nil tensor")
+    _need("quantize", "output", output.num_elements(), input.num_elements())
     r = _lib().cuda_quantize_per_tensor(_ptr(output), _ptr(scale), _ptr(input), input.num_elements())
     if r != 0:
         raise GPUError(f"quantize failed: {r}")
@@ -310,6 +347,7 @@ def QuantizePerTensor(output: Tensor, scale: Tensor, input: Tensor) -> None:
 def DequantizePerTensor(output: Tensor, input: Tensor, scale: Tensor) -> None:
     if output is None or input is None or scale is None:
         raise GPUError("nil tensor")
+    _need("dequantize", "output", output.num_elements(), input.num_elements())
     r = _lib().cuda_dequantize_per_tensor(_ptr(output), _ptr(input), _ptr(scale), input.num_elements())
     if r != 0:
         raise GPUError(f"dequantize failed: {r}")
@@ -319,7 +357,10 @@ def QuantizeWeights(output: Tensor, scales: Tensor, input: Tensor) -> None:
     """gpu.go:463-482: per-column, K = shape[0], N = shape[1]."""
     if output is None or scales is None or input is None:
         raise GPUError("nil tensor")
+    _rank("quantize weights", input, 2)
     K, N = input.shape[0], input.shape[1]
+    _need("quantize weights", "output", output.num_elements(), input.num_elements())
+    _need("quantize weights", "scales", scales.num_elements(), N)
     r = _lib().cuda_quantize_weights(_ptr(output), _ptr(scales), _ptr(input), K, N)
     if r != 0:
         raise GPUError(f"quantize weights failed: {r}")
