@@ -11,7 +11,9 @@ import pytest
 
 from gpu_util import C, assert_bits_equal, assert_close16, banner, dev, empty, get, ok
 
-pytestmark = pytest.mark.gpu
+# numpy's float32 -> float16 casts of values beyond the fp16 range give inf,
+# the expected result, and warn about it.
+pytestmark = [pytest.mark.gpu, pytest.mark.filterwarnings("ignore:overflow encountered in cast:RuntimeWarning")]
 
 RNG = np.random.Generator(np.random.PCG64(5))
 
