@@ -14,7 +14,13 @@ Flags worth noting:
     product, which differs from fp32-then-fp16 rounding in about 1 element in
     2^13-2^15;
   * ``-target-feature -packed-fp32-ops`` keeps the compiler from emitting
-    packed fp32 VALU instructions.
+    packed fp32 VALU instructions;
+  * ``-amdgpu-kernarg-preload-count=16``: the first 16 dwords of a kernel's
+    scalar arguments arrive in SGPRs when its waves start, instead of through
+    a scalar load of the argument segment. Kernels taking a struct by value
+    are not preloaded. Measured on MI355X: the embedding gather 2-2.5% faster
+    (Mistral-7B prefill 12.16 vs 12.47 us, Mistral-Nemo Zipf 6.32 vs
+    6.46 us), the element-wise kernels unchanged.
 """
 from __future__ import annotations
 
@@ -46,6 +52,7 @@ COMMON_FLAGS = [
     "-Wno-unused-variable",
     "-Wno-unused-but-set-variable",
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    "-mllvm", "-amdgpu-kernarg-preload-count=16",
     f"-I{ROOT / 'include'}",
 ]
 
