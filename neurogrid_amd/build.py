@@ -20,7 +20,9 @@ Flags worth noting:
     a scalar load of the argument segment. Kernels taking a struct by value
     are not preloaded. Measured on MI355X: the embedding gather 2-2.5% faster
     (Mistral-7B prefill 12.16 vs 12.47 us, Mistral-Nemo Zipf 6.32 vs
-    6.46 us), the element-wise kernels unchanged.
+    6.46 us), int8 GEMMs with a split-K reduction 3-4% faster at M = 16-64
+    (q_proj at M = 64: 12.05 vs 12.43 us), the element-wise kernels
+    unchanged.
 """
 from __future__ import annotations
 
