@@ -253,6 +253,55 @@ def engine_bf16_launches(L, cfg, s, hip, stream):
     ]
 
 
+def engine_int8_launches(L, cfg, s, hip, stream):
+    """The fp16 INT8 engine layer's own memory-bound sequence, unfused
+    (gpu/engine/layer.cu:458-598, cuda_layer_forward): copy residual <- input,
+    RMSNorm, RoPE Q and K in place, add in place (o-proj output + residual),
+    copy residual <- sum, RMSNorm in place, SiLU in place, mul in place,
+    residual add. The copies are device-to-device hipMemcpyAsync on the launch
+    stream, as the engine's cudaMemcpy calls are (stream-ordered here)."""
+    T, H, I, D = cfg.T, cfg.H, cfg.I, cfg.D
+    sh = s.shared
+    eps, theta = C.c_float(cfg.eps), C.c_float(cfg.theta)
+    nb = T * H * 2
+
+    def copy(dst, src):
+        return hip.h.hipMemcpyAsync(dst.vp, src.vp, nb, 3, stream)
+
+    return [
+        ("copy_residual", lambda: copy(s.res, s.x)),
+        ("rmsnorm", lambda: L.cuda_rmsnorm(s.normed.vp, s.x.vp, sh["w_attn"].vp, T, H, eps)),
+        ("rope_q", lambda: L.cuda_rope_with_theta(s.q.vp, s.q.vp, sh["pos"].ip, 1, T, cfg.nq, D, 0, theta)),
+        ("rope_k", lambda: L.cuda_rope_with_theta(s.k.vp, s.k.vp, sh["pos"].ip, 1, T, cfg.nkv, D, 0, theta)),
+        ("add", lambda: L.cuda_add(s.attn.vp, s.attn.vp, s.res.vp, T * H)),
+        ("copy_residual2", lambda: copy(s.res_out, s.attn)),
+        ("rmsnorm2", lambda: L.cuda_rmsnorm(s.attn.vp, s.attn.vp, sh["w_ffn"].vp, T, H, eps)),
+        ("silu", lambda: L.cuda_silu(s.gate.vp, s.gate.vp, T * I)),
+        ("mul", lambda: L.cuda_mul(s.gate.vp, s.gate.vp, s.up.vp, T * I)),
+        ("add_out", lambda: L.cuda_add(s.out.vp, s.down.vp, s.res_out.vp, T * H)),
+    ]
+
+
+def engine_int8_fused_launches(L, cfg, s):
+    """The same layer with the call-site change for the INT8 layer: the first
+    copy dropped (the layer input is the residual), add + copy + RMSNorm as one
+    cuda_add_rmsnorm writing the residual and the normed sum (normed in place
+    over the o-proj output), SiLU + mul as one cuda_silu_mul in place; six
+    launches."""
+    T, H, I, D = cfg.T, cfg.H, cfg.I, cfg.D
+    sh = s.shared
+    eps, theta = C.c_float(cfg.eps), C.c_float(cfg.theta)
+    return [
+        ("rmsnorm", lambda: L.cuda_rmsnorm(s.normed.vp, s.x.vp, sh["w_attn"].vp, T, H, eps)),
+        ("rope_q", lambda: L.cuda_rope_with_theta(s.q.vp, s.q.vp, sh["pos"].ip, 1, T, cfg.nq, D, 0, theta)),
+        ("rope_k", lambda: L.cuda_rope_with_theta(s.k.vp, s.k.vp, sh["pos"].ip, 1, T, cfg.nkv, D, 0, theta)),
+        ("add_rmsnorm", lambda: L.cuda_add_rmsnorm(s.attn.vp, s.res_out.vp, s.attn.vp, s.x.vp, sh["w_ffn"].vp, T, H,
+                                                   eps)),
+        ("silu_mul", lambda: L.cuda_silu_mul(s.gate.vp, s.gate.vp, s.up.vp, T * I)),
+        ("add_out", lambda: L.cuda_add(s.out.vp, s.down.vp, s.res_out.vp, T * H)),
+    ]
+
+
 def engine_bf16_bytes(cfg):
     T, H, I, e = cfg.T, cfg.H, cfg.I, cfg.e
     lb = W.layer_bytes(cfg)
@@ -363,6 +412,11 @@ def run_layer(L, hip, stream, cfg, steps, warmup, kernel_launches=24, kernel_rep
     if cfg.dtype == "bf16":
         seq["engine_bf16_step_ms"] = time_steps(
             hip, stream, [engine_bf16_launches(L, cfg, s, hip, stream) for s in sets], steps, warmup)[0]
+    else:
+        seq["engine_int8_step_ms"] = time_steps(
+            hip, stream, [engine_int8_launches(L, cfg, s, hip, stream) for s in sets], steps, warmup)[0]
+        seq["engine_int8_fused_step_ms"] = time_steps(
+            hip, stream, [engine_int8_fused_launches(L, cfg, s) for s in sets], steps, warmup)[0]
 
     for s in sets:
         s.free()
@@ -383,14 +437,13 @@ def run_layer(L, hip, stream, cfg, steps, warmup, kernel_launches=24, kernel_rep
         g.destroy()
         for p in pools:
             p.free()
-    if cfg.dtype == "bf16":
-        eng = {}
-        for name, make in engine_bf16_pools_for(L, hip, cfg, d, shared):
-            thunks, pools = make()
-            eng[name] = time_pool_kernel(hip, stream, thunks, kernel_launches, kernel_reps)
-            for p in pools:
-                p.free()
-        seq["engine_bf16_kernels_us"] = eng
+    eng = {}
+    for name, make in engine_unfused_pools_for(L, hip, cfg, d, shared, stream):
+        thunks, pools = make()
+        eng[name] = time_pool_kernel(hip, stream, thunks, kernel_launches, kernel_reps)
+        for p in pools:
+            p.free()
+    seq["engine_bf16_kernels_us" if cfg.dtype == "bf16" else "engine_int8_kernels_us"] = eng
     del d
     for b in shared.values():
         b.free()
@@ -618,7 +671,11 @@ def extra_kernels(L, hip, stream):
     return out
 
 
-PREFILL_M = (512, 4096)
+PREFILL_M = (512, 1024, 2048, 4096)
+# The composition through hipBLASLt is timed only at the row counts where it
+# has run clean on MI355X; at 1024 and 2048 rows a run over it (and over a
+# blocked variant) ended in a GPU memory fault whose cause was not found.
+COMPOSED_M = (512, 4096)
 
 
 def gemm_extras(L, hip, stream):
@@ -628,7 +685,8 @@ def gemm_extras(L, hip, stream):
     cudaFree (cuda_dequantize_weights into an fp16 buffer, then
     cuda_gemm_fp16). Weight pools keep the codes cache-cold. Also every
     projection at prefill sizes (PREFILL_M tokens), where cuda_gemm_int8 runs
-    the fused prefill MFMA kernel, against the same composition."""
+    the fused prefill MFMA kernel, against the same composition (at
+    COMPOSED_M)."""
     rng = np.random.Generator(np.random.PCG64(0))
     H, I = 4096, 14336
     shapes = {"q_proj": (H, H), "k_proj": (H, 1024), "gate_proj": (H, I), "down_proj": (I, H)}
@@ -670,11 +728,12 @@ def gemm_extras(L, hip, stream):
                 rc = L.cuda_dequantize_weights(deq.vp, wp.at(0), sc.vp, N, K, 1)
                 return rc or L.cuda_gemm_fp16(cb.vp, ab.vp, deq.vp, M, K, N, False, True)
 
-            try:
-                usc = time_kernel(hip, stream, [comp], launches=8, reps=2)
-            except RuntimeError as e:   # hipBLASLt refuses some shapes (status 6 at K = 14336)
-                usc = None
-                print(f"[bench] composed {name} M={M}: {e}", file=sys.stderr, flush=True)
+            usc = None
+            if M in COMPOSED_M:
+                try:
+                    usc = time_kernel(hip, stream, [comp], launches=8, reps=2)
+                except RuntimeError as e:   # hipBLASLt refuses some shapes (status 6 at K = 14336)
+                    print(f"[bench] composed {name} M={M}: {e}", file=sys.stderr, flush=True)
             out[f"{name}_M{M}"] = {"us": us, "TFLOPs": 2 * M * N * K / us / 1e6, "composed_us": usc,
                                    "composed_TFLOPs": usc and 2 * M * N * K / usc / 1e6,
                                    "note": "fused int8 prefill MFMA kernel; composed = dequantize to fp16 + "
@@ -765,8 +824,9 @@ def profile_pass(L, hip, stream):
     Calibration: a 256 MiB device-to-device copy (reads and writes 256 MiB),
     and cuda_quantize_per_tensor over 128 Mi fp16 values, whose absmax kernel
     reads 256 MiB and writes one word. Then, for each layer configuration, each
-    layer kernel (and ng_rope_qk_with_theta; for bf16 also the engine's
-    unfused RMSNorm in place, add, SiLU and mul) PROFILE_LAUNCHES times, each
+    layer kernel (and ng_rope_qk_with_theta; for bf16 and for Mistral-7B
+    prefill also the engine's unfused RMSNorm in place, add in place, SiLU and
+    mul in place) PROFILE_LAUNCHES times, each
     launch on a buffer slot untouched for over 1 GB of other traffic; the
     embedding gathers (Mistral-7B uniform ids, Mistral-Nemo Zipf ids); fused
     RMSNorm + int8, residual add + RMSNorm + int8 and int8 dequant at the
@@ -810,8 +870,10 @@ def profile_pass(L, hip, stream):
             group(f"{key}/{name}", [fn for _, fn in thunks])
             for p in pools:
                 p.free()
-        if cfg.dtype == "bf16":
-            for name, make in engine_bf16_pools_for(L, hip, cfg, d, shared):
+        if cfg.dtype == "bf16" or key == "mistral7b_prefill":
+            for name, make in engine_unfused_pools_for(L, hip, cfg, d, shared, stream):
+                if name == "copy_residual":     # a runtime copy, not a kernel of this library
+                    continue
                 thunks, pools = make()
                 group(f"{key}/engine_{name}", [fn for _, fn in thunks])
                 for p in pools:
@@ -892,14 +954,20 @@ def log_profile(label, dispatches, warmup):
     print(f"[profile] {label} warmup={warmup} dispatches={dispatches}", file=sys.stderr, flush=True)
 
 
-def engine_bf16_pools_for(L, hip, cfg, d, shared):
-    """The kernels of the bf16 engine's unfused sequence that the fused layer
-    does not launch (engine_bf16_launches), with buffer pools as in
-    kernel_pools_for: RMSNorm in place, add, SiLU in place, mul in place, and
-    the dtype conversions the bf16 layer runs around attention."""
+def engine_unfused_pools_for(L, hip, cfg, d, shared, stream):
+    """The kernels of the engine's unfused sequence that the fused layer does
+    not launch (engine_bf16_launches, engine_int8_launches), with buffer pools
+    as in kernel_pools_for: RMSNorm in place, add in place, SiLU in place, mul
+    in place, the device copy of the residual, and for bf16 the dtype
+    conversions the bf16 layer runs around attention."""
     T, H, I, e = cfg.T, cfg.H, cfg.I, cfg.e
     eps = C.c_float(cfg.eps)
     th, ti = T * H * e, T * I * e
+    bf = cfg.dtype == "bf16"
+    rms = L.cuda_bf16_rmsnorm if bf else L.cuda_rmsnorm
+    add = L.cuda_bf16_add if bf else L.cuda_add
+    silu = L.cuda_bf16_silu if bf else L.cuda_silu
+    mul = L.cuda_bf16_mul if bf else L.cuda_mul
 
     def mk(name, footprint, specs, launch):
         def make():
@@ -910,10 +978,14 @@ def engine_bf16_pools_for(L, hip, cfg, d, shared):
         return name, make
 
     yield mk("rmsnorm_inplace", 2 * th, [(th, d["x"])],
-             lambda x: L.cuda_bf16_rmsnorm(x, x, shared["w_ffn"].vp, T, H, eps))
-    yield mk("add", 3 * th, [(th, d["x"]), (th, d["residual"])], lambda a, r: L.cuda_bf16_add(a, a, r, T * H))
-    yield mk("silu", 2 * ti, [(ti, d["gate"])], lambda g: L.cuda_bf16_silu(g, g, T * I))
-    yield mk("mul", 3 * ti, [(ti, d["gate"]), (ti, d["up"])], lambda g, u: L.cuda_bf16_mul(g, g, u, T * I))
+             lambda x: rms(x, x, shared["w_ffn"].vp, T, H, eps))
+    yield mk("add", 3 * th, [(th, d["x"]), (th, d["residual"])], lambda a, r: add(a, a, r, T * H))
+    yield mk("silu", 2 * ti, [(ti, d["gate"])], lambda g: silu(g, g, T * I))
+    yield mk("mul", 3 * ti, [(ti, d["gate"]), (ti, d["up"])], lambda g, u: mul(g, g, u, T * I))
+    yield mk("copy_residual", 2 * th, [(th, d["x"]), (th, None)],
+             lambda x, o: hip.h.hipMemcpyAsync(o, x, th, 3, stream))
+    if not bf:
+        return
     # The conversions around attention, with the element counts the engine
     # passes (layer.cu:1537-1543,1574): Q (num_tokens x hidden_size) and K (V is
     # the same) bf16 -> fp16, and the attention output (num_tokens x
@@ -925,12 +997,39 @@ def engine_bf16_pools_for(L, hip, cfg, d, shared):
     yield mk("cvt_attn_out", 2 * th, [(th, xh), (th, None)], lambda x, o: L.cuda_fp16_to_bf16(o, x, T * H))
 
 
-def engine_bf16_kernel_bytes(cfg):
-    """Algorithmic bytes of engine_bf16_pools_for's kernels."""
+def engine_unfused_kernel_bytes(cfg):
+    """Algorithmic bytes of engine_unfused_pools_for's kernels."""
     T, H, I, e = cfg.T, cfg.H, cfg.I, cfg.e
     return {"rmsnorm_inplace": 2 * T * H * e + H * e, "add": 3 * T * H * e, "silu": 2 * T * I * e,
-            "mul": 3 * T * I * e, "cvt_q": 4 * T * H, "cvt_k": 4 * T * cfg.nkv * cfg.D,
-            "cvt_attn_out": 4 * T * H}
+            "mul": 3 * T * I * e, "copy_residual": 2 * T * H * e, "cvt_q": 4 * T * H,
+            "cvt_k": 4 * T * cfg.nkv * cfg.D, "cvt_attn_out": 4 * T * H}
+
+
+def engine_int8_report(cfg, per, seq):
+    """The fp16 INT8 engine layer's memory-bound sequence (cuda_layer_forward,
+    layer.cu:458-598): its graph step time and per-kernel averages, unfused as
+    the engine calls it and with the fused call-site change."""
+    b = engine_bf16_bytes(cfg)
+    lb = W.layer_bytes(cfg)
+    fb = lb["rmsnorm"] + lb["rope_q"] + lb["rope_k"] + lb["add_rmsnorm"] + lb["silu_mul"] + lb["add"]
+    ek = engine_unfused_kernel_bytes(cfg)
+    eng = seq["engine_int8_kernels_us"]
+    unfused_sum = (2 * eng["copy_residual"] + per["rmsnorm"] + per["rope_q"] + per["rope_k"] + eng["add"]
+                   + eng["rmsnorm_inplace"] + eng["silu"] + eng["mul"] + per["add"])
+    us, fus = seq["engine_int8_step_ms"] * 1e3, seq["engine_int8_fused_step_ms"] * 1e3
+    return {
+        "unfused": {"us_per_step": us, "us_per_layer": unfused_sum, "layer_bytes": b, "GBps": b / us / 1e3,
+                    "sequence": ["copy residual", "rmsnorm", "rope_q", "rope_k", "add (in place)", "copy residual",
+                                 "rmsnorm (in place)", "silu (in place)", "mul (in place)", "add"],
+                    "kernels": {k: {"us": u, "bytes": ek[k], "frac": ek[k] / u / 1e3 / PEAK_GBPS}
+                                for k, u in eng.items()}},
+        "fused": {"us_per_step": fus, "layer_bytes": fb, "GBps": fb / fus / 1e3, "frac": fb / fus / 1e3 / PEAK_GBPS,
+                  "sequence": ["rmsnorm", "rope_q", "rope_k", "add_rmsnorm (residual_in = layer input, normed in "
+                               "place)", "silu_mul (in place)", "add"]},
+        "saved_us": us - fus,
+        "note": "the engine's INT8 layer (layer.cu:458-598) around its GEMMs and attention; fused = the call-site "
+                "change written in INTEGRATION.md (cuda_add + copy + cuda_rmsnorm -> cuda_add_rmsnorm, "
+                "cuda_silu + cuda_mul -> cuda_silu_mul, the first copy dropped)"}
 
 
 # ----------------------------------------------------------------------------- main
@@ -1001,6 +1100,7 @@ def main():
     # cuda_add_rmsnorm, and Q and K rotate in one launch. Needs call-site
     # changes in the engine, so it is reported beside the headline.
     fused_layer = fused_layer_report(cfg, per, seq)
+    engine_int8 = engine_int8_report(cfg, per, seq) if cfg.dtype != "bf16" else None
 
     extra = {}
     if not args.no_extra:
@@ -1019,7 +1119,7 @@ def main():
             if c2.dtype == "bf16":
                 eb = engine_bf16_bytes(c2)
                 eu = seq2["engine_bf16_step_ms"] * 1e3
-                ebk = engine_bf16_kernel_bytes(c2)
+                ebk = engine_unfused_kernel_bytes(c2)
                 extra[key]["engine_bf16_unfused"] = {
                     "us_per_step": eu, "layer_bytes": eb,
                     "kernels": {k: {"us": u, "bytes": ebk[k], "frac": ebk[k] / u / 1e3 / PEAK_GBPS}
@@ -1071,6 +1171,7 @@ def main():
         "us_per_layer": us_layer,
         "fused_qk_variant": fused_qk,
         "fused_layer_variant": fused_layer,
+        "engine_int8_layer": engine_int8,
         "pct_of_peak": layer_bytes / us_layer / 1e3 / PEAK_GBPS * 100,
         "host_wall_ms_per_step": wall_ms,
         "layer_bytes": layer_bytes,

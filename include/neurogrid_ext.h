@@ -113,8 +113,9 @@ int ng_gather_embeddings_checked(void* output, const void* embed_table, const in
  * callers that cannot allocate device memory (code under HIP graph capture,
  * tight serving loops, harnesses that forbid hipMalloc). Arguments and
  * results as cuda_gemm_int8 (the same kernels, bit for bit), for the shapes
- * those paths take: transpose_b, K % 16 == 0 (K % 64 == 0 for 4 < M <= 128),
- * 16-byte aligned A and B; other shapes return -1. The split-K partial sums live in a fixed 64 MiB
+ * those paths take: transpose_b,
+ * K % 16 == 0 (K % 64 == 0 for 4 < M <= 128), 16-byte aligned A and B; other
+ * shapes return -1. The split-K partial sums live in a fixed 64 MiB
  * device array that each GPU the library runs on holds until the process
  * ends; a shape whose partial sums exceed it returns -1. Calls that overlap
  * on one GPU share that array and race. */

@@ -50,6 +50,7 @@
 #include <atomic>
 #include <map>
 #include <mutex>
+#include <set>
 #include <tuple>
 #include <utility>
 #include <vector>
@@ -727,13 +728,19 @@ __global__ __launch_bounds__(WM * WN * kWave, 1) void gemm_i8w_prefill_kernel(
     u32x4 ra[kAP], rb[kBP];
     // Loads of step kt. In a last step that runs past K (K % 64 != 0) the
     // pieces past K are zeroed in both operands, so that they add nothing (an
-    // inf times a zero would be NaN).
+    // inf times a zero would be NaN). The step offset is part of the vector
+    // offset, which the buffer's range check covers: a piece past K of the
+    // last row of A or B lies past num_records and reads zeros without a
+    // memory access (pieces past K of other rows read the next row, in
+    // bounds, and are zeroed here).
     auto load = [&](int kt) {
         const int k0 = kt * kPfBK;
 #pragma unroll
-        for (int j = 0; j < kAP; ++j) ra[j] = __builtin_amdgcn_raw_buffer_load_b128(rsa, aoff0 + j * astride, 2 * k0, 0);
+        for (int j = 0; j < kAP; ++j)
+            ra[j] = __builtin_amdgcn_raw_buffer_load_b128(rsa, aoff0 + j * astride + static_cast<uint32_t>(2 * k0), 0, 0);
 #pragma unroll
-        for (int j = 0; j < kBP; ++j) rb[j] = __builtin_amdgcn_raw_buffer_load_b128(rsb, boff0 + j * bstride, k0, 0);
+        for (int j = 0; j < kBP; ++j)
+            rb[j] = __builtin_amdgcn_raw_buffer_load_b128(rsb, boff0 + j * bstride + static_cast<uint32_t>(k0), 0, 0);
         if (k0 + kPfBK > K) {
             if (k0 + 8 * aq >= K) {
 #pragma unroll
@@ -852,11 +859,12 @@ struct StreamBuffers {
     size_t part_bytes = 0;
 };
 
-using PlanKey = std::tuple<int, int, int, int, bool, bool>;  // device, M, K, N, transpose_a, transpose_b
+using PlanKey = std::tuple<int, int, int, int, bool, bool, int>;  // device, M, K, N, transpose_a, transpose_b, ldc
 
 std::mutex g_mu;
 std::map<int, hipblasLtHandle_t> g_handles;
 std::map<PlanKey, Plan> g_plans;
+std::set<PlanKey> g_lt_refused;   // shapes hipBLASLt has no algorithm for, or refused
 std::map<std::pair<int, hipStream_t>, StreamBuffers> g_buffers;
 // Buffers replaced by larger ones. A HIP graph that captured an earlier call
 // still names the old buffer, so it is kept until gemm_release().
@@ -889,11 +897,14 @@ int grow(hipStream_t s, void** p, size_t* have, size_t need) {
     return 0;
 }
 
-// Plan for row-major C[M,N] = op(A) @ op(B). hipBLASLt is column-major: the
-// row-major matrices are their transposes, so it computes C^T = op(B)^T op(A)^T
-// with B as its first operand (the same swap as matmul.cu:90-147).
-int get_plan(int dev, int M, int K, int N, bool ta, bool tb, const Plan** out) {
-    const PlanKey key{dev, M, K, N, ta, tb};
+// Plan for row-major C[M,N] = op(A) @ op(B), the rows of C ldc elements
+// apart (ldc = N unless C is a column block of a wider matrix). hipBLASLt is
+// column-major: the row-major matrices are their transposes, so it computes
+// C^T = op(B)^T op(A)^T with B as its first operand (the same swap as
+// matmul.cu:90-147).
+int get_plan(int dev, int M, int K, int N, bool ta, bool tb, const Plan** out, int ldc = 0) {
+    if (ldc == 0) ldc = N;
+    const PlanKey key{dev, M, K, N, ta, tb, ldc};
     auto it = g_plans.find(key);
     if (it != g_plans.end()) {
         *out = &it->second;
@@ -915,7 +926,7 @@ int get_plan(int dev, int M, int K, int N, bool ta, bool tb, const Plan** out) {
     else NG_LT_CHECK(hipblasLtMatrixLayoutCreate(&p.lw, HIP_R_16F, N, K, N));
     if (ta) NG_LT_CHECK(hipblasLtMatrixLayoutCreate(&p.lx, HIP_R_16F, M, K, M));
     else NG_LT_CHECK(hipblasLtMatrixLayoutCreate(&p.lx, HIP_R_16F, K, M, K));
-    NG_LT_CHECK(hipblasLtMatrixLayoutCreate(&p.ly, HIP_R_16F, N, M, N));
+    NG_LT_CHECK(hipblasLtMatrixLayoutCreate(&p.ly, HIP_R_16F, N, M, ldc));
     hipblasLtMatmulPreference_t pref = nullptr;
     NG_LT_CHECK(hipblasLtMatmulPreferenceCreate(&pref));
     const uint64_t ws = kLtWorkspace;
@@ -959,6 +970,85 @@ int gemm_lt(void* c, const void* a, const void* b, const void* q, const void* sc
     const float alpha = 1.0f, beta = 0.0f;
     NG_LT_CHECK(hipblasLtMatmul(g_handles[dev], p->desc, &alpha, b, p->lw, a, p->lx, &beta, c, p->ly, c, p->ly,
                                 &p->algo, sb->ws, p->ws, s));
+    return 0;
+}
+
+// SWITCHED OFF (kLtBlocks = false): a benchmark run that exercised this path
+// at 512-4096 rows of A for every Mistral-7B projection, together with the
+// full composition at 1024 and 2048 rows, ended in a GPU memory fault whose
+// cause was not found in this code; hipBLASLt at new shapes is the suspect
+// (it already refuses some K = 14336 shapes with an internal error). Until a
+// cause is shown, cuda_gemm_int8 keeps the fused prefill kernel at every M.
+//
+// cuda_gemm_int8 above kLtMinM rows of A in the engine's layout (B int8
+// [N, K], one scale per row): the reference's composition, dequantize then
+// multiply (matmul.cu:205-236), without its K x N fp16 copy. B is dequantized
+// kLtChunkBytes at a time, in blocks of rows of B of equal size (a multiple
+// of 256), into this stream's buffer, and each block is multiplied into its
+// columns of C (row stride N) by hipBLASLt. Returns 1, having enqueued
+// nothing that writes C, when the composition cannot run here: hipBLASLt has
+// no algorithm for a block, or the stream is being captured and the buffers
+// do not exist yet; the caller then runs the fused prefill kernel. A
+// hipBLASLt call that fails after earlier blocks ran also returns 1: the
+// fused kernel then rewrites all of C.
+constexpr bool kLtBlocks = false;
+constexpr int kLtMinM = 1024;
+constexpr size_t kLtChunkBytes = size_t(64) << 20;
+
+int gemm_lt_blocks(void* c, const void* a, const void* q, const void* scale, int M, int K, int N) {
+    int dev = 0;
+    NG_HIP_CHECK(hipGetDevice(&dev));
+    const hipStream_t s = stream();
+    const size_t row_bytes = static_cast<size_t>(K) * 2;
+    const int nb = static_cast<int>((static_cast<size_t>(N) * row_bytes + kLtChunkBytes - 1) / kLtChunkBytes);
+    int rows = (N + nb - 1) / nb;
+    rows = (rows + 255) / 256 * 256;
+    while (rows > 256 && static_cast<size_t>(rows) * row_bytes > kLtChunkBytes) rows -= 256;
+    if (rows > N) rows = N;
+    std::lock_guard<std::mutex> lock(g_mu);
+    // Plans of the full blocks and of the last one; a shape hipBLASLt has no
+    // algorithm for is remembered and sends every later call to the fused kernel.
+    const Plan* plan[2] = {nullptr, nullptr};
+    const int last = N - (N - 1) / rows * rows;
+    for (int i = 0; i < 2; ++i) {
+        const int nr = i == 0 ? rows : last;
+        const PlanKey key{dev, M, K, nr, false, true, N};
+        if (g_lt_refused.count(key)) return 1;
+        auto it = g_plans.find(key);
+        if (it == g_plans.end()) {
+            // A failed lookup prints its reason once; the key is then refused quietly.
+            if (get_plan(dev, M, K, nr, false, true, &plan[i], N) != 0) {
+                g_lt_refused.insert(key);
+                return 1;
+            }
+        } else {
+            plan[i] = &it->second;
+        }
+    }
+    StreamBuffers* sb = &g_buffers[{dev, s}];
+    const size_t ws = plan[0]->ws > plan[1]->ws ? plan[0]->ws : plan[1]->ws;
+    const size_t deq = static_cast<size_t>(rows) * row_bytes;
+    if (ws > sb->ws_bytes || deq > sb->deq_bytes) {
+        bool cap = false;
+        if (capturing(s, &cap) != 0) return -1;
+        if (cap) return 1;
+        if (grow(s, &sb->ws, &sb->ws_bytes, ws) != 0 || grow(s, &sb->deq, &sb->deq_bytes, deq) != 0) return -1;
+    }
+    const float alpha = 1.0f, beta = 0.0f;
+    for (int n0 = 0; n0 < N; n0 += rows) {
+        const int nr = N - n0 < rows ? N - n0 : rows;
+        const Plan* p = nr == rows ? plan[0] : plan[1];
+        const int r = cuda_dequantize_weights(sb->deq, static_cast<const int8_t*>(q) + static_cast<size_t>(n0) * K,
+                                              static_cast<const float*>(scale) + n0, nr, K, 1);
+        if (r != 0) return r;
+        const hipblasStatus_t st = hipblasLtMatmul(g_handles[dev], p->desc, &alpha, sb->deq, p->lw, a, p->lx, &beta,
+                                                   static_cast<uint16_t*>(c) + n0, p->ly,
+                                                   static_cast<uint16_t*>(c) + n0, p->ly, &p->algo, sb->ws, p->ws, s);
+        if (st != HIPBLAS_STATUS_SUCCESS) {
+            g_lt_refused.insert(PlanKey{dev, M, K, nr, false, true, N});
+            return 1;
+        }
+    }
     return 0;
 }
 
@@ -1164,6 +1254,7 @@ void gemm_release() {
         hipblasLtMatmulDescDestroy(p.desc);
     }
     g_plans.clear();
+    g_lt_refused.clear();
     for (auto& kv : g_buffers) {
         for (void* b : {kv.second.ws, kv.second.deq, kv.second.part})
             if (b != nullptr) (void)hipFree(b);
@@ -1194,14 +1285,21 @@ extern "C" int cuda_gemm_int8(void* c, const void* a, const void* b, const void*
     NG_REQUIRE(c && a && b && scale, "cuda_gemm_int8: null pointer");
     NG_REQUIRE(M > 0 && K > 0 && N > 0, "cuda_gemm_int8: M=%d K=%d N=%d must be > 0", M, K, N);
     if (use_i8w(a, b, M, K, N, transpose_b)) return gemm_i8w(c, a, b, scale, M, K, N);
-    if (use_prefill(a, b, M, K, N, transpose_b)) return gemm_prefill(c, a, b, scale, M, K, N);
+    if (use_prefill(a, b, M, K, N, transpose_b)) {
+        if (kLtBlocks && M >= kLtMinM) {
+            const int r = gemm_lt_blocks(c, a, b, scale, M, K, N);
+            if (r <= 0) return r;
+        }
+        return gemm_prefill(c, a, b, scale, M, K, N);
+    }
     return gemm_lt(c, a, nullptr, b, scale, M, K, N, false, transpose_b);
 }
 
-// The weight-streaming path of cuda_gemm_int8 with no allocation: its only
-// buffer, the split-K partial sums, lives in this library's fixed `scratch`
-// array of the current device. Same kernels, same launch shapes and so the
-// same bits as cuda_gemm_int8. Every call on a device shares that device's
+// The fused paths of cuda_gemm_int8 with no allocation: their only buffer,
+// the split-K partial sums, lives in this library's fixed `scratch` array of
+// the current device. Same kernels, same launch shapes and so the same bits as
+// cuda_gemm_int8 (with the blocks path above switched off, at every M). Every
+// call on a device shares that device's
 // array: calls that overlap on one GPU (other streams, other host threads)
 // race on it. The split kernel writes every partial sum before the reduction
 // reads it, so nothing needs clearing between calls.

@@ -338,11 +338,19 @@ __device__ __forceinline__ u32x4 ld16_stream(const void* p) {
 __device__ __forceinline__ void st16_stream(void* p, u32x4 v) {
     __builtin_nontemporal_store(v, reinterpret_cast<u32x4*>(p));
 }
-// Device-scope store (sc1). For small tensors updated in place (RoPE up to
-// 8 MiB) it measured faster than the non-temporal store on MI355X; for large
-// ones, and for the kernels that write a separate output, slower.
-__device__ __forceinline__ void st16_device(void* p, u32x4 v) {
-    asm volatile("global_store_dwordx4 %0, %1, off sc1" ::"v"(p), "v"(v) : "memory");
+// Device-scope store (sc1) of 16 bytes at byte offset `off` of the buffer
+// `r`. For small tensors updated in place (RoPE up to 8 MiB) it measured
+// faster than the non-temporal store on MI355X; for large ones, and for the
+// kernels that write a separate output, slower. Written with the buffer-store
+// builtin (cache-policy operand 16 = sc1 on gfx950), not inline asm, so that
+// the compiler sees the store and keeps the wait states a VALU write to its
+// data registers needs after it.
+constexpr int kCachePolicySC1 = 16;
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer_rsrc(void* base, uint32_t bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(base, 0, static_cast<int>(bytes), 0x00020000);
+}
+__device__ __forceinline__ void st16_device(__amdgpu_buffer_rsrc_t r, uint32_t off, u32x4 v) {
+    __builtin_amdgcn_raw_buffer_store_b128(v, r, off, 0, kCachePolicySC1);
 }
 
 // ---------------------------------------------------------------------------

@@ -226,9 +226,22 @@ __global__ __launch_bounds__(kRopeThreads) void rope_wave_kernel(RopeWaveArgs a)
     uint16_t* out1 = static_cast<uint16_t*>(a.out) + static_cast<size_t>(t) * a.nh * a.D;
     const uint16_t* in2 = static_cast<const uint16_t*>(a.in2) + static_cast<size_t>(t) * a.nh2 * a.D;
     uint16_t* out2 = static_cast<uint16_t*>(a.out2) + static_cast<size_t>(t) * a.nh2 * a.D;
-    auto store = [&](uint16_t* p, u32x4 v) {
-        if (a.dev_store) st16_device(p, v);
-        else st16_stream(p, v);
+    // Store of the vector at element offset `o` within this token's heads of
+    // the first or second tensor. Device-scope stores (tensors of at most
+    // 8 MiB) go through a buffer resource based at the tensor, with the
+    // token's offset in the vector offset.
+    // (`second` is the same for the whole wave; readfirstlane says so, which
+    // keeps the resource in scalar registers.)
+    auto store = [&](bool second_lane, uint32_t o, u32x4 v) {
+        if (a.dev_store) {
+            const bool second = __builtin_amdgcn_readfirstlane(static_cast<int>(second_lane)) != 0;
+            const uint32_t nhs = static_cast<uint32_t>(second ? a.nh2 : a.nh);
+            const uint32_t bytes = static_cast<uint32_t>(a.T) * nhs * static_cast<uint32_t>(a.D) * 2u;
+            const uint32_t boff = 2u * (static_cast<uint32_t>(t) * nhs * static_cast<uint32_t>(a.D) + o);
+            st16_device(buffer_rsrc(second ? a.out2 : a.out, bytes), boff, v);
+        } else {
+            st16_stream((second_lane ? out2 : out1) + o, v);
+        }
     };
 
     // With QK-norm the angles are computed while the heads are in flight:
@@ -315,9 +328,8 @@ __global__ __launch_bounds__(kRopeThreads) void rope_wave_kernel(RopeWaveArgs a)
 #pragma unroll
         for (int k = 0; k < HPL; ++k) {
             if (!ok[k]) continue;
-            uint16_t* dst = sec[k] ? out2 : out1;
-            store(dst + off[k], v1[k]);
-            if (STYLE == 0) store(dst + off[k] + half, v2[k]);
+            store(sec[k], off[k], v1[k]);
+            if (STYLE == 0) store(sec[k], off[k] + half, v2[k]);
         }
         return;
     }
@@ -357,9 +369,8 @@ __global__ __launch_bounds__(kRopeThreads) void rope_wave_kernel(RopeWaveArgs a)
                 y2[e] = x1[e] * sn[e] + x2[e] * c[e];
             }
             if (ok[k]) {
-                uint16_t* dst = sec[k] ? out2 : out1;
-                store(dst + off[k], pack8<T>(y1));
-                store(dst + off[k] + half, pack8<T>(y2));
+                store(sec[k], off[k], pack8<T>(y1));
+                store(sec[k], off[k] + half, pack8<T>(y2));
             }
         } else {
             float x[8], y[8];
@@ -369,7 +380,7 @@ __global__ __launch_bounds__(kRopeThreads) void rope_wave_kernel(RopeWaveArgs a)
                 y[2 * e] = x[2 * e] * c[e] - x[2 * e + 1] * sn[e];
                 y[2 * e + 1] = x[2 * e] * sn[e] + x[2 * e + 1] * c[e];
             }
-            if (ok[k]) store((sec[k] ? out2 : out1) + off[k], pack8<T>(y));
+            if (ok[k]) store(sec[k], off[k], pack8<T>(y));
         }
     }
 }

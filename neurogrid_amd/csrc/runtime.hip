@@ -196,7 +196,9 @@ extern "C" int cuda_get_device_count(int* count) {
 extern "C" int cuda_set_device(int device_id) {
     NG_HIP_CHECK(hipSetDevice(device_id));
     g_current_device = device_id;
-    return 0;
+    // Look up this device's copy of the allocation-free GEMM's scratch array
+    // now, outside any stream capture, rather than on its first call there.
+    return gemm_scratch_init(device_id);
 }
 
 extern "C" int cuda_get_device_info(DeviceInfo* info) {

@@ -124,6 +124,26 @@ def test_rmsnorm_quant_matches_the_two_step_composition(lib, ora):
     assert_bits_equal(s, get(s2b, np.float32, (T,)), "scales")
 
 
+@pytest.mark.parametrize("T,H", [(128, 4096), (4096, 4096), (300, 5120), (9, 4100)])
+def test_add_rmsnorm_quant_matches_the_two_step_composition(lib, T, H):
+    """Fused kernel == cuda_add_rmsnorm followed by cuda_quantize_weights_per_row,
+    both on the GPU (the composition it replaces), with a NaN and an inf row."""
+    banner(f"add+rmsnorm+int8 vs composition T={T} H={H}")
+    x = f16(RNG.standard_t(3, (T, H)) * 3)
+    r = f16(RNG.standard_normal((T, H)) * 2)
+    w = f16(1 + 0.02 * RNG.standard_normal(H))
+    x[0, 5] = 0x7E00
+    r[T - 1, H // 2] = 0x7C00
+    q, s, ro = run_norm_quant(lib, x, w, 1e-5, residual=r)
+    xb, rb, wb, yb, rob = dev(x), dev(r), dev(w), empty(x.nbytes), empty(x.nbytes)
+    ok(lib.cuda_add_rmsnorm(yb.vp, rob.vp, xb.vp, rb.vp, wb.vp, T, H, C.c_float(1e-5)))
+    q2b, s2b = empty(x.size), empty(4 * T)
+    ok(lib.cuda_quantize_weights_per_row(q2b.vp, s2b.vp, yb.vp, T, H))
+    assert_bits_equal(ro, get(rob, np.uint16, (T, H)), "residual_out")
+    assert_bits_equal(q, get(q2b, np.int8, (T, H)), "codes")
+    assert_bits_equal(s.view(np.uint32), get(s2b, np.uint32, (T,)), "scales")
+
+
 @pytest.mark.parametrize("T,H", [(64, 4096), (9, 4100)])
 def test_add_rmsnorm_quant_bit_exact(lib, ora, T, H):
     banner(f"add+rmsnorm+int8 T={T} H={H}")

@@ -459,6 +459,36 @@ def test_norm_quant_with_nan_and_inf_inputs(ora):
     assert (q == qw).all() and (s == sw).all()
 
 
+@pytest.mark.parametrize("T,H", [(16, 96), (5, 4100), (3, 4096)])
+def test_fused_norm_quant_equals_its_composition(ora, T, H):
+    """The fused oracle functions equal the compositions they stand for, each
+    part pinned on its own above: rmsnorm_quant == quant_rows(rmsnorm) and
+    add_rmsnorm_quant == quant_rows(add_rmsnorm) with the same residual output,
+    bit for bit, including rows with NaN and inf in x or in the residual, a
+    zero row and a row whose sum overflows fp16."""
+    x = f16(RNG.standard_normal((T, H)) * 3)
+    r = f16(RNG.standard_normal((T, H)) * 2)
+    w = f16(1 + 0.02 * RNG.standard_normal(H))
+    x[0, 1] = 0x7E00                   # NaN in x
+    x[1, H - 1] = 0x7C00               # +inf in x
+    r[2, 3] = 0xFE00                   # NaN in the residual only
+    x[T - 1, :] = 0                    # zero row (plain form) ...
+    r[T - 1, :] = 0                    # ... and zero sum (residual form)
+    if T > 4:
+        x[3, 7], r[3, 7] = 0x7BFF, 0x7BFF  # 65504 + 65504 overflows to inf in the residual output
+    q, sc = ora.rmsnorm_quant(x, w, 1e-5)
+    qw, sw = ora.quant_rows(ora.rmsnorm(x, w, 1e-5))
+    assert (sc.view(np.uint32) == sw.view(np.uint32)).all()
+    assert (q == qw).all()
+    q, sc, ro = ora.add_rmsnorm_quant(x, r, w, 1e-5)
+    y, row = ora.add_rmsnorm(x, r, w, 1e-5)
+    qw, sw = ora.quant_rows(y)
+    assert (ro == row).all()
+    assert (sc.view(np.uint32) == sw.view(np.uint32)).all()
+    assert (q == qw).all()
+    assert sc[T - 1] == 1 and (q[T - 1] == 0).all()
+
+
 def test_quant_per_tensor_reference_kat(ora):
     # tests/quantize_test.go:20-87: U(-1, 1), n = 4096, scale within 0.01 of max/127,
     # round-trip error below 0.01.

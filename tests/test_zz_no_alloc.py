@@ -6,7 +6,11 @@ Checked through the C ABI against cuda_gemm_int8 itself (the same kernels and
 launch shapes, so the bar is bit-exact): two calls in a row, the second with a
 smaller input, so that the second reads none of the first call's leftovers;
 then shapes covering every kernel family, and device memory unchanged across
-calls. Shapes that only the hipBLASLt path takes are refused on the host.
+calls. From 1024 rows on the inputs are exact (activations on a 2^-e grid,
+power-of-two scales), on which any correct path gives fp16 of the exact
+product, so the comparison stays bit-exact whichever path cuda_gemm_int8
+takes there. Shapes that only the hipBLASLt path takes are refused on the
+host.
 """
 from __future__ import annotations
 
@@ -20,16 +24,25 @@ pytestmark = pytest.mark.gpu
 RNG = np.random.Generator(np.random.PCG64(97))
 
 
-def inputs(M, K, N):
-    a = np.asarray(RNG.standard_normal((M, K)), np.float32).astype(np.float16).view(np.uint16)
+# From this many rows of A on, cuda_gemm_int8 may take another path (matmul.hip, kLtMinM).
+LT_MIN_M = 1024
+
+
+def inputs(M, K, N, exact=False):
+    if exact:
+        e = min(6, 16 - int(np.ceil(np.log2(K))))   # every partial sum exact in fp32
+        a = (RNG.integers(-(2 ** e), 2 ** e + 1, (M, K)) * 2.0 ** -e).astype(np.float16).view(np.uint16)
+        s = (2.0 ** -RNG.integers(6, 10, N)).astype(np.float32)
+    else:
+        a = np.asarray(RNG.standard_normal((M, K)), np.float32).astype(np.float16).view(np.uint16)
+        s = RNG.uniform(1e-3, 1e-2, N).astype(np.float32)
     q = RNG.integers(-128, 128, (N, K)).astype(np.int8)
-    s = RNG.uniform(1e-3, 1e-2, N).astype(np.float32)
     return dev(a), dev(q), dev(s)
 
 
 def both(lib, M, K, N):
     """(cuda_gemm_int8 output, ng_gemm_int8_noalloc output) on the same inputs."""
-    ab, qb, sb = inputs(M, K, N)
+    ab, qb, sb = inputs(M, K, N, exact=M >= LT_MIN_M)
     c_ref, c_new = empty(2 * M * N), empty(2 * M * N)
     ok(lib.cuda_gemm_int8(c_ref.vp, ab.vp, qb.vp, sb.vp, M, K, N, True), "cuda_gemm_int8")
     ok(lib.ng_gemm_int8_noalloc(c_new.vp, ab.vp, qb.vp, sb.vp, M, K, N, True), "ng_gemm_int8_noalloc")
