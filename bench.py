@@ -34,6 +34,7 @@ Usage: python bench.py [--gpus 1] [--steps 50] [--warmup 5] [--no-cpu] [--no-ext
        python bench.py --profile-pass  (eager launches of every kernel for rocprofv3: the kernel trace and
                                         the --pmc FETCH_SIZE / WRITE_SIZE runs)
        python bench.py --gemm-only  (cuda_gemm_int8 timings only)
+       python bench.py --floors-only  (the access-pattern floor kernels only)
 """
 from __future__ import annotations
 
@@ -752,6 +753,183 @@ def gemm_extras(L, hip, stream):
     return out
 
 
+# ----------------------------------------------------------------------------- access-pattern floors
+
+# Hand-written kernels that move exactly the bytes of a library kernel, in its
+# access pattern, with no arithmetic: the time that pattern costs on this GPU.
+# They are measurement aids, not part of the library: compiled at run time
+# with hipRTC from this source and launched through the module API.
+FLOOR_SRC = r"""
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
+// One row of 64 V 16-byte vectors per one-wave workgroup, all loads first
+// (the row kernels' pattern). MODE 0: read only; 1: write 8 bytes per vector
+// (int8 codes of an fp16 row, 8-byte stores); 2: the same, 16-byte stores
+// after a lane-pair exchange; 3: write 16 bytes per vector (a 1:1 row copy);
+// 4: write only, 8 bytes per vector.
+template <int MODE, int V>
+__device__ void rows(void* out, const u32x4* x, unsigned* sink) {
+    const unsigned lane = threadIdx.x;
+    const u32x4* r = x + (unsigned long long)blockIdx.x * (64 * V);
+    u32x4 v[V];
+    if (MODE != 4) {
+#pragma unroll
+        for (int k = 0; k < V; ++k) v[k] = __builtin_nontemporal_load(r + lane + 64 * k);
+    } else {
+#pragma unroll
+        for (int k = 0; k < V; ++k) v[k] = u32x4{lane, (unsigned)k, blockIdx.x, 7u};
+    }
+    if (MODE == 0) {
+        u32x4 a = v[0];
+#pragma unroll
+        for (int k = 1; k < V; ++k) a ^= v[k];
+        if ((a[0] ^ a[1] ^ a[2] ^ a[3]) == 0x9e3779b9u) sink[0] = a[0];
+    } else if (MODE == 1 || MODE == 4) {
+        u32x2* q = (u32x2*)out + (unsigned long long)blockIdx.x * (64 * V);
+#pragma unroll
+        for (int k = 0; k < V; ++k) __builtin_nontemporal_store(u32x2{v[k][0] ^ v[k][1], v[k][2] ^ v[k][3]}, q + lane + 64 * k);
+    } else if (MODE == 2) {
+        char* q = (char*)out + (unsigned long long)blockIdx.x * (64 * V) * 8;
+        const bool odd = lane & 1;
+#pragma unroll
+        for (int k = 0; k < V; k += 2) {
+            const u32x2 c0 = {v[k][0] ^ v[k][1], v[k][2] ^ v[k][3]};
+            const u32x2 c1 = {v[k + 1][0] ^ v[k + 1][1], v[k + 1][2] ^ v[k + 1][3]};
+            const u32x2 send = odd ? c0 : c1;
+            const u32x2 recv = {(unsigned)__builtin_amdgcn_update_dpp(0, (int)send[0], 0xB1, 0xf, 0xf, false),
+                                (unsigned)__builtin_amdgcn_update_dpp(0, (int)send[1], 0xB1, 0xf, 0xf, false)};
+            const u32x4 o = odd ? u32x4{recv[0], recv[1], c1[0], c1[1]} : u32x4{c0[0], c0[1], recv[0], recv[1]};
+            const unsigned v0 = odd ? (lane - 1 + (k + 1) * 64) : (lane + k * 64);
+            __builtin_nontemporal_store(o, (u32x4*)(q + v0 * 8));
+        }
+    } else {
+        u32x4* y = (u32x4*)out + (unsigned long long)blockIdx.x * (64 * V);
+#pragma unroll
+        for (int k = 0; k < V; ++k) __builtin_nontemporal_store(v[k] ^ u32x4{1u, 2u, 3u, 4u}, y + lane + 64 * k);
+    }
+}
+extern "C" __global__ __launch_bounds__(64) void floor_rows_read(void* o, const u32x4* x, unsigned* s) { rows<0, 8>(o, x, s); }
+extern "C" __global__ __launch_bounds__(64) void floor_rows_code8(void* o, const u32x4* x, unsigned* s) { rows<1, 8>(o, x, s); }
+extern "C" __global__ __launch_bounds__(64) void floor_rows_code16(void* o, const u32x4* x, unsigned* s) { rows<2, 8>(o, x, s); }
+extern "C" __global__ __launch_bounds__(64) void floor_rows_copy(void* o, const u32x4* x, unsigned* s) { rows<3, 8>(o, x, s); }
+extern "C" __global__ __launch_bounds__(64) void floor_rows_write8(void* o, const u32x4* x, unsigned* s) { rows<4, 8>(o, x, s); }
+// Flat streams, one 16-byte vector per lane: a 1:1 copy, and 16 bytes in /
+// 8 bytes out.
+extern "C" __global__ __launch_bounds__(64) void floor_flat_copy(u32x4* y, const u32x4* x) {
+    const unsigned long long i = (unsigned long long)blockIdx.x * 64 + threadIdx.x;
+    __builtin_nontemporal_store(__builtin_nontemporal_load(x + i), y + i);
+}
+extern "C" __global__ __launch_bounds__(64) void floor_flat_code8(u32x2* q, const u32x4* x) {
+    const unsigned long long i = (unsigned long long)blockIdx.x * 64 + threadIdx.x;
+    const u32x4 v = __builtin_nontemporal_load(x + i);
+    __builtin_nontemporal_store(u32x2{v[0] ^ v[1], v[2] ^ v[3]}, q + i);
+}
+extern "C" __global__ __launch_bounds__(64) void floor_empty(unsigned* s) {
+    if (threadIdx.x == 1000u) s[0] = 1u;
+}
+"""
+
+
+class FloorKernels:
+    """FLOOR_SRC compiled for gfx950 with hipRTC and loaded as a module."""
+
+    def __init__(self, hip):
+        rtc = C.CDLL("libhiprtc.so")
+        prog = C.c_void_p()
+        if rtc.hiprtcCreateProgram(C.byref(prog), FLOOR_SRC.encode(), b"floors.hip", 0, None, None) != 0:
+            raise RuntimeError("hiprtcCreateProgram failed")
+        opts = [b"--offload-arch=gfx950", b"-O3"]
+        arr = (C.c_char_p * len(opts))(*opts)
+        rc = rtc.hiprtcCompileProgram(prog, len(opts), arr)
+        if rc != 0:
+            n = C.c_size_t()
+            rtc.hiprtcGetProgramLogSize(prog, C.byref(n))
+            log = C.create_string_buffer(n.value)
+            rtc.hiprtcGetProgramLog(prog, log)
+            raise RuntimeError(f"hiprtcCompileProgram failed: {log.value.decode(errors='replace')}")
+        n = C.c_size_t()
+        rtc.hiprtcGetCodeSize(prog, C.byref(n))
+        self.code = C.create_string_buffer(n.value)
+        rtc.hiprtcGetCode(prog, self.code)
+        rtc.hiprtcDestroyProgram(C.byref(prog))
+        self.hip = hip
+        self.mod = C.c_void_p()
+        hip.check(hip.h.hipModuleLoadData(C.byref(self.mod), self.code), "hipModuleLoadData")
+        self.fns = {}
+        hip.h.hipModuleLaunchKernel.argtypes = [C.c_void_p] + [C.c_uint] * 6 + [C.c_uint, C.c_void_p, C.c_void_p,
+                                                                                 C.c_void_p]
+
+    def fn(self, name):
+        if name not in self.fns:
+            f = C.c_void_p()
+            self.hip.check(self.hip.h.hipModuleGetFunction(C.byref(f), self.mod, name.encode()),
+                           "hipModuleGetFunction")
+            self.fns[name] = f
+        return self.fns[name]
+
+    def launch(self, name, grid, stream, *ptrs):
+        args = [C.c_void_p(p.value if isinstance(p, C.c_void_p) else p) for p in ptrs]
+        params = (C.c_void_p * len(args))(*[C.cast(C.byref(a), C.c_void_p) for a in args])
+        return self.hip.h.hipModuleLaunchKernel(self.fn(name), grid, 1, 1, 64, 1, 1, 0, stream, params, None)
+
+    def unload(self):
+        self.hip.h.hipModuleUnload(self.mod)
+
+
+def floor_extras(hip, stream):
+    """Each access pattern at Mistral-7B prefill sizes (T = H = 4096, fp16)
+    next to the library kernel that has it, timed like the kernels (a graph of
+    back-to-back launches over buffer pools touching more than 1 GB between
+    reuses of a buffer): the 50.3 MB norm+int8 pattern (read 33.5 MB, write
+    16.8 MB of codes) with 8- and 16-byte code stores and as a flat stream; the
+    67.1 MB 1:1 pattern of RMSNorm, RoPE Q and the gather as rows and as a flat
+    stream; the two halves alone; an empty grid of 4096 one-wave workgroups;
+    and flat copies at the sizes of RoPE K (16.8 MB) and of Llama-2-13B's
+    RMSNorm (167.8 MB)."""
+    fk = FloorKernels(hip)
+    T, H = 4096, 4096
+    xb, qb = 2 * T * H, T * H
+    nv = T * H // 8
+    sink = DB(256)
+    out = {}
+
+    def pools(in_bytes, out_bytes):
+        n = pool_slots(in_bytes + out_bytes)
+        return Pool(hip, in_bytes, n), Pool(hip, max(out_bytes, 256), n), n
+
+    def timed(name, grid, in_bytes, out_bytes, moved, extra_sink=True):
+        src, dst, n = pools(in_bytes, out_bytes)
+        hip.h.hipMemsetAsync.argtypes = [C.c_void_p, C.c_int, C.c_size_t, C.c_void_p]
+        hip.check(hip.h.hipMemsetAsync(src.buf.offset(0), 0x11, src.slot * src.n, None), "hipMemsetAsync")
+        hip.sync()
+        args = (lambda j: (dst.at(j), src.at(j), sink.vp)) if extra_sink else (lambda j: (dst.at(j), src.at(j)))
+        thunks = [(name, (lambda j=j: fk.launch(name, grid, stream, *args(j)))) for j in range(n)]
+        us = time_pool_kernel(hip, stream, thunks)
+        src.free()
+        dst.free()
+        return {"us": us, "bytes": moved, "GBps": moved / us / 1e3 if moved else None,
+                "frac": moved / us / 1e3 / PEAK_GBPS if moved else None}
+
+    out["rows_code8_50MB"] = timed("floor_rows_code8", T, xb, qb, xb + qb)
+    out["rows_code16_50MB"] = timed("floor_rows_code16", T, xb, qb, xb + qb)
+    out["flat_code8_50MB"] = timed("floor_flat_code8", nv // 64, xb, qb, xb + qb, extra_sink=False)
+    out["rows_copy_67MB"] = timed("floor_rows_copy", T, xb, xb, 2 * xb)
+    out["flat_copy_67MB"] = timed("floor_flat_copy", nv // 64, xb, xb, 2 * xb, extra_sink=False)
+    out["rows_read_33MB"] = timed("floor_rows_read", T, xb, 0, xb)
+    out["rows_write8_17MB"] = timed("floor_rows_write8", T, 256, qb, qb)
+    for label, b in (("flat_copy_17MB", 8 << 20), ("flat_copy_168MB", 2 * 8192 * 5120 * 2 // 2)):
+        out[label] = timed("floor_flat_copy", b // 16 // 64, b, b, 2 * b, extra_sink=False)
+    thunks = [("floor_empty", (lambda: hip.h.hipModuleLaunchKernel(
+        fk.fn("floor_empty"), T, 1, 1, 64, 1, 1, 0, stream,
+        (C.c_void_p * 1)(C.cast(C.byref(C.c_void_p(sink.ptr)), C.c_void_p)), None)))]
+    out["empty_4096_workgroups"] = {"us": time_pool_kernel(hip, stream, thunks)}
+    sink.free()
+    fk.unload()
+    out["note"] = ("hand-written kernels with a library kernel's access pattern and bytes and no arithmetic "
+                   "(compiled at run time by hipRTC from bench.py's FLOOR_SRC), timed as the kernels are")
+    return out
+
+
 # ----------------------------------------------------------------------------- CPU baseline
 
 def cpu_baseline(cfg, budget_s=10.0, sample_1t=256):
@@ -1057,6 +1235,8 @@ def main():
                     help="eager launches of every kernel for rocprofv3 (kernel trace and --pmc runs)")
     ap.add_argument("--gemm-only", action="store_true",
                     help="time only cuda_gemm_int8 at Mistral-7B's INT8 projections and print that JSON")
+    ap.add_argument("--floors-only", action="store_true",
+                    help="time only the access-pattern floor kernels and print that JSON")
     args = ap.parse_args()
     if args.gpus != 1:
         print(json.dumps({"error": "this build runs on one GPU: every kernel shards over tokens with no exchange, "
@@ -1074,6 +1254,9 @@ def main():
         return
     if args.gemm_only:
         print(json.dumps({"gemm_int8": gemm_extras(L, hip, stream)}), flush=True)
+        return
+    if args.floors_only:
+        print(json.dumps({"floors": floor_extras(hip, stream)}), flush=True)
         return
 
     cfg = W.CONFIGS[args.config]
@@ -1132,6 +1315,8 @@ def main():
                             "change in the engine (layer.cu:1584-1607)"}
         log("gather / rmsnorm+int8 / dequant")
         extra.update(extra_kernels(L, hip, stream))
+        log("access-pattern floors")
+        extra["floors"] = floor_extras(hip, stream)
         sized = [v for v in extra.values() if isinstance(v, dict) and "bytes" in v and "us" in v]
         xc = copy_times(hip, stream, [v["bytes"] for v in sized])
         for v in sized:

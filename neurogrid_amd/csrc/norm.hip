@@ -601,6 +601,12 @@ static int launch_rows(const char* name, int rows, const RowArgs& a0) {
                 NG_CHECK_LAUNCH(name);
                 return 0;
             }
+            //   H = 5120, T >= 4096: 5 waves of 2 vectors per lane (T = 8192, in
+            //   place: 54.96 vs 56.02 us with 2 waves of 5, 55.77 with 4 of 3)
+            if (a.nvec == 640 && rows >= 4096) {
+                nw = 5;
+                V = 2;
+            }
         }
         RowDispatch<T, NORM, ADD, QUANT>::launch(V, dim3(rows), dim3(nw * 64), a, rows >= 2048);
     } else {

@@ -1,16 +1,16 @@
 /* Exhaustive check of the division-free int8 codes the GPU kernels compute
- * (neurogrid_amd/csrc/ng_common.hpp), against the reference's rule
- * q = clamp(rint(v / s), -127, 127) with the IEEE quotient
+ * (qcode8 and qcode_int in neurogrid_amd/csrc/ng_common.hpp), against the
+ * reference's rule q = clamp(rint(v / s), -127, 127) with the IEEE quotient
  * (gpu/cuda/quantize.cu:292-313, half-to-even rounding), for every positive
  * finite fp16 row absmax m, s = RN(m / 127), and every finite fp16 v with
- * |v| <= m (the values a row with that absmax holds).
- *
- *   markstein (qcode8, qcode_int): z = RN(v inv), r = RN(v - z s),
- *       z1 = RN(z + r inv), code = low byte of RN(z1 + 1.5 2^23);
- *   bracket (qcode8_bracket): t_lo = RN(v inv_lo + 1.5 2^23),
- *       t_hi = RN(v inv_hi + 1.5 2^23), inv_lo = RN(inv (1 - 2^-22)),
- *       inv_hi = RN(inv (1 + 2^-22)); where t_lo == t_hi the code is the low
- *       byte of t_lo, otherwise the kernel falls back to the IEEE quotient.
+ * |v| <= m (the values a row with that absmax holds):
+ *   z = RN(v inv), r = RN(v - z s), z1 = RN(z + r inv) (Markstein's
+ *   correction step), code = low byte of RN(z1 + 1.5 2^23).
+ * Also counted, for comparison: the plain product z (without the correction)
+ * and a two-product bracket, t_lo = RN(v inv_lo + 1.5 2^23),
+ * t_hi = RN(v inv_hi + 1.5 2^23) with inv_lo / inv_hi = RN(inv (1 -/+ 2^-22)),
+ * which is right wherever t_lo == t_hi but leaves undecided every v / s near a
+ * half-integer, among them v = m / 2 (q = 63.5), common in fp16 rows.
  *
  * inv = RN(1 / s). Every operation is one IEEE fp32 rounding (fmaf is fused,
  * build with -ffp-contract=off), as on the GPU (v_fma_mix_f32 widens the fp16
@@ -36,8 +36,8 @@ static int low_code(float t) {
 int main(void) {
     const float M = 12582912.0f; /* 1.5 * 2^23 */
     const float c_lo = 1.0f - 0x1p-22f, c_hi = 1.0f + 0x1p-22f;
-    long long total = 0, bad_mk = 0, bad_br = 0, fallback = 0;
-#pragma omp parallel for reduction(+ : total, bad_mk, bad_br, fallback) schedule(dynamic, 32)
+    long long total = 0, bad_mk = 0, bad_br = 0, fallback = 0, bad_plain = 0;
+#pragma omp parallel for reduction(+ : total, bad_mk, bad_br, fallback, bad_plain) schedule(dynamic, 32)
     for (int mb = 1; mb < 0x7c00; ++mb) {
         const float m = h2f((uint16_t)mb);
         const float s = m / 127.0f;
@@ -53,6 +53,7 @@ int main(void) {
             const float r = fmaf(-z, s, v);
             const float z1 = fmaf(r, inv, z);
             if (low_code(z1 + M) != ref) ++bad_mk;
+            if (low_code(z + M) != ref) ++bad_plain;
             const float tl = fmaf(v, inv_lo, M), th = fmaf(v, inv_hi, M);
             if (tl == th) {
                 if (low_code(tl) != ref) ++bad_br;
@@ -62,7 +63,7 @@ int main(void) {
             ++total;
         }
     }
-    printf("pairs %lld markstein_wrong %lld bracket_wrong %lld bracket_fallback %lld\n", total, bad_mk, bad_br,
-           fallback);
+    printf("pairs %lld markstein_wrong %lld plain_wrong %lld bracket_wrong %lld bracket_undecided %lld\n", total,
+           bad_mk, bad_plain, bad_br, fallback);
     return (bad_mk || bad_br) ? 1 : 0;
 }

@@ -61,3 +61,22 @@ def test_bench_refuses_more_than_one_gpu():
     assert proc.returncode == 2
     line = json.loads(proc.stdout.strip().splitlines()[-1])
     assert "one GPU" in line["error"]
+
+
+def test_floor_kernels_compile_for_gfx950():
+    """The access-pattern floor kernels bench.py times compile with hipRTC for
+    gfx950 (compilation needs no GPU), so a GPU run never finds them broken."""
+    import ctypes as C
+
+    sys.path.insert(0, str(ROOT))
+    import bench
+
+    rtc = C.CDLL("libhiprtc.so")
+    prog = C.c_void_p()
+    assert rtc.hiprtcCreateProgram(C.byref(prog), bench.FLOOR_SRC.encode(), b"floors.hip", 0, None, None) == 0
+    opts = (C.c_char_p * 2)(b"--offload-arch=gfx950", b"-O3")
+    rc = rtc.hiprtcCompileProgram(prog, 2, opts)
+    n = C.c_size_t()
+    rtc.hiprtcGetCodeSize(prog, C.byref(n))
+    rtc.hiprtcDestroyProgram(C.byref(prog))
+    assert rc == 0 and n.value > 0
