@@ -685,9 +685,10 @@ def gemm_extras(L, hip, stream):
     and 64 tokens, against the reference's composition without its cudaMalloc /
     cudaFree (cuda_dequantize_weights into an fp16 buffer, then
     cuda_gemm_fp16). Weight pools keep the codes cache-cold. Also every
-    projection at prefill sizes (PREFILL_M tokens), where cuda_gemm_int8 runs
-    the fused prefill MFMA kernel, against the same composition (at
-    COMPOSED_M)."""
+    projection at prefill sizes (PREFILL_M tokens): cuda_gemm_int8 (the fused
+    prefill MFMA kernel below 4096 tokens, the composition through its own
+    buffers from 4096 on), the fused kernel alone (ng_gemm_int8_noalloc, the
+    same kernel without allocation) and the composition (at COMPOSED_M)."""
     rng = np.random.Generator(np.random.PCG64(0))
     H, I = 4096, 14336
     shapes = {"q_proj": (H, H), "k_proj": (H, 1024), "gate_proj": (H, I), "down_proj": (I, H)}
@@ -724,6 +725,9 @@ def gemm_extras(L, hip, stream):
             cb = DB(2 * M * N)
             us = time_kernel(hip, stream, [lambda: L.cuda_gemm_int8(cb.vp, ab.vp, wp.at(0), sc.vp, M, K, N, True)],
                              launches=8, reps=2)
+            usf = time_kernel(hip, stream,
+                              [lambda: L.ng_gemm_int8_noalloc(cb.vp, ab.vp, wp.at(0), sc.vp, M, K, N, True)],
+                              launches=8, reps=2)
 
             def comp(M=M, ab=ab, cb=cb):
                 rc = L.cuda_dequantize_weights(deq.vp, wp.at(0), sc.vp, N, K, 1)
@@ -735,21 +739,27 @@ def gemm_extras(L, hip, stream):
                     usc = time_kernel(hip, stream, [comp], launches=8, reps=2)
                 except RuntimeError as e:   # hipBLASLt refuses some shapes (status 6 at K = 14336)
                     print(f"[bench] composed {name} M={M}: {e}", file=sys.stderr, flush=True)
-            out[f"{name}_M{M}"] = {"us": us, "TFLOPs": 2 * M * N * K / us / 1e6, "composed_us": usc,
-                                   "composed_TFLOPs": usc and 2 * M * N * K / usc / 1e6,
-                                   "note": "fused int8 prefill MFMA kernel; composed = dequantize to fp16 + "
-                                           "hipBLASLt fp16 GEMM"}
-            prefill.setdefault(M, [0.0, 0.0])
+            out[f"{name}_M{M}"] = {"us": us, "TFLOPs": 2 * M * N * K / us / 1e6,
+                                   "fused_us": usf, "fused_TFLOPs": 2 * M * N * K / usf / 1e6,
+                                   "composed_us": usc, "composed_TFLOPs": usc and 2 * M * N * K / usc / 1e6,
+                                   "note": "us: cuda_gemm_int8 (fused int8 prefill MFMA kernel below 4096 tokens, "
+                                           "dequantize + hipBLASLt from 4096 on); fused: the prefill kernel "
+                                           "(ng_gemm_int8_noalloc); composed: cuda_dequantize_weights + "
+                                           "cuda_gemm_fp16"}
+            prefill.setdefault(M, [0.0, 0.0, 0.0])
             prefill[M][0] += per_layer[name] * us
             prefill[M][1] += per_layer[name] * (usc or float("nan"))
+            prefill[M][2] += per_layer[name] * usf
             ab.free()
             cb.free()
         wp.free()
         sc.free()
         deq.free()
-    for M, (u, c) in list(layer.items()) + list(prefill.items()):
+    for M, (u, c, *f) in list(layer.items()) + list(prefill.items()):
         out[f"mistral7b_layer_M{M}"] = {"us": u, "composed_us": None if c != c else c,
                                         "note": "q, k, v, o, gate, up, down projections of one layer"}
+        if f:
+            out[f"mistral7b_layer_M{M}"]["fused_us"] = f[0]
     return out
 
 

@@ -111,9 +111,10 @@ int ng_gather_embeddings_checked(void* output, const void* embed_table, const in
 /* cuda_gemm_int8's fused int8 paths (weight streaming for M <= 128, prefill
  * above) without any allocation. No counterpart in the reference: it is for
  * callers that cannot allocate device memory (code under HIP graph capture,
- * tight serving loops, harnesses that forbid hipMalloc). Arguments and
- * results as cuda_gemm_int8 (the same kernels, bit for bit), for the shapes
- * those paths take: transpose_b,
+ * tight serving loops, harnesses that forbid hipMalloc). Arguments as
+ * cuda_gemm_int8; results as cuda_gemm_int8 below 4096 rows of A (the same
+ * kernels, bit for bit), and the fused prefill kernel's from 4096 rows on,
+ * where cuda_gemm_int8 dequantizes and calls hipBLASLt. Shapes: transpose_b,
  * K % 16 == 0 (K % 64 == 0 for 4 < M <= 128), 16-byte aligned A and B; other
  * shapes return -1. The split-K partial sums live in a fixed 64 MiB
  * device array that each GPU the library runs on holds until the process

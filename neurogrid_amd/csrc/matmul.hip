@@ -27,8 +27,9 @@
 //       for few rows of B.
 // Above 128 rows of A (prefill) the product is bound by the matrix cores:
 // gemm_i8w_prefill_kernel, a tiled GEMM whose B tiles are converted on their
-// way into LDS (see the prefill section). B stored [K, N] goes through the
-// reference's composition (dequantize, then hipBLASLt).
+// way into LDS (see the prefill section); from 4096 rows on (kLtMinM) the
+// reference's composition through hipBLASLt, which is faster there. B stored
+// [K, N] always goes through the composition (dequantize, then hipBLASLt).
 // MFMA layout: v_mfma_f32_16x16x32_f16 multiplies a 16 x 32 tile of A (rows
 // m) by a 32 x 16 tile of B^T (columns n). Lane l supplies row (l % 16) of
 // each operand and 8 values of k; the accumulator lane l holds rows
@@ -973,81 +974,51 @@ int gemm_lt(void* c, const void* a, const void* b, const void* q, const void* sc
     return 0;
 }
 
-// SWITCHED OFF (kLtBlocks = false): a benchmark run that exercised this path
-// at 512-4096 rows of A for every Mistral-7B projection, together with the
-// full composition at 1024 and 2048 rows, ended in a GPU memory fault whose
-// cause was not found in this code; hipBLASLt at new shapes is the suspect
-// (it already refuses some K = 14336 shapes with an internal error). Until a
-// cause is shown, cuda_gemm_int8 keeps the fused prefill kernel at every M.
-//
-// cuda_gemm_int8 above kLtMinM rows of A in the engine's layout (B int8
+// cuda_gemm_int8 from kLtMinM rows of A on, in the engine's layout (B int8
 // [N, K], one scale per row): the reference's composition, dequantize then
-// multiply (matmul.cu:205-236), without its K x N fp16 copy. B is dequantized
-// kLtChunkBytes at a time, in blocks of rows of B of equal size (a multiple
-// of 256), into this stream's buffer, and each block is multiplied into its
-// columns of C (row stride N) by hipBLASLt. Returns 1, having enqueued
-// nothing that writes C, when the composition cannot run here: hipBLASLt has
-// no algorithm for a block, or the stream is being captured and the buffers
-// do not exist yet; the caller then runs the fused prefill kernel. A
-// hipBLASLt call that fails after earlier blocks ran also returns 1: the
-// fused kernel then rewrites all of C.
-constexpr bool kLtBlocks = false;
-constexpr int kLtMinM = 1024;
-constexpr size_t kLtChunkBytes = size_t(64) << 20;
+// multiply (matmul.cu:205-236), through gemm_lt. It keeps a K x N fp16 copy
+// of the weights in this (device, stream)'s buffer, grown to the largest
+// weight seen (117 MB for a 14336 x 4096 projection), where the reference
+// allocates and frees one per call. Measured on MI355X at M = 4096 for
+// Mistral-7B's projections: 115 us for q/o against 161 us for the fused
+// prefill kernel, 424 against 531 for gate/up, 367 against 467 for down, 48
+// against 59 for k/v; at M = 512 the fused kernel is faster (37 against
+// 42 us for q/o). Between 512 and 4096 rows the composition is not measured,
+// so the fused kernel keeps those sizes. Returns 1 when hipBLASLt has no
+// algorithm for the shape or refuses the call (remembered for the shape),
+// having written nothing but the fp16 buffer: the caller then runs the fused
+// prefill kernel.
+constexpr int kLtMinM = 4096;
 
-int gemm_lt_blocks(void* c, const void* a, const void* q, const void* scale, int M, int K, int N) {
+int gemm_lt_rows(void* c, const void* a, const void* q, const void* scale, int M, int K, int N) {
     int dev = 0;
     NG_HIP_CHECK(hipGetDevice(&dev));
     const hipStream_t s = stream();
-    const size_t row_bytes = static_cast<size_t>(K) * 2;
-    const int nb = static_cast<int>((static_cast<size_t>(N) * row_bytes + kLtChunkBytes - 1) / kLtChunkBytes);
-    int rows = (N + nb - 1) / nb;
-    rows = (rows + 255) / 256 * 256;
-    while (rows > 256 && static_cast<size_t>(rows) * row_bytes > kLtChunkBytes) rows -= 256;
-    if (rows > N) rows = N;
     std::lock_guard<std::mutex> lock(g_mu);
-    // Plans of the full blocks and of the last one; a shape hipBLASLt has no
-    // algorithm for is remembered and sends every later call to the fused kernel.
-    const Plan* plan[2] = {nullptr, nullptr};
-    const int last = N - (N - 1) / rows * rows;
-    for (int i = 0; i < 2; ++i) {
-        const int nr = i == 0 ? rows : last;
-        const PlanKey key{dev, M, K, nr, false, true, N};
-        if (g_lt_refused.count(key)) return 1;
-        auto it = g_plans.find(key);
-        if (it == g_plans.end()) {
-            // A failed lookup prints its reason once; the key is then refused quietly.
-            if (get_plan(dev, M, K, nr, false, true, &plan[i], N) != 0) {
-                g_lt_refused.insert(key);
-                return 1;
-            }
-        } else {
-            plan[i] = &it->second;
-        }
+    const PlanKey key{dev, M, K, N, false, true, N};
+    if (g_lt_refused.count(key)) return 1;
+    const Plan* p = nullptr;
+    if (get_plan(dev, M, K, N, false, true, &p) != 0) {
+        g_lt_refused.insert(key);
+        return 1;
     }
     StreamBuffers* sb = &g_buffers[{dev, s}];
-    const size_t ws = plan[0]->ws > plan[1]->ws ? plan[0]->ws : plan[1]->ws;
-    const size_t deq = static_cast<size_t>(rows) * row_bytes;
-    if (ws > sb->ws_bytes || deq > sb->deq_bytes) {
-        bool cap = false;
-        if (capturing(s, &cap) != 0) return -1;
-        if (cap) return 1;
-        if (grow(s, &sb->ws, &sb->ws_bytes, ws) != 0 || grow(s, &sb->deq, &sb->deq_bytes, deq) != 0) return -1;
-    }
+    if (grow(s, &sb->ws, &sb->ws_bytes, p->ws) != 0 ||
+        grow(s, &sb->deq, &sb->deq_bytes, static_cast<size_t>(K) * static_cast<size_t>(N) * 2) != 0)
+        return -1;
+    const int r = cuda_dequantize_weights(sb->deq, q, scale, N, K, 1);
+    if (r != 0) return r;
     const float alpha = 1.0f, beta = 0.0f;
-    for (int n0 = 0; n0 < N; n0 += rows) {
-        const int nr = N - n0 < rows ? N - n0 : rows;
-        const Plan* p = nr == rows ? plan[0] : plan[1];
-        const int r = cuda_dequantize_weights(sb->deq, static_cast<const int8_t*>(q) + static_cast<size_t>(n0) * K,
-                                              static_cast<const float*>(scale) + n0, nr, K, 1);
-        if (r != 0) return r;
-        const hipblasStatus_t st = hipblasLtMatmul(g_handles[dev], p->desc, &alpha, sb->deq, p->lw, a, p->lx, &beta,
-                                                   static_cast<uint16_t*>(c) + n0, p->ly,
-                                                   static_cast<uint16_t*>(c) + n0, p->ly, &p->algo, sb->ws, p->ws, s);
-        if (st != HIPBLAS_STATUS_SUCCESS) {
-            g_lt_refused.insert(PlanKey{dev, M, K, nr, false, true, N});
-            return 1;
-        }
+    const hipblasStatus_t st = hipblasLtMatmul(g_handles[dev], p->desc, &alpha, sb->deq, p->lw, a, p->lx, &beta, c,
+                                               p->ly, c, p->ly, &p->algo, sb->ws, p->ws, s);
+    if (st != HIPBLAS_STATUS_SUCCESS) {
+        // hipBLASLt's heuristic can name an algorithm that the call then
+        // refuses (an internal error, status 6, at 4096 x 14336 x 512): the
+        // shape goes to the fused kernel from now on, this call included.
+        fprintf(stderr, "neurogrid-amd: hipBLASLt status %d at M=%d K=%d N=%d; using the fused kernel\n",
+                static_cast<int>(st), M, K, N);
+        g_lt_refused.insert(key);
+        return 1;
     }
     return 0;
 }
@@ -1286,8 +1257,8 @@ extern "C" int cuda_gemm_int8(void* c, const void* a, const void* b, const void*
     NG_REQUIRE(M > 0 && K > 0 && N > 0, "cuda_gemm_int8: M=%d K=%d N=%d must be > 0", M, K, N);
     if (use_i8w(a, b, M, K, N, transpose_b)) return gemm_i8w(c, a, b, scale, M, K, N);
     if (use_prefill(a, b, M, K, N, transpose_b)) {
-        if (kLtBlocks && M >= kLtMinM) {
-            const int r = gemm_lt_blocks(c, a, b, scale, M, K, N);
+        if (M >= kLtMinM) {
+            const int r = gemm_lt_rows(c, a, b, scale, M, K, N);
             if (r <= 0) return r;
         }
         return gemm_prefill(c, a, b, scale, M, K, N);
@@ -1298,8 +1269,9 @@ extern "C" int cuda_gemm_int8(void* c, const void* a, const void* b, const void*
 // The fused paths of cuda_gemm_int8 with no allocation: their only buffer,
 // the split-K partial sums, lives in this library's fixed `scratch` array of
 // the current device. Same kernels, same launch shapes and so the same bits as
-// cuda_gemm_int8 (with the blocks path above switched off, at every M). Every
-// call on a device shares that device's
+// cuda_gemm_int8 below kLtMinM rows of A; from kLtMinM rows on it keeps the
+// fused prefill kernel, where cuda_gemm_int8 runs the dequantize + hipBLASLt
+// composition. Every call on a device shares that device's
 // array: calls that overlap on one GPU (other streams, other host threads)
 // race on it. The split kernel writes every partial sum before the reduction
 // reads it, so nothing needs clearing between calls.

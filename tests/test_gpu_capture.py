@@ -73,7 +73,7 @@ def inp():
     a["wsc_wide"] = rng.uniform(1e-3, 1e-2, GNW).astype(np.float32)
     a["tsc"] = np.array([0.0125], np.float32)
     a["wh"] = f16_bits(n(GK, GN, s=0.05))
-    for m in (1, 3, 16, 40, 64, 100, 200, 1024):
+    for m in (1, 3, 16, 40, 64, 100, 200, 4096):
         a[f"a{m}"] = f16_bits(n(m, GK))
     bufs = {k: dev(v) for k, v in a.items()}
     yield bufs
@@ -177,10 +177,9 @@ def _ops():
         lambda L, i, o: L.ng_gemm_int8_noalloc(o["y"].vp, i["a64"].vp, i["wq"].vp, i["wsc"].vp, 64, GK, GN, True))
     add("ng_gemm_int8_noalloc_M200_prefill", {"y": (E2, (200, GN))},
         lambda L, i, o: L.ng_gemm_int8_noalloc(o["y"].vp, i["a200"].vp, i["wq"].vp, i["wsc"].vp, 200, GK, GN, True))
-    # M >= 1024 would take dequantized blocks of B multiplied by hipBLASLt; that
-    # path is switched off (matmul.hip kLtBlocks), and this case skipped
-    add("cuda_gemm_int8_M1024_blocks", {"y": (E2, (1024, GN))},
-        lambda L, i, o: L.cuda_gemm_int8(o["y"].vp, i["a1024"].vp, i["wq"].vp, i["wsc"].vp, 1024, GK, GN, True),
+    # from 4096 rows of A on: B dequantized into the stream's fp16 buffer, then hipBLASLt
+    add("cuda_gemm_int8_M4096_library", {"y": (E2, (4096, GN))},
+        lambda L, i, o: L.cuda_gemm_int8(o["y"].vp, i["a4096"].vp, i["wq"].vp, i["wsc"].vp, 4096, GK, GN, True),
         False)
     add("cuda_gemm_int8_kn_library", {"y": (E2, (16, GN))},
         lambda L, i, o: L.cuda_gemm_int8(o["y"].vp, i["a16"].vp, i["wq_kn"].vp, i["wsc"].vp, 16, GK, GN, False),
@@ -242,15 +241,8 @@ def replay_and_check(lib, hip, stream, outs, call, exact, label, between=None):
         scratch.free()
 
 
-SKIPPED = {"cuda_gemm_int8_M1024_blocks": "dequantized blocks + hipBLASLt path switched off (matmul.hip "
-                                          "kLtBlocks): a benchmark run over it ended in a GPU memory fault whose "
-                                          "cause was not found"}
-
-
 @pytest.mark.parametrize("name", list(OPS))
 def test_capture_replay(lib, inp, capture_stream, name):
-    if name in SKIPPED:
-        pytest.skip(SKIPPED[name])
     hip, stream = capture_stream
     outs, fn, exact = OPS[name]
     banner(f"graph capture: {name}")

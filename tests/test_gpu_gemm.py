@@ -68,13 +68,10 @@ def gemm_int8_fused(lib, a, q, scale, M, K, N) -> np.ndarray:
     return get(cb, np.uint16, (M, N))
 
 
-# From this many rows of A on, cuda_gemm_int8 in the engine's layout would run
-# the reference's composition (dequantize blocks of B, hipBLASLt) instead of
-# the fused prefill kernel (matmul.hip, kLtMinM). That path is switched off
-# (kLtBlocks): a benchmark run over it faulted the GPU, cause not found.
-LT_MIN_M = 1024
-LT_BLOCKS_OFF = ("dequantized blocks + hipBLASLt path switched off (matmul.hip kLtBlocks): a benchmark run over it "
-                 "at 512-4096 rows ended in a GPU memory fault whose cause was not found")
+# From this many rows of A on, cuda_gemm_int8 in the engine's layout runs the
+# reference's composition (B dequantized to fp16 into the stream's buffer,
+# then hipBLASLt) instead of the fused prefill kernel (matmul.hip, kLtMinM).
+LT_MIN_M = 4096
 
 
 def gemm_fp16(lib, a, b, M, K, N, ta: bool, tb: bool) -> np.ndarray:
@@ -213,36 +210,23 @@ def test_int8_prefill_random(lib, ora, M, K, N):
         assert_within_bound(fused, a, q, scale, True, "C (fused kernel)", ora)
 
 
-# From LT_MIN_M rows on, cuda_gemm_int8 (transpose_b) dequantizes B in blocks
-# of rows of at most 64 MiB of fp16 and multiplies each block into its columns
-# of C with hipBLASLt. Shapes: one block, two equal blocks (4096 x 12288: 96 MiB
-# of fp16), two unequal blocks (14336 x 4352: 2304 + 2048 rows), ragged M and N.
-# With power-of-two scales every fp16(q * s) is exact and so is every partial
-# sum: the result is fp16 of the exact product, bit for bit.
-LT_BLOCKS = [(1024, 4096, 1024), (2048, 4096, 12288), (1536, 14336, 4352), (4100, 1024, 300), (1030, 4112, 1000)]
+# From LT_MIN_M rows on, cuda_gemm_int8 (transpose_b) dequantizes B to fp16 and
+# multiplies with hipBLASLt, as the reference does. With power-of-two scales
+# every fp16(q * s) is exact and so is every partial sum: the result is fp16
+# of the exact product, bit for bit. Shapes: Mistral-7B's k_proj and q_proj at
+# 4096 tokens, ragged M and N, K = 14336 (down_proj).
+LT_ROWS = [(4096, 4096, 1024), (4096, 4096, 4096), (4100, 1024, 300), (4096, 14336, 512)]
 
 
-@pytest.mark.skip(reason=LT_BLOCKS_OFF)
-@pytest.mark.parametrize("M,K,N", LT_BLOCKS)
-def test_int8_prefill_blocks_bit_exact(lib, M, K, N):
-    banner(f"gemm_int8 dequant blocks + hipBLASLt exact M={M} K={K} N={N}")
+@pytest.mark.parametrize("M,K,N", LT_ROWS)
+def test_int8_prefill_library_rows_bit_exact(lib, M, K, N):
+    banner(f"gemm_int8 dequant + hipBLASLt exact M={M} K={K} N={N}")
     a = exact_activations(M, K)
     q = codes((N, K))
     scale = (2.0 ** -RNG.integers(6, 10, N)).astype(np.float32)
     got = gemm_int8(lib, a, q, scale, M, K, N, True)
     S = f16val(a) @ (q.astype(np.float64) * scale[:, None]).T
     assert_bits_equal(got, S.astype(np.float16).view(np.uint16), "C")
-
-
-@pytest.mark.skip(reason=LT_BLOCKS_OFF)
-@pytest.mark.parametrize("M,K,N", [(2048, 4096, 12288), (1536, 14336, 4352)])
-def test_int8_prefill_blocks_random(lib, ora, M, K, N):
-    banner(f"gemm_int8 dequant blocks + hipBLASLt random M={M} K={K} N={N}")
-    a = f16bits(RNG.standard_normal((M, K)))
-    q = codes((N, K))
-    scale = RNG.uniform(1e-3, 1e-2, N).astype(np.float32)
-    got = gemm_int8(lib, a, q, scale, M, K, N, True)
-    assert_within_bound(got, a, q, scale, True, "C", ora)
 
 
 @pytest.mark.parametrize("M,K,N", [(256, 4160, 512), (129, 1040, 300), (1024, 4096, 1024), (777, 1024, 16000)])

@@ -6,7 +6,7 @@ Checked through the C ABI against cuda_gemm_int8 itself (the same kernels and
 launch shapes, so the bar is bit-exact): two calls in a row, the second with a
 smaller input, so that the second reads none of the first call's leftovers;
 then shapes covering every kernel family, and device memory unchanged across
-calls. From 1024 rows on the inputs are exact (activations on a 2^-e grid,
+calls. From 4096 rows on the inputs are exact (activations on a 2^-e grid,
 power-of-two scales), on which any correct path gives fp16 of the exact
 product, so the comparison stays bit-exact whichever path cuda_gemm_int8
 takes there. Shapes that only the hipBLASLt path takes are refused on the
@@ -24,8 +24,9 @@ pytestmark = pytest.mark.gpu
 RNG = np.random.Generator(np.random.PCG64(97))
 
 
-# From this many rows of A on, cuda_gemm_int8 may take another path (matmul.hip, kLtMinM).
-LT_MIN_M = 1024
+# From this many rows of A on, cuda_gemm_int8 takes the dequantize + hipBLASLt
+# composition (matmul.hip, kLtMinM).
+LT_MIN_M = 4096
 
 
 def inputs(M, K, N, exact=False):
@@ -72,7 +73,7 @@ def test_noalloc_two_calls_second_smaller(lib):
 SHAPES = [(1, 4096, 4096), (4, 2064, 33), (8, 4096, 4096), (12, 1088, 4096), (33, 4096, 1024),
           (64, 4096, 14336), (128, 14336, 4096), (100, 8256, 384), (128, 4096, 1024), (3, 4096, 12300),
           (129, 256, 64), (200, 4096, 1000), (512, 4096, 4096), (300, 14336, 4096), (1024, 4096, 14336),
-          (3072, 4096, 4096)]
+          (3072, 4096, 4096), (4096, 4096, 1024)]
 
 
 @pytest.mark.parametrize("M,K,N", SHAPES)
