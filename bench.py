@@ -818,6 +818,71 @@ __device__ void rows(void* out, const u32x4* x, unsigned* sink) {
         for (int k = 0; k < V; ++k) __builtin_nontemporal_store(v[k] ^ u32x4{1u, 2u, 3u, 4u}, y + lane + 64 * k);
     }
 }
+// The int8 row pattern with its scale stores (one word per row into `sink`,
+// 4096 rows): R rows per one-wave workgroup, every load first; or a
+// persistent grid striding over the rows, the next row's loads issued before
+// the current row is stored.
+template <int R>
+__device__ void rows_code8_scales(void* out, const u32x4* x, unsigned* sink) {
+    const unsigned lane = threadIdx.x;
+    const unsigned row0 = blockIdx.x * R;
+    u32x4 v[R][8];
+#pragma unroll
+    for (int j = 0; j < R; ++j)
+#pragma unroll
+        for (int k = 0; k < 8; ++k) v[j][k] = __builtin_nontemporal_load(x + (unsigned long long)(row0 + j) * 512 + lane + 64 * k);
+#pragma unroll
+    for (int j = 0; j < R; ++j) {
+        unsigned m = 0;
+#pragma unroll
+        for (int k = 0; k < 8; ++k) m ^= v[j][k][0] ^ v[j][k][3];
+        m ^= (unsigned)__builtin_amdgcn_update_dpp(0, (int)m, 0xB1, 0xf, 0xf, false);
+        u32x2* q = (u32x2*)out + (unsigned long long)(row0 + j) * 512;
+#pragma unroll
+        for (int k = 0; k < 8; ++k) __builtin_nontemporal_store(u32x2{v[j][k][0] ^ v[j][k][1], v[j][k][2] ^ v[j][k][3] ^ m}, q + lane + 64 * k);
+        if (lane == 0) sink[row0 + j] = m;
+    }
+}
+extern "C" __global__ __launch_bounds__(64) void floor_rows_code8_scales(void* o, const u32x4* x, unsigned* s) { rows_code8_scales<1>(o, x, s); }
+extern "C" __global__ __launch_bounds__(64) void floor_rows4_code8_scales(void* o, const u32x4* x, unsigned* s) { rows_code8_scales<4>(o, x, s); }
+extern "C" __global__ __launch_bounds__(64) void floor_persistent_code8_scales(void* o, const u32x4* x, unsigned* s) {
+    const unsigned lane = threadIdx.x, G = gridDim.x;
+    unsigned r = blockIdx.x;
+    u32x4 a[8], b[8];
+#pragma unroll
+    for (int k = 0; k < 8; ++k) a[k] = __builtin_nontemporal_load(x + (unsigned long long)r * 512 + lane + 64 * k);
+    while (r < 4096u) {
+        const unsigned rn = r + G < 4096u ? r + G : r;
+#pragma unroll
+        for (int k = 0; k < 8; ++k) b[k] = __builtin_nontemporal_load(x + (unsigned long long)rn * 512 + lane + 64 * k);
+        __builtin_amdgcn_sched_barrier(0);
+        unsigned m = 0;
+#pragma unroll
+        for (int k = 0; k < 8; ++k) m ^= a[k][0] ^ a[k][3];
+        u32x2* q = (u32x2*)o + (unsigned long long)r * 512;
+#pragma unroll
+        for (int k = 0; k < 8; ++k) __builtin_nontemporal_store(u32x2{a[k][0] ^ a[k][1], a[k][2] ^ a[k][3] ^ m}, q + lane + 64 * k);
+        if (lane == 0) s[r] = m;
+        if (rn == r) break;
+#pragma unroll
+        for (int k = 0; k < 8; ++k) a[k] = b[k];
+        r = rn;
+    }
+}
+// A 1:1 row copy, four rows per one-wave workgroup, every load first.
+extern "C" __global__ __launch_bounds__(64) void floor_rows4_copy(u32x4* y, const u32x4* x) {
+    const unsigned lane = threadIdx.x;
+    const unsigned long long row0 = (unsigned long long)blockIdx.x * 4;
+    u32x4 v[4][8];
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+#pragma unroll
+        for (int k = 0; k < 8; ++k) v[j][k] = __builtin_nontemporal_load(x + (row0 + j) * 512 + lane + 64 * k);
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+#pragma unroll
+        for (int k = 0; k < 8; ++k) __builtin_nontemporal_store(v[j][k] ^ u32x4{1u, 2u, 3u, 4u}, y + (row0 + j) * 512 + lane + 64 * k);
+}
 extern "C" __global__ __launch_bounds__(64) void floor_rows_read(void* o, const u32x4* x, unsigned* s) { rows<0, 8>(o, x, s); }
 extern "C" __global__ __launch_bounds__(64) void floor_rows_code8(void* o, const u32x4* x, unsigned* s) { rows<1, 8>(o, x, s); }
 extern "C" __global__ __launch_bounds__(64) void floor_rows_code16(void* o, const u32x4* x, unsigned* s) { rows<2, 8>(o, x, s); }
@@ -893,14 +958,16 @@ def floor_extras(hip, stream):
     reuses of a buffer): the 50.3 MB norm+int8 pattern (read 33.5 MB, write
     16.8 MB of codes) with 8- and 16-byte code stores and as a flat stream; the
     67.1 MB 1:1 pattern of RMSNorm, RoPE Q and the gather as rows and as a flat
-    stream; the two halves alone; an empty grid of 4096 one-wave workgroups;
-    and flat copies at the sizes of RoPE K (16.8 MB) and of Llama-2-13B's
-    RMSNorm (167.8 MB)."""
+    stream; the two halves alone; the int8 pattern with its scale stores, one
+    and four rows per wave and as a persistent grid of 1024 waves; the 1:1
+    pattern four rows per wave; empty grids of 1 to 16384 one-wave workgroups
+    (the fixed cost of a launch); and flat copies at the sizes of RoPE K
+    (16.8 MB) and of Llama-2-13B's RMSNorm (167.8 MB)."""
     fk = FloorKernels(hip)
     T, H = 4096, 4096
     xb, qb = 2 * T * H, T * H
     nv = T * H // 8
-    sink = DB(256)
+    sink = DB(4 * T)
     out = {}
 
     def pools(in_bytes, out_bytes):
@@ -921,6 +988,10 @@ def floor_extras(hip, stream):
                 "frac": moved / us / 1e3 / PEAK_GBPS if moved else None}
 
     out["rows_code8_50MB"] = timed("floor_rows_code8", T, xb, qb, xb + qb)
+    out["rows_code8_scales_50MB"] = timed("floor_rows_code8_scales", T, xb, qb, xb + qb + 4 * T)
+    out["rows4_code8_scales_50MB"] = timed("floor_rows4_code8_scales", T // 4, xb, qb, xb + qb + 4 * T)
+    out["persistent1024_code8_scales_50MB"] = timed("floor_persistent_code8_scales", 1024, xb, qb, xb + qb + 4 * T)
+    out["rows4_copy_67MB"] = timed("floor_rows4_copy", T // 4, xb, xb, 2 * xb, extra_sink=False)
     out["rows_code16_50MB"] = timed("floor_rows_code16", T, xb, qb, xb + qb)
     out["flat_code8_50MB"] = timed("floor_flat_code8", nv // 64, xb, qb, xb + qb, extra_sink=False)
     out["rows_copy_67MB"] = timed("floor_rows_copy", T, xb, xb, 2 * xb)
@@ -929,10 +1000,11 @@ def floor_extras(hip, stream):
     out["rows_write8_17MB"] = timed("floor_rows_write8", T, 256, qb, qb)
     for label, b in (("flat_copy_17MB", 8 << 20), ("flat_copy_168MB", 2 * 8192 * 5120 * 2 // 2)):
         out[label] = timed("floor_flat_copy", b // 16 // 64, b, b, 2 * b, extra_sink=False)
-    thunks = [("floor_empty", (lambda: hip.h.hipModuleLaunchKernel(
-        fk.fn("floor_empty"), T, 1, 1, 64, 1, 1, 0, stream,
-        (C.c_void_p * 1)(C.cast(C.byref(C.c_void_p(sink.ptr)), C.c_void_p)), None)))]
-    out["empty_4096_workgroups"] = {"us": time_pool_kernel(hip, stream, thunks)}
+    for grid in (1, 1024, 4096, 16384):
+        thunks = [("floor_empty", (lambda grid=grid: hip.h.hipModuleLaunchKernel(
+            fk.fn("floor_empty"), grid, 1, 1, 64, 1, 1, 0, stream,
+            (C.c_void_p * 1)(C.cast(C.byref(C.c_void_p(sink.ptr)), C.c_void_p)), None)))]
+        out[f"empty_{grid}_workgroups"] = {"us": time_pool_kernel(hip, stream, thunks)}
     sink.free()
     fk.unload()
     out["note"] = ("hand-written kernels with a library kernel's access pattern and bytes and no arithmetic "
