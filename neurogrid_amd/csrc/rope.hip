@@ -483,12 +483,14 @@ static int launch_rope_wave(const char* name, void* out, const void* in, void* o
     const long long waves = static_cast<long long>(tokens) * G;
     NG_REQUIRE(waves < (1ll << 31), "%s: tensor too large", name);
     // One-wave workgroups for one pass per wave from 8192 tokens on and for
-    // tensors up to 8 MiB, four-wave ones otherwise. Measured on MI355X, four
-    // against one wave per workgroup: Llama-2-13B's Q (8192 x 40 heads)
-    // 29.30 vs 28.67 us, Q at T = 64 2.20 vs 2.11 us; Q and K in one launch at
+    // tensors up to 1 MiB (decode), four-wave ones otherwise. Measured on
+    // MI355X, four against one wave per workgroup: Llama-2-13B's Q (8192 x 40
+    // heads) 29.30 vs 28.67 us, Q at T = 64 2.20 vs 2.11 us, K at T = 64 2.22
+    // vs 2.10 us; Mistral-7B's K at T = 4096 (8 MiB) 4.54 vs 4.85 us,
+    // Mistral-Nemo's K (4 MiB) 2.63 vs 2.98 us, Q and K in one launch at
     // T = 4096 14.47 vs 14.85 us, Q at T = 2048 6.63 vs 6.72 us.
     const bool small = rotate && !qknorm && bytes <= (8ll << 20);
-    const int wpb = (tokens >= 8192 && hpl == 1) || (small && hpl == 1) ? 1 : kRopeThreads / kWave;
+    const int wpb = hpl == 1 && (tokens >= 8192 || (small && bytes <= (1ll << 20))) ? 1 : kRopeThreads / kWave;
     const unsigned blocks = static_cast<unsigned>((waves + wpb - 1) / wpb);
     auto go = [&](auto kern) { kern<<<dim3(blocks), dim3(wpb * kWave), 0, stream()>>>(w); };
 #define NG_ROPE_WAVE(HPL)                                                                   \

@@ -98,6 +98,30 @@ def assert_within_bound(got_bits, a, q, scale, tb: bool, what: str, ora) -> None
                           f"max |d|/bound {(d / bound).max():.3g}"
 
 
+def assert_fused_tight(got_bits, a, q, scale, what: str) -> None:
+    """The fused int8 kernels' own semantics, fp16(RN32(S32) * scale[n]) with
+    S32 the fp32 sum of a_k * q_k (each product exact in fp32) in the matrix
+    cores' order, against the exact S (float64, whose own error is below
+    K 2^-53 of sum |a q|). Bound: the fp32 accumulation, at most (K / 8 + 64)
+    rounded additions on any path (MFMA k-groups, K slices, the in-order slice
+    reduction), each within 2^-24 of the partial sum magnitude, so
+    (K / 8 + 64) 2^-24 sum_k |a_k q_k| scale[n]; the fp32 product with the
+    scale (2^-24 relative) and the fp16 rounding of the result (half an fp16
+    ulp, taken as one). At K = 4096 that is about 3e-5 of sum |a w|, 70 times
+    tighter than the bound to the reference's composition, whose fp16
+    rounding of q * s it need not cover."""
+    x = f16val(a)
+    qq = q.astype(np.float64)
+    K = qq.shape[1]
+    ref = (x @ qq.T) * scale[None, :].astype(np.float64)
+    mag = (np.abs(x) @ np.abs(qq).T) * scale[None, :].astype(np.float64)
+    d = np.abs(f16val(got_bits) - ref)
+    bound = ulp16(ref) + (K / 8 + 64) * 2.0 ** -24 * mag + 2.0 ** -24 * np.abs(ref)
+    bad = d > bound
+    assert not bad.any(), f"{what}: {bad.sum()} outside the fused-semantics bound; max |d| {d.max():.3g}, " \
+                          f"max |d|/bound {(d / bound).max():.3g}"
+
+
 # M, K, N: the weight-streaming path takes transpose_b, M <= 128 and K % 64 == 0
 # (K % 16 == 0 for M <= 4). M <= 4 runs the GEMV kernel (K in 1024-code
 # segments, the last one possibly partial); M > 16, and 4 < M <= 16 with K or
@@ -144,6 +168,7 @@ def test_int8_weight_streaming_random(lib, ora, M, K, N):
     scale = RNG.uniform(1e-3, 1e-2, N).astype(np.float32)
     got = gemm_int8(lib, a, q, scale, M, K, N, True)
     assert_within_bound(got, a, q, scale, True, "C", ora)
+    assert_fused_tight(got, a, q, scale, "C")
 
 
 INF_SHAPES = [(1, 1040, 100), (2, 14352, 64), (4, 2064, 33), (8, 4160, 512), (12, 1088, 4096), (64, 4096, 4096),
@@ -205,9 +230,12 @@ def test_int8_prefill_random(lib, ora, M, K, N):
     scale = RNG.uniform(1e-3, 1e-2, N).astype(np.float32)
     got = gemm_int8(lib, a, q, scale, M, K, N, True)
     assert_within_bound(got, a, q, scale, True, "C", ora)
-    if M >= LT_MIN_M:
+    if M < LT_MIN_M:
+        assert_fused_tight(got, a, q, scale, "C")
+    else:
         fused = gemm_int8_fused(lib, a, q, scale, M, K, N)
         assert_within_bound(fused, a, q, scale, True, "C (fused kernel)", ora)
+        assert_fused_tight(fused, a, q, scale, "C (fused kernel)")
 
 
 # From LT_MIN_M rows on, cuda_gemm_int8 (transpose_b) dequantizes B to fp16 and
