@@ -257,6 +257,24 @@ def test_int8_prefill_library_rows_bit_exact(lib, M, K, N):
     assert_bits_equal(got, S.astype(np.float16).view(np.uint16), "C")
 
 
+@pytest.mark.parametrize("M,K,N", [(4096, 4096, 4096), (4096, 4096, 1024)])
+def test_int8_prefill_library_rows_is_the_composition(lib, ora, M, K, N):
+    """From LT_MIN_M rows on, cuda_gemm_int8 on random inputs gives the bits of
+    the reference's two calls made separately: cuda_dequantize_weights into
+    an fp16 buffer, then cuda_gemm_fp16 (matmul.cu:205-236), which use the
+    same hipBLASLt algorithm for the shape."""
+    banner(f"gemm_int8 = dequantize + gemm_fp16, random M={M} K={K} N={N}")
+    a = f16bits(RNG.standard_normal((M, K)))
+    q = codes((N, K))
+    scale = RNG.uniform(1e-3, 1e-2, N).astype(np.float32)
+    got = gemm_int8(lib, a, q, scale, M, K, N, True)
+    wb, qb, sb = empty(2 * N * K), dev(q), dev(scale)
+    ok(lib.cuda_dequantize_weights(wb.vp, qb.vp, sb.vp, N, K, 1), "cuda_dequantize_weights")
+    want = gemm_fp16(lib, a, get(wb, np.uint16, (N, K)), M, K, N, False, True)
+    assert_bits_equal(got, want, "C")
+    assert_within_bound(got, a, q, scale, True, "C", ora)
+
+
 @pytest.mark.parametrize("M,K,N", [(256, 4160, 512), (129, 1040, 300), (1024, 4096, 1024), (777, 1024, 16000)])
 def test_int8_prefill_inf_activations(lib, M, K, N):
     test_int8_weight_streaming_inf_activations(lib, M, K, N)
