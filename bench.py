@@ -669,6 +669,12 @@ def extra_kernels(L, hip, stream):
     for x in (wq, wk, pos):
         x.free()
     out["gemm_int8"] = gemm_extras(L, hip, stream)
+    out["gemm_int8_shared_a"] = sh = shared_a_extras(L, hip, stream)
+    g = out["gemm_int8"]
+    g["mistral7b_layer_M1"]["shared_a_us"] = (sh["qkv_M1"]["us"] + g["q_proj_M1"]["us"] + sh["gate_up_M1"]["us"]
+                                              + g["down_proj_M1"]["us"])
+    g["mistral7b_layer_M1"]["shared_a_note"] = ("q/k/v in one ng_gemm_int8_shared_a call, o, gate/up in one call, "
+                                                "down")
     return out
 
 
@@ -760,6 +766,56 @@ def gemm_extras(L, hip, stream):
                                         "note": "q, k, v, o, gate, up, down projections of one layer"}
         if f:
             out[f"mistral7b_layer_M{M}"]["fused_us"] = f[0]
+    return out
+
+
+def shared_a_extras(L, hip, stream):
+    """ng_gemm_int8_shared_a against separate cuda_gemm_int8 calls for the
+    projections of one Mistral-7B INT8 layer that read the same normed rows:
+    q/k/v (layer.cu:487-501) and gate/up (layer.cu:575-583), at M = 1 and 2
+    decode tokens. Both forms give the same bits; weight pools keep the codes
+    cache-cold."""
+    rng = np.random.Generator(np.random.PCG64(5))
+    K = 4096
+    sets = {"qkv": [4096, 1024, 1024], "gate_up": [14336, 14336]}
+    out = {}
+    for name, ns in sets.items():
+        n = pool_slots(sum(ns) * K)
+        pools = []
+        for N in ns:
+            wq = rng.integers(-128, 128, (N, K)).astype(np.int8)
+            pools.append((N, Pool(hip, wq.nbytes, n, wq), DB.from_array(rng.uniform(1e-3, 1e-2, N).astype(np.float32))))
+            del wq
+        cnt = len(ns)
+        for M in (1, 2):
+            ab = DB.from_array(W.round_to(rng.standard_normal((M, K), dtype=np.float32), "f16"))
+            cps = [Pool(hip, 2 * M * N, n) for N in ns]
+
+            def sep(j, M=M, ab=ab, cps=cps):
+                for (N, wp, sc), cp in zip(pools, cps):
+                    rc = L.cuda_gemm_int8(cp.at(j), ab.vp, wp.at(j), sc.vp, M, K, N, True)
+                    if rc:
+                        return rc
+                return 0
+
+            args = [((C.c_void_p * cnt)(*[cp.at(j) for cp in cps]), (C.c_void_p * cnt)(*[wp.at(j) for _, wp, _ in pools]))
+                    for j in range(n)]
+            scv = (C.c_void_p * cnt)(*[sc.ptr for _, _, sc in pools])
+            nv = (C.c_int * cnt)(*ns)
+            us_sep = time_pool_kernel(hip, stream, [("separate", (lambda j=j: sep(j))) for j in range(n)])
+            us_sh = time_pool_kernel(hip, stream, [("shared", (lambda j=j, M=M, ab=ab: L.ng_gemm_int8_shared_a(
+                cnt, args[j][0], ab.vp, args[j][1], scv, nv, M, K))) for j in range(n)])
+            b = sum(N * K + 2 * M * N + 4 * N for N in ns) + 2 * M * K
+            out[f"{name}_M{M}"] = {"us": us_sh, "separate_us": us_sep, "GBps": b / us_sh / 1e3,
+                                   "frac": b / us_sh / 1e3 / PEAK_GBPS, "bytes": b, "buffer_sets": n}
+            for cp in cps:
+                cp.free()
+            ab.free()
+        for _, wp, sc in pools:
+            wp.free()
+            sc.free()
+    out["note"] = ("us: one ng_gemm_int8_shared_a call (one GEMV launch for the set); separate_us: one "
+                   "cuda_gemm_int8 call per projection")
     return out
 
 
@@ -1335,7 +1391,8 @@ def main():
         profile_pass(L, hip, stream)
         return
     if args.gemm_only:
-        print(json.dumps({"gemm_int8": gemm_extras(L, hip, stream)}), flush=True)
+        print(json.dumps({"gemm_int8": gemm_extras(L, hip, stream),
+                          "gemm_int8_shared_a": shared_a_extras(L, hip, stream)}), flush=True)
         return
     if args.floors_only:
         print(json.dumps({"floors": floor_extras(hip, stream)}), flush=True)

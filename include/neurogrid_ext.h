@@ -123,6 +123,20 @@ int ng_gather_embeddings_checked(void* output, const void* embed_table, const in
 int ng_gemm_int8_noalloc(void* c, const void* a, const void* b, const void* scale, int M, int K, int N,
                          bool transpose_b);
 
+/* count (1..4) products that share one A: for i < count,
+ *   c[i] = cuda_gemm_int8(c[i], a, b[i], scales[i], M, K, n[i], true)
+ * bit for bit (B_i int8 [n[i], K], per-row scales, C_i fp16 [M, n[i]]). The
+ * engine's INT8 layer calls cuda_gemm_int8 three times on the same normed rows
+ * for q/k/v (gpu/engine/layer.cu:487-501) and twice for gate/up (:575-583).
+ * When every product takes cuda_gemm_int8's GEMV kernel (M <= 4, K % 16 == 0,
+ * 16-byte aligned A and B; M = 3, 4 also need K and N below 8192), they run
+ * in one launch; otherwise this is one cuda_gemm_int8 call per product. The
+ * arrays c, b, scales and n are host arrays. C_i must not overlap A or each
+ * other. Returns 0, or -1 (null pointers, count outside 1..4, sizes <= 0, or
+ * a failing cuda_gemm_int8). */
+int ng_gemm_int8_shared_a(int count, void* const* c, const void* a, const void* const* b,
+                          const void* const* scales, const int* n, int M, int K);
+
 #ifdef __cplusplus
 }
 #endif

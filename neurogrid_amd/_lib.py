@@ -92,6 +92,7 @@ SIGNATURES: dict[str, tuple] = {
     "cuda_gemm_fp16": (_i, [_vp, _cvp, _cvp, _i, _i, _i, C.c_bool, C.c_bool]),
     "cuda_gemm_int8": (_i, [_vp, _cvp, _cvp, _cvp, _i, _i, _i, C.c_bool]),
     "ng_gemm_int8_noalloc": (_i, [_vp, _cvp, _cvp, _cvp, _i, _i, _i, C.c_bool]),
+    "ng_gemm_int8_shared_a": (_i, [_i, C.POINTER(_vp), _cvp, C.POINTER(_cvp), C.POINTER(_cvp), _ip, _i, _i]),
 }
 
 _LIB = None

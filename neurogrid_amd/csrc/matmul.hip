@@ -49,6 +49,7 @@
 #include <hipblaslt/hipblaslt.h>
 
 #include <atomic>
+#include <climits>
 #include <map>
 #include <mutex>
 #include <set>
@@ -236,12 +237,11 @@ int launch_i8w(uint16_t* c, const uint16_t* a, const int8_t* b, const float* sca
 constexpr int kGvWaves = 4;
 constexpr int kGvSeg = 1024;  // codes per wave step: 64 lanes x 16
 
+// One block of the GEMV kernels: rows blk R .. blk R + R - 1 of B.
 template <int MR, int R>
-__global__ __launch_bounds__(kGvWaves * kWave) void gemv_i8w_kernel(uint16_t* __restrict__ c,
-                                                                    const uint16_t* __restrict__ a,
-                                                                    const int8_t* __restrict__ b,
-                                                                    const float* __restrict__ scale, int M, int N,
-                                                                    int K) {
+__device__ __forceinline__ void gemv_i8w_block(uint16_t* __restrict__ c, const uint16_t* __restrict__ a,
+                                               const int8_t* __restrict__ b, const float* __restrict__ scale,
+                                               int M, int N, int K, int blk) {
     constexpr int V = R * MR;                 // outputs per block
     constexpr int kParts = kGvWaves * kWave / V;  // threads that share one output in the first reduction stage
     static_assert(kGvWaves * kWave % V == 0 && kWave % kParts == 0, "reduction shape");
@@ -249,7 +249,7 @@ __global__ __launch_bounds__(kGvWaves * kWave) void gemv_i8w_kernel(uint16_t* __
     const int tid = threadIdx.x;
     const int lane = tid & (kWave - 1);
     const int wave = __builtin_amdgcn_readfirstlane(tid / kWave);
-    const int n0 = blockIdx.x * R;
+    const int n0 = blk * R;
     const int nseg = (K + kGvSeg - 1) / kGvSeg;
 
     float acc[R][MR];
@@ -324,6 +324,49 @@ __global__ __launch_bounds__(kGvWaves * kWave) void gemv_i8w_kernel(uint16_t* __
         const int r = tid / MR, m = tid % MR, n = n0 + r;
         if (m < M && n < N) c[static_cast<size_t>(m) * N + n] = from_f32<f16>(v * scale[n]);
     }
+}
+
+template <int MR, int R>
+__global__ __launch_bounds__(kGvWaves * kWave) void gemv_i8w_kernel(uint16_t* __restrict__ c,
+                                                                    const uint16_t* __restrict__ a,
+                                                                    const int8_t* __restrict__ b,
+                                                                    const float* __restrict__ scale, int M, int N,
+                                                                    int K) {
+    gemv_i8w_block<MR, R>(c, a, b, scale, M, N, K, blockIdx.x);
+}
+
+// Several products that share A in one launch (ng_gemm_int8_shared_a):
+// blocks first[p] .. first[p + 1] - 1 run product p exactly as
+// gemv_i8w_kernel's blocks 0 .. would, so each C is bit-identical to its own
+// launch. The product's pointers are picked with selects, not by indexing
+// the argument arrays (which would copy them to scratch memory).
+constexpr int kMaxShared = 4;
+struct GemvSet {
+    uint16_t* c[kMaxShared];
+    const int8_t* b[kMaxShared];
+    const float* scale[kMaxShared];
+    int n[kMaxShared];
+    int first[kMaxShared];  // first block of each product, increasing
+};
+
+template <int MR, int R>
+__global__ __launch_bounds__(kGvWaves * kWave) void gemv_i8w_shared_kernel(GemvSet s, const uint16_t* __restrict__ a,
+                                                                           int M, int K) {
+    const int blk = blockIdx.x;
+    const int p = (blk >= s.first[1]) + (blk >= s.first[2]) + (blk >= s.first[3]);
+    auto pick = [p](auto v0, auto v1, auto v2, auto v3) { return p == 0 ? v0 : p == 1 ? v1 : p == 2 ? v2 : v3; };
+    gemv_i8w_block<MR, R>(pick(s.c[0], s.c[1], s.c[2], s.c[3]), a, pick(s.b[0], s.b[1], s.b[2], s.b[3]),
+                          pick(s.scale[0], s.scale[1], s.scale[2], s.scale[3]), M,
+                          pick(s.n[0], s.n[1], s.n[2], s.n[3]), K,
+                          blk - pick(s.first[0], s.first[1], s.first[2], s.first[3]));
+}
+
+template <int MR, int R>
+int launch_gemv_shared(const GemvSet& set, int blocks, const uint16_t* a, int M, int K) {
+    gemv_i8w_shared_kernel<MR, R><<<dim3(static_cast<unsigned>(blocks)), dim3(kGvWaves * kWave), 0, stream()>>>(
+        set, a, M, K);
+    NG_CHECK_LAUNCH("ng_gemm_int8_shared_a");
+    return 0;
 }
 
 template <int MR, int R>
@@ -1089,6 +1132,17 @@ int launch_split(uint16_t* c, const uint16_t* a, const int8_t* b, const float* s
     return S > 1 ? launch_reduce(s, c, part, scale, M, N, S) : 0;
 }
 
+// The GEMV kernel gemm_i8w runs for a product on the weight-streaming path:
+// 1 (one row of A, 8 rows of B per block), 2 (two rows of A, 8 of B), 3 (up
+// to four rows of A, 4 of B), or 0 for the MFMA kernels. The GEMV kernel
+// takes M <= 4 and K % 16 == 0, except M = 3, 4 with K or N of 8192 or more
+// and K % 64 == 0, where the split kernel is faster.
+int gemv_shape(int M, int K, int N) {
+    const bool big = K >= 8192 || N >= 8192;
+    if (M > 4 || K % 16 != 0 || (M >= 3 && big && K % kChunk == 0)) return 0;
+    return M == 1 ? 1 : M == 2 ? 2 : 3;
+}
+
 // Kernel and tile shape by M, K and N, from sweeps on MI355X over K x N in
 // {4096 x 4096, 4096 x 1024, 4096 x 14336, 14336 x 4096} and M from 1 to 128:
 // the GEMV kernel up to M = 4 (8 rows of B per block for M <= 2, 4 for M = 3,
@@ -1104,10 +1158,11 @@ int gemm_i8w(void* c, const void* a, const void* b, const void* scale, int M, in
     auto* bp = static_cast<const int8_t*>(b);
     auto* sp = static_cast<const float*>(scale);
     const bool big = K >= 8192 || N >= 8192;
-    if (M <= 4 && K % 16 == 0 && !(M >= 3 && big && K % kChunk == 0)) {
-        if (M == 1) return launch_gemv<1, 8>(cp, ap, bp, sp, M, N, K);
-        if (M == 2) return launch_gemv<2, 8>(cp, ap, bp, sp, M, N, K);
-        return launch_gemv<4, 4>(cp, ap, bp, sp, M, N, K);
+    switch (gemv_shape(M, K, N)) {
+        case 1: return launch_gemv<1, 8>(cp, ap, bp, sp, M, N, K);
+        case 2: return launch_gemv<2, 8>(cp, ap, bp, sp, M, N, K);
+        case 3: return launch_gemv<4, 4>(cp, ap, bp, sp, M, N, K);
+        default: break;
     }
     // K >= 8192 (down): 8 waves per block. N >= 12288 at smaller K (gate/up):
     // 192 or more tiles of 64 rows fill the GPU with one slice of K, split
@@ -1290,4 +1345,49 @@ extern "C" int ng_gemm_int8_noalloc(void* c, const void* a, const void* b, const
     if (scratch_ptr(dev, &part) != 0) return -1;
     if (stream_path) return gemm_i8w(c, a, b, scale, M, K, N, part, kNoAllocScratchBytes);
     return gemm_prefill(c, a, b, scale, M, K, N, part, kNoAllocScratchBytes);
+}
+
+// Products that share A (the engine's q/k/v and gate/up projections): when
+// every one takes the GEMV kernel with the same shape, one launch of
+// gemv_i8w_shared_kernel runs them all, each product's blocks exactly as its
+// own launch would; otherwise one cuda_gemm_int8 call each. Either way the
+// results are cuda_gemm_int8's, bit for bit.
+extern "C" int ng_gemm_int8_shared_a(int count, void* const* c, const void* a, const void* const* b,
+                                     const void* const* scales, const int* n, int M, int K) {
+    NG_REQUIRE(c && a && b && scales && n, "ng_gemm_int8_shared_a: null pointer");
+    NG_REQUIRE(count >= 1 && count <= kMaxShared, "ng_gemm_int8_shared_a: count=%d must be in [1, %d]", count,
+               kMaxShared);
+    NG_REQUIRE(M > 0 && K > 0, "ng_gemm_int8_shared_a: M=%d K=%d must be > 0", M, K);
+    int shape = -1;
+    for (int i = 0; i < count; ++i) {
+        NG_REQUIRE(c[i] && b[i] && scales[i], "ng_gemm_int8_shared_a: null pointer in product %d", i);
+        NG_REQUIRE(n[i] > 0, "ng_gemm_int8_shared_a: n[%d]=%d must be > 0", i, n[i]);
+        const int gv = use_i8w(a, b[i], M, K, n[i], true) ? gemv_shape(M, K, n[i]) : 0;
+        shape = (shape == -1 || shape == gv) ? gv : 0;
+    }
+    if (shape <= 0 || count == 1) {
+        for (int i = 0; i < count; ++i) {
+            const int r = cuda_gemm_int8(c[i], a, b[i], scales[i], M, K, n[i], true);
+            if (r != 0) return r;
+        }
+        return 0;
+    }
+    const int R = shape == 3 ? 4 : 8;
+    GemvSet set{};
+    long long blocks = 0;
+    for (int i = 0; i < kMaxShared; ++i) {
+        const int j = i < count ? i : 0;  // unused slots repeat product 0 and are never selected
+        set.c[i] = static_cast<uint16_t*>(c[j]);
+        set.b[i] = static_cast<const int8_t*>(b[j]);
+        set.scale[i] = static_cast<const float*>(scales[j]);
+        set.n[i] = n[j];
+        set.first[i] = i < count ? static_cast<int>(blocks) : INT_MAX;
+        if (i < count) blocks += (n[i] + R - 1) / R;
+        NG_REQUIRE(blocks < (1ll << 31), "ng_gemm_int8_shared_a: too many rows of B");
+    }
+    const auto* ap = static_cast<const uint16_t*>(a);
+    const int nb = static_cast<int>(blocks);
+    if (shape == 1) return launch_gemv_shared<1, 8>(set, nb, ap, M, K);
+    if (shape == 2) return launch_gemv_shared<2, 8>(set, nb, ap, M, K);
+    return launch_gemv_shared<4, 4>(set, nb, ap, M, K);
 }

@@ -98,6 +98,14 @@ def test_argument_errors_return_minus_one_without_touching_the_gpu(capfd):
     assert L.ng_gemm_int8_noalloc(p, p, None, p, 4, 64, 16, True) == -1
     assert L.ng_gemm_int8_noalloc(p, p, p, p, 129, 72, 16, True) == -1     # K % 16 != 0: hipBLASLt path
     assert L.ng_gemm_int8_noalloc(p, p, p, p, 4, 64, 16, False) == -1
+    pv = (C.c_void_p * 2)(256, 512)
+    pn = (C.c_void_p * 2)(256, None)
+    nv = (C.c_int * 2)(16, 0)
+    assert L.ng_gemm_int8_shared_a(0, pv, p, pv, pv, nv, 1, 64) == -1    # count outside 1..4
+    assert L.ng_gemm_int8_shared_a(5, pv, p, pv, pv, nv, 1, 64) == -1
+    assert L.ng_gemm_int8_shared_a(2, pv, p, pn, pv, nv, 1, 64) == -1    # null weights of product 1
+    assert L.ng_gemm_int8_shared_a(2, pv, p, pv, pv, nv, 1, 64) == -1    # n[1] == 0
+    assert L.ng_gemm_int8_shared_a(1, None, p, pv, pv, nv, 1, 64) == -1
     err = capfd.readouterr().err
     assert "neurogrid-amd:" in err and "null pointer" in err
 

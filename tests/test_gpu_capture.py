@@ -177,6 +177,11 @@ def _ops():
         lambda L, i, o: L.ng_gemm_int8_noalloc(o["y"].vp, i["a64"].vp, i["wq"].vp, i["wsc"].vp, 64, GK, GN, True))
     add("ng_gemm_int8_noalloc_M200_prefill", {"y": (E2, (200, GN))},
         lambda L, i, o: L.ng_gemm_int8_noalloc(o["y"].vp, i["a200"].vp, i["wq"].vp, i["wsc"].vp, 200, GK, GN, True))
+    # two products that share A in one GEMV launch
+    add("ng_gemm_int8_shared_a_M1", {"y": (E2, (1, GN)), "y2": (E2, (1, GNW))},
+        lambda L, i, o: L.ng_gemm_int8_shared_a(
+            2, (C.c_void_p * 2)(o["y"].ptr, o["y2"].ptr), i["a1"].vp, (C.c_void_p * 2)(i["wq"].ptr, i["wq_wide"].ptr),
+            (C.c_void_p * 2)(i["wsc"].ptr, i["wsc_wide"].ptr), (C.c_int * 2)(GN, GNW), 1, GK))
     # from 4096 rows of A on: B dequantized into the stream's fp16 buffer, then hipBLASLt
     add("cuda_gemm_int8_M4096_library", {"y": (E2, (4096, GN))},
         lambda L, i, o: L.cuda_gemm_int8(o["y"].vp, i["a4096"].vp, i["wq"].vp, i["wsc"].vp, 4096, GK, GN, True),

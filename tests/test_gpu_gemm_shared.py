@@ -1,0 +1,125 @@
+"""ng_gemm_int8_shared_a on the GPU: int8-weight products that share one A.
+
+Bars:
+  * every C_i is bit-identical to its own cuda_gemm_int8(c_i, a, b_i, scale_i,
+    M, K, n_i, true) on the same inputs (random activations, random codes and
+    scales), whether the products ran in one launch (every product on the GEMV
+    kernel with the same shape) or as one call each;
+  * exact inputs (activations on a grid 2^-e, so that every partial sum of
+    A @ q is exact in fp32) give fp16(fp32(sum_k a_k q_k) * scale[n]) bit for
+    bit, the weight-streaming paths' formula, checked against numpy;
+  * a second call with other inputs and fewer products leaves nothing behind.
+"""
+from __future__ import annotations
+
+import math
+
+import numpy as np
+import pytest
+
+from gpu_util import C, assert_bits_equal, banner, dev, empty, get, ok
+
+pytestmark = pytest.mark.gpu
+
+RNG = np.random.Generator(np.random.PCG64(47))
+
+# (M, K, [n_i]): q/k/v and gate/up at Mistral-7B and Llama-2-13B sizes, ragged
+# rows of B and K (K % 1024 != 0), four products, one product, tiny K; and
+# sets that cannot share a launch: M = 3, 4 with N >= 8192 (split kernel), a
+# mix of a GEMV product and a split-kernel one, and M = 64.
+SETS = [
+    (1, 4096, [4096, 1024, 1024]),
+    (2, 4096, [4096, 1024, 1024]),
+    (3, 4096, [4096, 1024, 1024]),
+    (4, 4096, [4096, 1024, 1024]),
+    (1, 4096, [14336, 14336]),
+    (2, 4096, [14336, 14336]),
+    (1, 14336, [4096]),
+    (1, 5120, [5120, 5120, 5120]),
+    (2, 4112, [1000, 333, 7, 64]),
+    (3, 2064, [17, 1, 40]),
+    (1, 16, [5, 9]),
+    (4, 4096, [14336, 14336]),
+    (3, 4096, [4096, 12300]),
+    (64, 4096, [4096, 1024, 1024]),
+]
+
+
+def f16bits(x) -> np.ndarray:
+    return np.asarray(x, np.float32).astype(np.float16).view(np.uint16)
+
+
+def f16val(bits) -> np.ndarray:
+    return np.asarray(bits, np.uint16).view(np.float16).astype(np.float64)
+
+
+def exact_activations(M: int, K: int) -> np.ndarray:
+    """j * 2^-e in [-1, 1] with K * 128 * 2^e <= 2^23 (every partial sum exact)."""
+    e = min(6, 16 - math.ceil(math.log2(K)))
+    return f16bits(RNG.integers(-(2 ** e), 2 ** e + 1, size=(M, K)) * 2.0 ** -e)
+
+
+def problem(M: int, K: int, ns, exact: bool):
+    a = exact_activations(M, K) if exact else f16bits(RNG.standard_normal((M, K)))
+    qs = [RNG.integers(-128, 128, size=(n, K)).astype(np.int8) for n in ns]
+    scales = [RNG.uniform(1e-3, 1e-2, n).astype(np.float16).astype(np.float32) for n in ns]
+    return a, qs, scales
+
+
+def shared(lib, a, qs, scales, M, K):
+    ab = dev(a)
+    qb = [dev(q) for q in qs]
+    sb = [dev(s) for s in scales]
+    cb = [empty(M * q.shape[0] * 2) for q in qs]
+    cnt = len(qs)
+    rc = lib.ng_gemm_int8_shared_a(cnt, (C.c_void_p * cnt)(*[c.ptr for c in cb]), ab.vp,
+                                   (C.c_void_p * cnt)(*[b.ptr for b in qb]),
+                                   (C.c_void_p * cnt)(*[s.ptr for s in sb]),
+                                   (C.c_int * cnt)(*[q.shape[0] for q in qs]), M, K)
+    ok(rc, "ng_gemm_int8_shared_a")
+    return [get(c, np.uint16, (M, q.shape[0])) for c, q in zip(cb, qs)]
+
+
+def separate(lib, a, qs, scales, M, K):
+    ab = dev(a)
+    out = []
+    for q, s in zip(qs, scales):
+        qb, sb = dev(q), dev(s)
+        cb = empty(M * q.shape[0] * 2)
+        ok(lib.cuda_gemm_int8(cb.vp, ab.vp, qb.vp, sb.vp, M, K, q.shape[0], True), "cuda_gemm_int8")
+        out.append(get(cb, np.uint16, (M, q.shape[0])))
+    return out
+
+
+@pytest.mark.parametrize("M,K,ns", SETS)
+def test_shared_a_is_cuda_gemm_int8_bit_for_bit(lib, M, K, ns):
+    banner(f"gemm_int8_shared_a random M={M} K={K} n={ns}")
+    a, qs, scales = problem(M, K, ns, exact=False)
+    got = shared(lib, a, qs, scales, M, K)
+    want = separate(lib, a, qs, scales, M, K)
+    for i, (g, w) in enumerate(zip(got, want)):
+        assert_bits_equal(g, w, f"C_{i}")
+
+
+@pytest.mark.parametrize("M,K,ns", [SETS[0], SETS[3], SETS[4], SETS[8], SETS[9], SETS[12]])
+def test_shared_a_exact_inputs(lib, M, K, ns):
+    banner(f"gemm_int8_shared_a exact M={M} K={K} n={ns}")
+    a, qs, scales = problem(M, K, ns, exact=True)
+    got = shared(lib, a, qs, scales, M, K)
+    for i, (g, q, s) in enumerate(zip(got, qs, scales)):
+        S = f16val(a) @ q.astype(np.float64).T
+        want = (S.astype(np.float32) * s[None, :]).astype(np.float16).view(np.uint16)
+        assert_bits_equal(g, want, f"C_{i}")
+
+
+def test_shared_a_consecutive_calls(lib):
+    banner("gemm_int8_shared_a two calls, the second smaller")
+    M, K = 1, 4096
+    a, qs, scales = problem(M, K, [4096, 1024, 1024], exact=False)
+    first = shared(lib, a, qs, scales, M, K)
+    a2, qs2, scales2 = problem(M, K, [2000, 48], exact=False)
+    second = shared(lib, a2, qs2, scales2, M, K)
+    for i, (g, w) in enumerate(zip(first, separate(lib, a, qs, scales, M, K))):
+        assert_bits_equal(g, w, f"first C_{i}")
+    for i, (g, w) in enumerate(zip(second, separate(lib, a2, qs2, scales2, M, K))):
+        assert_bits_equal(g, w, f"second C_{i}")
