@@ -105,12 +105,37 @@ __device__ __forceinline__ void codes16_to_operands(const u32x4 v, f16x8& b0, f1
 // through LDS in wave order. B is read in whole 128-byte lines (8 rows x 128
 // codes per instruction) and reordered into the MFMA layout through a per-wave
 // LDS buffer, as in the split kernel below.
+//
+// Products that share A (ng_gemm_int8_shared_a) run in one launch of the
+// *_shared_kernel forms of this kernel and of the GEMV kernel below: blocks
+// first[p] .. first[p + 1] - 1 run product p exactly as the blocks 0 .. of its
+// own launch would, so each C is bit-identical to its own call. A product's
+// pointers are picked with selects, not by indexing the argument arrays
+// (which would copy them to scratch memory).
+constexpr int kMaxShared = 4;
+struct SharedSet {
+    uint16_t* c[kMaxShared];
+    const int8_t* b[kMaxShared];
+    const float* scale[kMaxShared];
+    int n[kMaxShared];
+    int first[kMaxShared];  // first block of each product, increasing; INT_MAX past the last
+};
+
+// Runs block(c, b, scale, n, block index within the product) for the product that owns this block.
+template <typename F>
+__device__ __forceinline__ void shared_dispatch(const SharedSet& s, F&& block) {
+    const int blk = blockIdx.x;
+    const int p = (blk >= s.first[1]) + (blk >= s.first[2]) + (blk >= s.first[3]);
+    auto pick = [p](auto v0, auto v1, auto v2, auto v3) { return p == 0 ? v0 : p == 1 ? v1 : p == 2 ? v2 : v3; };
+    block(pick(s.c[0], s.c[1], s.c[2], s.c[3]), pick(s.b[0], s.b[1], s.b[2], s.b[3]),
+          pick(s.scale[0], s.scale[1], s.scale[2], s.scale[3]), pick(s.n[0], s.n[1], s.n[2], s.n[3]),
+          blk - pick(s.first[0], s.first[1], s.first[2], s.first[3]));
+}
+
 template <int MT, int NT, int WAVES, int U>
-__global__ __launch_bounds__(WAVES * kWave) void gemm_i8w_kernel(uint16_t* __restrict__ c,
-                                                                  const uint16_t* __restrict__ a,
-                                                                  const int8_t* __restrict__ b,
-                                                                  const float* __restrict__ scale, int M, int N,
-                                                                  int K) {
+__device__ __forceinline__ void gemm_i8w_block(uint16_t* __restrict__ c, const uint16_t* __restrict__ a,
+                                               const int8_t* __restrict__ b, const float* __restrict__ scale,
+                                               int M, int N, int K, int blk) {
     static_assert(NT == 1, "one tile of B per block");
     __shared__ f32x4 partial[WAVES - 1][MT][kWave];
     __shared__ __align__(16) u32x4 lds_b[WAVES][2 * kWave];
@@ -118,7 +143,7 @@ __global__ __launch_bounds__(WAVES * kWave) void gemm_i8w_kernel(uint16_t* __res
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
     const int col = lane & 15;
     const int grp = lane >> 4;
-    const int n0 = blockIdx.x * 16;
+    const int n0 = blk * 16;
     const int nbatch = (K + 127) / 128;
     const bool half_last = (K % 128) != 0;
 
@@ -214,6 +239,23 @@ __global__ __launch_bounds__(WAVES * kWave) void gemm_i8w_kernel(uint16_t* __res
             if (m < M && n < N) c[static_cast<size_t>(m) * N + n] = from_f32<f16>(v[e] * s);
         }
     }
+}
+
+template <int MT, int NT, int WAVES, int U>
+__global__ __launch_bounds__(WAVES * kWave) void gemm_i8w_kernel(uint16_t* __restrict__ c,
+                                                                  const uint16_t* __restrict__ a,
+                                                                  const int8_t* __restrict__ b,
+                                                                  const float* __restrict__ scale, int M, int N,
+                                                                  int K) {
+    gemm_i8w_block<MT, NT, WAVES, U>(c, a, b, scale, M, N, K, blockIdx.x);
+}
+
+template <int MT, int NT, int WAVES, int U>
+__global__ __launch_bounds__(WAVES * kWave) void gemm_i8w_shared_kernel(SharedSet s, const uint16_t* __restrict__ a,
+                                                                         int M, int K) {
+    shared_dispatch(s, [&](uint16_t* c, const int8_t* b, const float* scale, int n, int blk) {
+        gemm_i8w_block<MT, NT, WAVES, U>(c, a, b, scale, M, n, K, blk);
+    });
 }
 
 template <int MT, int NT, int WAVES, int U>
@@ -335,34 +377,16 @@ __global__ __launch_bounds__(kGvWaves * kWave) void gemv_i8w_kernel(uint16_t* __
     gemv_i8w_block<MR, R>(c, a, b, scale, M, N, K, blockIdx.x);
 }
 
-// Several products that share A in one launch (ng_gemm_int8_shared_a):
-// blocks first[p] .. first[p + 1] - 1 run product p exactly as
-// gemv_i8w_kernel's blocks 0 .. would, so each C is bit-identical to its own
-// launch. The product's pointers are picked with selects, not by indexing
-// the argument arrays (which would copy them to scratch memory).
-constexpr int kMaxShared = 4;
-struct GemvSet {
-    uint16_t* c[kMaxShared];
-    const int8_t* b[kMaxShared];
-    const float* scale[kMaxShared];
-    int n[kMaxShared];
-    int first[kMaxShared];  // first block of each product, increasing
-};
-
 template <int MR, int R>
-__global__ __launch_bounds__(kGvWaves * kWave) void gemv_i8w_shared_kernel(GemvSet s, const uint16_t* __restrict__ a,
+__global__ __launch_bounds__(kGvWaves * kWave) void gemv_i8w_shared_kernel(SharedSet s, const uint16_t* __restrict__ a,
                                                                            int M, int K) {
-    const int blk = blockIdx.x;
-    const int p = (blk >= s.first[1]) + (blk >= s.first[2]) + (blk >= s.first[3]);
-    auto pick = [p](auto v0, auto v1, auto v2, auto v3) { return p == 0 ? v0 : p == 1 ? v1 : p == 2 ? v2 : v3; };
-    gemv_i8w_block<MR, R>(pick(s.c[0], s.c[1], s.c[2], s.c[3]), a, pick(s.b[0], s.b[1], s.b[2], s.b[3]),
-                          pick(s.scale[0], s.scale[1], s.scale[2], s.scale[3]), M,
-                          pick(s.n[0], s.n[1], s.n[2], s.n[3]), K,
-                          blk - pick(s.first[0], s.first[1], s.first[2], s.first[3]));
+    shared_dispatch(s, [&](uint16_t* c, const int8_t* b, const float* scale, int n, int blk) {
+        gemv_i8w_block<MR, R>(c, a, b, scale, M, n, K, blk);
+    });
 }
 
 template <int MR, int R>
-int launch_gemv_shared(const GemvSet& set, int blocks, const uint16_t* a, int M, int K) {
+int launch_gemv_shared(const SharedSet& set, int blocks, const uint16_t* a, int M, int K) {
     gemv_i8w_shared_kernel<MR, R><<<dim3(static_cast<unsigned>(blocks)), dim3(kGvWaves * kWave), 0, stream()>>>(
         set, a, M, K);
     NG_CHECK_LAUNCH("ng_gemm_int8_shared_a");
@@ -1143,6 +1167,16 @@ int gemv_shape(int M, int K, int N) {
     return M == 1 ? 1 : M == 2 ? 2 : 3;
 }
 
+// The kernel gemm_i8w runs for a product on the weight-streaming path, for
+// ng_gemm_int8_shared_a: the GEMV shapes 1-3 above, 4 for the small-M MFMA
+// kernel (4 < M <= 16 with K and N below 8192, gemm_i8w's last case), 0 for
+// the split kernel.
+int shared_path(int M, int K, int N) {
+    const int gv = gemv_shape(M, K, N);
+    if (gv != 0) return gv;
+    return M <= 16 && K < 8192 && N < 8192 ? 4 : 0;
+}
+
 // Kernel and tile shape by M, K and N, from sweeps on MI355X over K x N in
 // {4096 x 4096, 4096 x 1024, 4096 x 14336, 14336 x 4096} and M from 1 to 128:
 // the GEMV kernel up to M = 4 (8 rows of B per block for M <= 2, 4 for M = 3,
@@ -1348,32 +1382,33 @@ extern "C" int ng_gemm_int8_noalloc(void* c, const void* a, const void* b, const
 }
 
 // Products that share A (the engine's q/k/v and gate/up projections): when
-// every one takes the GEMV kernel with the same shape, one launch of
-// gemv_i8w_shared_kernel runs them all, each product's blocks exactly as its
-// own launch would; otherwise one cuda_gemm_int8 call each. Either way the
-// results are cuda_gemm_int8's, bit for bit.
+// every one takes the same kernel of gemm_i8w (the GEMV kernel with one
+// shape, or the small-M MFMA kernel), one launch of that kernel's shared form
+// runs them all, each product's blocks exactly as its own launch would;
+// otherwise one cuda_gemm_int8 call each. Either way the results are
+// cuda_gemm_int8's, bit for bit.
 extern "C" int ng_gemm_int8_shared_a(int count, void* const* c, const void* a, const void* const* b,
                                      const void* const* scales, const int* n, int M, int K) {
     NG_REQUIRE(c && a && b && scales && n, "ng_gemm_int8_shared_a: null pointer");
     NG_REQUIRE(count >= 1 && count <= kMaxShared, "ng_gemm_int8_shared_a: count=%d must be in [1, %d]", count,
                kMaxShared);
     NG_REQUIRE(M > 0 && K > 0, "ng_gemm_int8_shared_a: M=%d K=%d must be > 0", M, K);
-    int shape = -1;
+    int path = -1;
     for (int i = 0; i < count; ++i) {
         NG_REQUIRE(c[i] && b[i] && scales[i], "ng_gemm_int8_shared_a: null pointer in product %d", i);
         NG_REQUIRE(n[i] > 0, "ng_gemm_int8_shared_a: n[%d]=%d must be > 0", i, n[i]);
-        const int gv = use_i8w(a, b[i], M, K, n[i], true) ? gemv_shape(M, K, n[i]) : 0;
-        shape = (shape == -1 || shape == gv) ? gv : 0;
+        const int pi = use_i8w(a, b[i], M, K, n[i], true) ? shared_path(M, K, n[i]) : 0;
+        path = (path == -1 || path == pi) ? pi : 0;
     }
-    if (shape <= 0 || count == 1) {
+    if (path <= 0 || count == 1) {
         for (int i = 0; i < count; ++i) {
             const int r = cuda_gemm_int8(c[i], a, b[i], scales[i], M, K, n[i], true);
             if (r != 0) return r;
         }
         return 0;
     }
-    const int R = shape == 3 ? 4 : 8;
-    GemvSet set{};
+    const int R = path == 3 ? 4 : path == 4 ? 16 : 8;  // rows of B per block
+    SharedSet set{};
     long long blocks = 0;
     for (int i = 0; i < kMaxShared; ++i) {
         const int j = i < count ? i : 0;  // unused slots repeat product 0 and are never selected
@@ -1387,7 +1422,14 @@ extern "C" int ng_gemm_int8_shared_a(int count, void* const* c, const void* a, c
     }
     const auto* ap = static_cast<const uint16_t*>(a);
     const int nb = static_cast<int>(blocks);
-    if (shape == 1) return launch_gemv_shared<1, 8>(set, nb, ap, M, K);
-    if (shape == 2) return launch_gemv_shared<2, 8>(set, nb, ap, M, K);
-    return launch_gemv_shared<4, 4>(set, nb, ap, M, K);
+    switch (path) {
+        case 1: return launch_gemv_shared<1, 8>(set, nb, ap, M, K);
+        case 2: return launch_gemv_shared<2, 8>(set, nb, ap, M, K);
+        case 3: return launch_gemv_shared<4, 4>(set, nb, ap, M, K);
+        default:
+            gemm_i8w_shared_kernel<1, 1, 8, 4><<<dim3(static_cast<unsigned>(nb)), dim3(8 * kWave), 0, stream()>>>(
+                set, ap, M, K);
+            NG_CHECK_LAUNCH("ng_gemm_int8_shared_a");
+            return 0;
+    }
 }

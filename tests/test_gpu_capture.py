@@ -177,7 +177,11 @@ def _ops():
         lambda L, i, o: L.ng_gemm_int8_noalloc(o["y"].vp, i["a64"].vp, i["wq"].vp, i["wsc"].vp, 64, GK, GN, True))
     add("ng_gemm_int8_noalloc_M200_prefill", {"y": (E2, (200, GN))},
         lambda L, i, o: L.ng_gemm_int8_noalloc(o["y"].vp, i["a200"].vp, i["wq"].vp, i["wsc"].vp, 200, GK, GN, True))
-    # two products that share A in one GEMV launch
+    # products that share A in one launch: the GEMV kernel (M = 1), the small-M MFMA kernel (M = 16)
+    add("ng_gemm_int8_shared_a_M16", {"y": (E2, (16, GN)), "y2": (E2, (16, GN))},
+        lambda L, i, o: L.ng_gemm_int8_shared_a(
+            2, (C.c_void_p * 2)(o["y"].ptr, o["y2"].ptr), i["a16"].vp, (C.c_void_p * 2)(i["wq"].ptr, i["wq"].ptr),
+            (C.c_void_p * 2)(i["wsc"].ptr, i["wsc"].ptr), (C.c_int * 2)(GN, GN), 16, GK))
     add("ng_gemm_int8_shared_a_M1", {"y": (E2, (1, GN)), "y2": (E2, (1, GNW))},
         lambda L, i, o: L.ng_gemm_int8_shared_a(
             2, (C.c_void_p * 2)(o["y"].ptr, o["y2"].ptr), i["a1"].vp, (C.c_void_p * 2)(i["wq"].ptr, i["wq_wide"].ptr),

@@ -3,8 +3,9 @@
 Bars:
   * every C_i is bit-identical to its own cuda_gemm_int8(c_i, a, b_i, scale_i,
     M, K, n_i, true) on the same inputs (random activations, random codes and
-    scales), whether the products ran in one launch (every product on the GEMV
-    kernel with the same shape) or as one call each;
+    scales), whether the products ran in one launch (every product on the same
+    kernel: the GEMV kernel with one shape, or the small-M MFMA kernel) or as
+    one call each;
   * exact inputs (activations on a grid 2^-e, so that every partial sum of
     A @ q is exact in fp32) give fp16(fp32(sum_k a_k q_k) * scale[n]) bit for
     bit, the weight-streaming paths' formula, checked against numpy;
@@ -23,10 +24,12 @@ pytestmark = pytest.mark.gpu
 
 RNG = np.random.Generator(np.random.PCG64(47))
 
-# (M, K, [n_i]): q/k/v and gate/up at Mistral-7B and Llama-2-13B sizes, ragged
-# rows of B and K (K % 1024 != 0), four products, one product, tiny K; and
-# sets that cannot share a launch: M = 3, 4 with N >= 8192 (split kernel), a
-# mix of a GEMV product and a split-kernel one, and M = 64.
+# (M, K, [n_i]): q/k/v and gate/up at Mistral-7B and Llama-2-13B sizes on the
+# GEMV kernel (M <= 4), ragged rows of B and K (K % 1024 != 0), four products,
+# one product, tiny K; q/k/v on the small-M MFMA kernel (4 < M <= 16); and sets
+# that cannot share a launch: M = 3, 4 with N >= 8192 (split kernel), a mix of
+# a GEMV product and a split-kernel one, a small-M MFMA product with a split
+# one (M = 12), and M = 64.
 SETS = [
     (1, 4096, [4096, 1024, 1024]),
     (2, 4096, [4096, 1024, 1024]),
@@ -39,7 +42,11 @@ SETS = [
     (2, 4112, [1000, 333, 7, 64]),
     (3, 2064, [17, 1, 40]),
     (1, 16, [5, 9]),
+    (8, 4096, [4096, 1024, 1024]),
+    (16, 4096, [4096, 1024, 1024]),
+    (5, 4160, [1000, 77, 2048]),
     (4, 4096, [14336, 14336]),
+    (12, 4096, [4096, 14336]),
     (3, 4096, [4096, 12300]),
     (64, 4096, [4096, 1024, 1024]),
 ]
@@ -101,7 +108,10 @@ def test_shared_a_is_cuda_gemm_int8_bit_for_bit(lib, M, K, ns):
         assert_bits_equal(g, w, f"C_{i}")
 
 
-@pytest.mark.parametrize("M,K,ns", [SETS[0], SETS[3], SETS[4], SETS[8], SETS[9], SETS[12]])
+@pytest.mark.parametrize("M,K,ns", [(1, 4096, [4096, 1024, 1024]), (4, 4096, [4096, 1024, 1024]),
+                                    (1, 4096, [14336, 14336]), (2, 4112, [1000, 333, 7, 64]),
+                                    (3, 2064, [17, 1, 40]), (8, 4096, [4096, 1024, 1024]),
+                                    (5, 4160, [1000, 77, 2048]), (3, 4096, [4096, 12300])])
 def test_shared_a_exact_inputs(lib, M, K, ns):
     banner(f"gemm_int8_shared_a exact M={M} K={K} n={ns}")
     a, qs, scales = problem(M, K, ns, exact=True)
