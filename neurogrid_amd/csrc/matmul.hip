@@ -121,15 +121,31 @@ struct SharedSet {
     int first[kMaxShared];  // first block of each product, increasing; INT_MAX past the last
 };
 
-// Runs block(c, b, scale, n, block index within the product) for the product that owns this block.
+// Per-product split-K parameters (gemm_i8w_split_shared_kernel): the
+// product's partial-sum region, its slice count, tiles of B and batches per
+// slice.
+struct SplitSet {
+    float* part[kMaxShared];
+    int S[kMaxShared];
+    int tiles[kMaxShared];
+    int cps[kMaxShared];
+};
+
+// Element p of four (a select chain on a wave-uniform p).
+template <typename V>
+__device__ __forceinline__ V pick4(int p, V v0, V v1, V v2, V v3) {
+    return p == 0 ? v0 : p == 1 ? v1 : p == 2 ? v2 : v3;
+}
+
+// Runs block(c, b, scale, n, block index within the product, p) for the
+// product p that owns this block.
 template <typename F>
 __device__ __forceinline__ void shared_dispatch(const SharedSet& s, F&& block) {
     const int blk = blockIdx.x;
     const int p = (blk >= s.first[1]) + (blk >= s.first[2]) + (blk >= s.first[3]);
-    auto pick = [p](auto v0, auto v1, auto v2, auto v3) { return p == 0 ? v0 : p == 1 ? v1 : p == 2 ? v2 : v3; };
-    block(pick(s.c[0], s.c[1], s.c[2], s.c[3]), pick(s.b[0], s.b[1], s.b[2], s.b[3]),
-          pick(s.scale[0], s.scale[1], s.scale[2], s.scale[3]), pick(s.n[0], s.n[1], s.n[2], s.n[3]),
-          blk - pick(s.first[0], s.first[1], s.first[2], s.first[3]));
+    block(pick4(p, s.c[0], s.c[1], s.c[2], s.c[3]), pick4(p, s.b[0], s.b[1], s.b[2], s.b[3]),
+          pick4(p, s.scale[0], s.scale[1], s.scale[2], s.scale[3]), pick4(p, s.n[0], s.n[1], s.n[2], s.n[3]),
+          blk - pick4(p, s.first[0], s.first[1], s.first[2], s.first[3]), p);
 }
 
 template <int MT, int NT, int WAVES, int U>
@@ -253,7 +269,7 @@ __global__ __launch_bounds__(WAVES * kWave) void gemm_i8w_kernel(uint16_t* __res
 template <int MT, int NT, int WAVES, int U>
 __global__ __launch_bounds__(WAVES * kWave) void gemm_i8w_shared_kernel(SharedSet s, const uint16_t* __restrict__ a,
                                                                          int M, int K) {
-    shared_dispatch(s, [&](uint16_t* c, const int8_t* b, const float* scale, int n, int blk) {
+    shared_dispatch(s, [&](uint16_t* c, const int8_t* b, const float* scale, int n, int blk, int) {
         gemm_i8w_block<MT, NT, WAVES, U>(c, a, b, scale, M, n, K, blk);
     });
 }
@@ -380,7 +396,7 @@ __global__ __launch_bounds__(kGvWaves * kWave) void gemv_i8w_kernel(uint16_t* __
 template <int MR, int R>
 __global__ __launch_bounds__(kGvWaves * kWave) void gemv_i8w_shared_kernel(SharedSet s, const uint16_t* __restrict__ a,
                                                                            int M, int K) {
-    shared_dispatch(s, [&](uint16_t* c, const int8_t* b, const float* scale, int n, int blk) {
+    shared_dispatch(s, [&](uint16_t* c, const int8_t* b, const float* scale, int n, int blk, int) {
         gemv_i8w_block<MR, R>(c, a, b, scale, M, n, K, blk);
     });
 }
@@ -436,10 +452,10 @@ int launch_gemv(uint16_t* c, const uint16_t* a, const int8_t* b, const float* sc
 constexpr int kBatch = 128;  // k per batch
 
 template <int MT, int W, int G>
-__global__ __launch_bounds__(G * W * kWave) void gemm_i8w_split_kernel(
+__device__ __forceinline__ void gemm_i8w_split_block(
     uint16_t* __restrict__ c, const uint16_t* __restrict__ a, const int8_t* __restrict__ b,
     const float* __restrict__ scale, float* __restrict__ part, int M, int N, int K, int S, int tiles, int cps,
-    int TT) {
+    int TT, int blk) {
     // A batch of A in LDS. From 4 tiles of A on: 256 bytes per row, 16-byte
     // piece q of row m stored at piece q xor (m mod 16), so the MFMA reads
     // (16 rows, one piece each per lane group) are conflict-free; padded rows
@@ -460,11 +476,11 @@ __global__ __launch_bounds__(G * W * kWave) void gemm_i8w_split_kernel(
     // With TT > 1 token tiles, block b takes rows 16 MT ty .. of A for unit u
     // (a tile and slice), with the TT blocks of a unit on one XCD (ids u + 8 j
     // apart), so that they read its rows of B from one L2.
-    int unit = blockIdx.x, ty = 0;
+    int unit = blk, ty = 0;
     if (TT > 1) {
-        const int i = blockIdx.x / 8;
+        const int i = blk / 8;
         ty = i % TT;
-        unit = (i / TT) * 8 + blockIdx.x % 8;
+        unit = (i / TT) * 8 + blk % 8;
         if (unit >= tiles * S) return;
     }
     const int Mall = M;
@@ -662,6 +678,29 @@ __global__ __launch_bounds__(G * W * kWave) void gemm_i8w_split_kernel(
     }
 }
 
+template <int MT, int W, int G>
+__global__ __launch_bounds__(G * W * kWave) void gemm_i8w_split_kernel(
+    uint16_t* __restrict__ c, const uint16_t* __restrict__ a, const int8_t* __restrict__ b,
+    const float* __restrict__ scale, float* __restrict__ part, int M, int N, int K, int S, int tiles, int cps,
+    int TT) {
+    gemm_i8w_split_block<MT, W, G>(c, a, b, scale, part, M, N, K, S, tiles, cps, TT, blockIdx.x);
+}
+
+// Products that share A on one split-kernel shape (ng_gemm_int8_shared_a):
+// each product keeps its own slices of K and its own region of the
+// partial-sum buffer, so its sums are those of its own launch.
+template <int MT, int W, int G>
+__global__ __launch_bounds__(G * W * kWave) void gemm_i8w_split_shared_kernel(SharedSet s, SplitSet sp,
+                                                                               const uint16_t* __restrict__ a, int M,
+                                                                               int K) {
+    shared_dispatch(s, [&](uint16_t* c, const int8_t* b, const float* scale, int n, int blk, int p) {
+        gemm_i8w_split_block<MT, W, G>(c, a, b, scale, pick4(p, sp.part[0], sp.part[1], sp.part[2], sp.part[3]), M,
+                                       n, K, pick4(p, sp.S[0], sp.S[1], sp.S[2], sp.S[3]),
+                                       pick4(p, sp.tiles[0], sp.tiles[1], sp.tiles[2], sp.tiles[3]),
+                                       pick4(p, sp.cps[0], sp.cps[1], sp.cps[2], sp.cps[3]), 1, blk);
+    });
+}
+
 // C[m, n] = fp16(scale[n] * sum over slices q = 0 .. S-1, in that order, of
 // part[q][m][n]), S <= 8. Four outputs per thread when N % 4 == 0 (16-byte
 // loads of the partial sums and scales, one 8-byte store), else one. Every
@@ -669,10 +708,10 @@ __global__ __launch_bounds__(G * W * kWave) void gemm_i8w_split_kernel(
 // so the loads overlap: 1.3-1.5 us faster than a loop of dependent loads
 // with 8 slices.
 template <bool VEC4>
-__global__ __launch_bounds__(256) void split_reduce_kernel(uint16_t* __restrict__ c, const float* __restrict__ part,
-                                                           const float* __restrict__ scale, int M, int N, int S) {
+__device__ __forceinline__ void split_reduce_block(uint16_t* __restrict__ c, const float* __restrict__ part,
+                                                   const float* __restrict__ scale, int M, int N, int S, int blk) {
     const size_t mn = static_cast<size_t>(M) * N;
-    const size_t t = static_cast<size_t>(blockIdx.x) * 256 + threadIdx.x;
+    const size_t t = static_cast<size_t>(blk) * 256 + threadIdx.x;
     if (VEC4) {
         const size_t i = 4 * t;
         if (i >= mn) return;
@@ -698,6 +737,22 @@ __global__ __launch_bounds__(256) void split_reduce_kernel(uint16_t* __restrict_
             if (q < S) v += pv[q];
         c[t] = from_f32<f16>(v * scale[t % N]);
     }
+}
+
+template <bool VEC4>
+__global__ __launch_bounds__(256) void split_reduce_kernel(uint16_t* __restrict__ c, const float* __restrict__ part,
+                                                           const float* __restrict__ scale, int M, int N, int S) {
+    split_reduce_block<VEC4>(c, part, scale, M, N, S, blockIdx.x);
+}
+
+// The reductions of the products of gemm_i8w_split_shared_kernel in one
+// launch (blocks partitioned by product as in SharedSet).
+template <bool VEC4>
+__global__ __launch_bounds__(256) void split_reduce_shared_kernel(SharedSet s, SplitSet sp, int M) {
+    shared_dispatch(s, [&](uint16_t* c, const int8_t*, const float* scale, int n, int blk, int p) {
+        split_reduce_block<VEC4>(c, pick4(p, sp.part[0], sp.part[1], sp.part[2], sp.part[3]), scale, M, n,
+                                 pick4(p, sp.S[0], sp.S[1], sp.S[2], sp.S[3]), blk);
+    });
 }
 
 
@@ -1128,19 +1183,25 @@ int launch_reduce(hipStream_t s, uint16_t* c, const float* part, const float* sc
     return 0;
 }
 
+// Slices of K for a split launch of `tiles` tiles of B (and TT token tiles):
+// enough for about 256 blocks (512 for K >= 8192; with G groups in the
+// block, 192 blocks of twice the waves), at most 8, each of at least two
+// turns, none empty; cps batches of 128 k per slice.
+void split_slices(int tiles, int TT, int G, int K, int& S, int& cps) {
+    const int nbatch = (K + kBatch - 1) / kBatch;
+    const int target = G > 1 ? 192 : K >= 8192 ? 512 : 256;
+    S = (target + tiles * TT - 1) / (tiles * TT);
+    S = max(1, min(S, min(8, nbatch / (2 * G))));
+    cps = (nbatch + S - 1) / S;
+    S = (nbatch + cps - 1) / cps;
+}
+
 template <int MT, int W, int G>
 int launch_split(uint16_t* c, const uint16_t* a, const int8_t* b, const float* scale, int M, int N, int K,
                  float* scratch, size_t scratch_bytes, int TT = 1) {
     const int tiles = (N + 16 * W - 1) / (16 * W);
-    const int nbatch = (K + kBatch - 1) / kBatch;
-    // Enough slices of K for about 256 blocks (512 for K >= 8192; with groups
-    // in the block, 192 blocks of twice the waves), at most 8, each of at
-    // least two turns, none empty.
-    const int target = G > 1 ? 192 : K >= 8192 ? 512 : 256;
-    int S = (target + tiles * TT - 1) / (tiles * TT);
-    S = max(1, min(S, min(8, nbatch / (2 * G))));
-    const int cps = (nbatch + S - 1) / S;
-    S = (nbatch + cps - 1) / cps;
+    int S = 0, cps = 0;
+    split_slices(tiles, TT, G, K, S, cps);
     // With S > 1 the partial-sum buffer is this stream's: the lock is held
     // until both kernels are enqueued, so calls from other host threads on the
     // same stream cannot slip a launch between them.
@@ -1167,14 +1228,42 @@ int gemv_shape(int M, int K, int N) {
     return M == 1 ? 1 : M == 2 ? 2 : 3;
 }
 
+// The split kernel's launch shape <MT, W, G> that gemm_i8w takes when the
+// GEMV kernel does not, or kSmallM for the small-M MFMA kernel:
+//   K >= 8192 (down): 8 waves per block;
+//   N >= 12288 at smaller K (gate/up): 192 or more tiles of 64 rows fill the
+//   GPU with one slice of K, split between two groups of 4 waves per block;
+//   few rows of B (k/v: N = 1024 gives 16 tiles) and M > 32: blocks of 32
+//   rows of A each (token tiles sharing B through one XCD's L2) instead of
+//   one block for all of A: 7-16% faster at M = 64-128 (k/v: 9.0 vs 10.5 us
+//   at M = 96); for larger N, and with 16-row token tiles, slower;
+//   M <= 16 with K and N below 8192: the small-M MFMA kernel.
+enum SplitConfig {
+    kSmallM, kSplitTokenTiles, kSplit881, kSplit842, kSplit841, kSplit481, kSplit442, kSplit441, kSplit281,
+    kSplit242, kSplit241, kSplit142, kSplit141
+};
+SplitConfig split_config(int M, int K, int N) {
+    const bool big = K >= 8192 || N >= 8192;
+    const bool deep = K >= 8192;
+    const bool wide = !deep && N >= 12288;
+    if (!deep && N <= 2048 && M > 32) return kSplitTokenTiles;
+    if (M > 64) return deep ? kSplit881 : wide ? kSplit842 : kSplit841;
+    if (M > 32) return deep ? kSplit481 : wide ? kSplit442 : kSplit441;
+    if (M > 16) return deep ? kSplit281 : wide ? kSplit242 : kSplit241;
+    if (big) return wide ? kSplit142 : kSplit141;
+    return kSmallM;
+}
+
 // The kernel gemm_i8w runs for a product on the weight-streaming path, for
 // ng_gemm_int8_shared_a: the GEMV shapes 1-3 above, 4 for the small-M MFMA
-// kernel (4 < M <= 16 with K and N below 8192, gemm_i8w's last case), 0 for
-// the split kernel.
+// kernel, 10 + c for split shape c that ng_gemm_int8_shared_a can share
+// (one tile of A per block), 0 for the rest (token tiles).
 int shared_path(int M, int K, int N) {
     const int gv = gemv_shape(M, K, N);
     if (gv != 0) return gv;
-    return M <= 16 && K < 8192 && N < 8192 ? 4 : 0;
+    const SplitConfig sc = split_config(M, K, N);
+    if (sc == kSmallM) return 4;
+    return sc == kSplitTokenTiles ? 0 : 10 + static_cast<int>(sc);
 }
 
 // Kernel and tile shape by M, K and N, from sweeps on MI355X over K x N in
@@ -1191,40 +1280,27 @@ int gemm_i8w(void* c, const void* a, const void* b, const void* scale, int M, in
     auto* ap = static_cast<const uint16_t*>(a);
     auto* bp = static_cast<const int8_t*>(b);
     auto* sp = static_cast<const float*>(scale);
-    const bool big = K >= 8192 || N >= 8192;
     switch (gemv_shape(M, K, N)) {
         case 1: return launch_gemv<1, 8>(cp, ap, bp, sp, M, N, K);
         case 2: return launch_gemv<2, 8>(cp, ap, bp, sp, M, N, K);
         case 3: return launch_gemv<4, 4>(cp, ap, bp, sp, M, N, K);
         default: break;
     }
-    // K >= 8192 (down): 8 waves per block. N >= 12288 at smaller K (gate/up):
-    // 192 or more tiles of 64 rows fill the GPU with one slice of K, split
-    // between two groups of 4 waves per block.
-    const bool deep = K >= 8192;
-    const bool wide = !deep && N >= 12288;
-    // Few rows of B (k/v: N = 1024 gives 16 tiles): blocks of 32 rows of A
-    // each (token tiles sharing B through one XCD's L2) instead of one block
-    // for all of A: 7-16% faster at M = 64-128 (k/v: 9.0 vs 10.5 us at
-    // M = 96); for larger N, and with 16-row token tiles, slower.
-    if (!deep && N <= 2048 && M > 32)
-        return launch_split<2, 4, 1>(cp, ap, bp, sp, M, N, K, scratch, scratch_bytes, (M + 31) / 32);
-    if (M > 64)
-        return deep ? launch_split<8, 8, 1>(cp, ap, bp, sp, M, N, K, scratch, scratch_bytes)
-               : wide ? launch_split<8, 4, 2>(cp, ap, bp, sp, M, N, K, scratch, scratch_bytes)
-                      : launch_split<8, 4, 1>(cp, ap, bp, sp, M, N, K, scratch, scratch_bytes);
-    if (M > 32)
-        return deep ? launch_split<4, 8, 1>(cp, ap, bp, sp, M, N, K, scratch, scratch_bytes)
-               : wide ? launch_split<4, 4, 2>(cp, ap, bp, sp, M, N, K, scratch, scratch_bytes)
-                      : launch_split<4, 4, 1>(cp, ap, bp, sp, M, N, K, scratch, scratch_bytes);
-    if (M > 16)
-        return deep ? launch_split<2, 8, 1>(cp, ap, bp, sp, M, N, K, scratch, scratch_bytes)
-               : wide ? launch_split<2, 4, 2>(cp, ap, bp, sp, M, N, K, scratch, scratch_bytes)
-                      : launch_split<2, 4, 1>(cp, ap, bp, sp, M, N, K, scratch, scratch_bytes);
-    if (big)
-        return wide ? launch_split<1, 4, 2>(cp, ap, bp, sp, M, N, K, scratch, scratch_bytes)
-                    : launch_split<1, 4, 1>(cp, ap, bp, sp, M, N, K, scratch, scratch_bytes);
-    return launch_i8w<1, 1, 8, 4>(cp, ap, bp, sp, M, N, K);
+    switch (split_config(M, K, N)) {
+        case kSplitTokenTiles: return launch_split<2, 4, 1>(cp, ap, bp, sp, M, N, K, scratch, scratch_bytes, (M + 31) / 32);
+        case kSplit881: return launch_split<8, 8, 1>(cp, ap, bp, sp, M, N, K, scratch, scratch_bytes);
+        case kSplit842: return launch_split<8, 4, 2>(cp, ap, bp, sp, M, N, K, scratch, scratch_bytes);
+        case kSplit841: return launch_split<8, 4, 1>(cp, ap, bp, sp, M, N, K, scratch, scratch_bytes);
+        case kSplit481: return launch_split<4, 8, 1>(cp, ap, bp, sp, M, N, K, scratch, scratch_bytes);
+        case kSplit442: return launch_split<4, 4, 2>(cp, ap, bp, sp, M, N, K, scratch, scratch_bytes);
+        case kSplit441: return launch_split<4, 4, 1>(cp, ap, bp, sp, M, N, K, scratch, scratch_bytes);
+        case kSplit281: return launch_split<2, 8, 1>(cp, ap, bp, sp, M, N, K, scratch, scratch_bytes);
+        case kSplit242: return launch_split<2, 4, 2>(cp, ap, bp, sp, M, N, K, scratch, scratch_bytes);
+        case kSplit241: return launch_split<2, 4, 1>(cp, ap, bp, sp, M, N, K, scratch, scratch_bytes);
+        case kSplit142: return launch_split<1, 4, 2>(cp, ap, bp, sp, M, N, K, scratch, scratch_bytes);
+        case kSplit141: return launch_split<1, 4, 1>(cp, ap, bp, sp, M, N, K, scratch, scratch_bytes);
+        default: return launch_i8w<1, 1, 8, 4>(cp, ap, bp, sp, M, N, K);
+    }
 }
 
 // The prefill kernel takes transpose_b, K % 16 == 0 and 16-byte aligned A and B.
@@ -1381,6 +1457,75 @@ extern "C" int ng_gemm_int8_noalloc(void* c, const void* a, const void* b, const
     return gemm_prefill(c, a, b, scale, M, K, N, part, kNoAllocScratchBytes);
 }
 
+// Products that share A on one split-kernel shape: one launch of the split
+// kernel, and one of the reduction for the products with more than one slice
+// of K, each product with its own slices and its own region of the stream's
+// partial-sum buffer (the lock is held until both kernels are enqueued, as in
+// launch_split).
+template <int MT, int W, int G>
+int launch_split_shared(int count, void* const* c, const uint16_t* a, const void* const* b,
+                        const void* const* scales, const int* n, int M, int K) {
+    int S[kMaxShared] = {}, cps[kMaxShared] = {}, tiles[kMaxShared] = {};
+    long long cols = 0;
+    for (int i = 0; i < count; ++i) {
+        tiles[i] = (n[i] + 16 * W - 1) / (16 * W);
+        split_slices(tiles[i], 1, G, K, S[i], cps[i]);
+        if (S[i] > 1) cols += static_cast<long long>(S[i]) * n[i];
+    }
+    NG_REQUIRE(cols < (1ll << 31), "ng_gemm_int8_shared_a: too many rows of B");
+    const hipStream_t st = stream();
+    float* part = nullptr;
+    std::unique_lock<std::mutex> lock(g_mu, std::defer_lock);
+    if (cols > 0 && partial_buffer(st, 1, M, static_cast<int>(cols), K, nullptr, 0, lock, &part) != 0) return -1;
+    SharedSet set{}, rset{};
+    SplitSet sp{};
+    long long blocks = 0, rblocks = 0, off = 0;
+    bool vec4_all = true, vec4_any = false;
+    for (int i = 0; i < kMaxShared; ++i) {
+        const int j = i < count ? i : 0;  // unused slots repeat product 0 and are never selected
+        set.c[i] = rset.c[i] = static_cast<uint16_t*>(c[j]);
+        set.b[i] = rset.b[i] = static_cast<const int8_t*>(b[j]);
+        set.scale[i] = rset.scale[i] = static_cast<const float*>(scales[j]);
+        set.n[i] = rset.n[i] = n[j];
+        sp.S[i] = S[j];
+        sp.tiles[i] = tiles[j];
+        sp.cps[i] = cps[j];
+        sp.part[i] = nullptr;
+        set.first[i] = i < count ? static_cast<int>(blocks) : INT_MAX;
+        rset.first[i] = i < count ? static_cast<int>(rblocks) : INT_MAX;
+        if (i >= count) continue;
+        blocks += static_cast<long long>(tiles[i]) * S[i];
+        if (S[i] > 1) {
+            sp.part[i] = part + off;
+            off += static_cast<long long>(S[i]) * M * n[i];
+            const bool v4 = n[i] % 4 == 0 && aligned16(scales[i]) && aligned8(c[i]);
+            vec4_all = vec4_all && v4;
+            vec4_any = vec4_any || v4;
+            const long long mn = static_cast<long long>(M) * n[i];
+            rblocks += v4 ? (mn / 4 + 255) / 256 : (mn + 255) / 256;
+        }
+        NG_REQUIRE(blocks < (1ll << 31) && rblocks < (1ll << 31), "ng_gemm_int8_shared_a: too many rows of B");
+    }
+    gemm_i8w_split_shared_kernel<MT, W, G><<<dim3(static_cast<unsigned>(blocks)), dim3(G * W * kWave), 0, st>>>(
+        set, sp, a, M, K);
+    NG_CHECK_LAUNCH("ng_gemm_int8_shared_a");
+    if (rblocks == 0) return 0;
+    if (vec4_all || !vec4_any) {
+        if (vec4_all)
+            split_reduce_shared_kernel<true><<<dim3(static_cast<unsigned>(rblocks)), dim3(256), 0, st>>>(rset, sp, M);
+        else
+            split_reduce_shared_kernel<false><<<dim3(static_cast<unsigned>(rblocks)), dim3(256), 0, st>>>(rset, sp, M);
+        NG_CHECK_LAUNCH("ng_gemm_int8_shared_a");
+        return 0;
+    }
+    // Products whose reductions take different forms: one reduction each.
+    for (int i = 0; i < count; ++i)
+        if (S[i] > 1 && launch_reduce(st, static_cast<uint16_t*>(c[i]), sp.part[i], static_cast<const float*>(scales[i]),
+                                      M, n[i], S[i]) != 0)
+            return -1;
+    return 0;
+}
+
 // Products that share A (the engine's q/k/v and gate/up projections): when
 // every one takes the same kernel of gemm_i8w (the GEMV kernel with one
 // shape, or the small-M MFMA kernel), one launch of that kernel's shared form
@@ -1401,6 +1546,22 @@ extern "C" int ng_gemm_int8_shared_a(int count, void* const* c, const void* a, c
         path = (path == -1 || path == pi) ? pi : 0;
     }
     if (path <= 0 || count == 1) {
+        for (int i = 0; i < count; ++i) {
+            const int r = cuda_gemm_int8(c[i], a, b[i], scales[i], M, K, n[i], true);
+            if (r != 0) return r;
+        }
+        return 0;
+    }
+    const auto* ap0 = static_cast<const uint16_t*>(a);
+    switch (path) {
+        case 10 + kSplit241: return launch_split_shared<2, 4, 1>(count, c, ap0, b, scales, n, M, K);
+        case 10 + kSplit142: return launch_split_shared<1, 4, 2>(count, c, ap0, b, scales, n, M, K);
+        case 10 + kSplit242: return launch_split_shared<2, 4, 2>(count, c, ap0, b, scales, n, M, K);
+        case 10 + kSplit442: return launch_split_shared<4, 4, 2>(count, c, ap0, b, scales, n, M, K);
+        case 10 + kSplit842: return launch_split_shared<8, 4, 2>(count, c, ap0, b, scales, n, M, K);
+        default: break;
+    }
+    if (path >= 10) {  // split shapes no group of the engine's projections shares: one call each
         for (int i = 0; i < count; ++i) {
             const int r = cuda_gemm_int8(c[i], a, b[i], scales[i], M, K, n[i], true);
             if (r != 0) return r;

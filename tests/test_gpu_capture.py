@@ -73,7 +73,7 @@ def inp():
     a["wsc_wide"] = rng.uniform(1e-3, 1e-2, GNW).astype(np.float32)
     a["tsc"] = np.array([0.0125], np.float32)
     a["wh"] = f16_bits(n(GK, GN, s=0.05))
-    for m in (1, 3, 16, 40, 64, 100, 200, 4096):
+    for m in (1, 3, 16, 24, 40, 64, 100, 200, 4096):
         a[f"a{m}"] = f16_bits(n(m, GK))
     bufs = {k: dev(v) for k, v in a.items()}
     yield bufs
@@ -177,7 +177,12 @@ def _ops():
         lambda L, i, o: L.ng_gemm_int8_noalloc(o["y"].vp, i["a64"].vp, i["wq"].vp, i["wsc"].vp, 64, GK, GN, True))
     add("ng_gemm_int8_noalloc_M200_prefill", {"y": (E2, (200, GN))},
         lambda L, i, o: L.ng_gemm_int8_noalloc(o["y"].vp, i["a200"].vp, i["wq"].vp, i["wsc"].vp, 200, GK, GN, True))
-    # products that share A in one launch: the GEMV kernel (M = 1), the small-M MFMA kernel (M = 16)
+    # products that share A in one launch: the split kernel with two K slices and the shared reduction (M = 24)
+    add("ng_gemm_int8_shared_a_M24_split", {"y": (E2, (24, GN)), "y2": (E2, (24, GN))},
+        lambda L, i, o: L.ng_gemm_int8_shared_a(
+            2, (C.c_void_p * 2)(o["y"].ptr, o["y2"].ptr), i["a24"].vp, (C.c_void_p * 2)(i["wq"].ptr, i["wq"].ptr),
+            (C.c_void_p * 2)(i["wsc"].ptr, i["wsc"].ptr), (C.c_int * 2)(GN, GN), 24, GK))
+    # the GEMV kernel (M = 1), the small-M MFMA kernel (M = 16)
     add("ng_gemm_int8_shared_a_M16", {"y": (E2, (16, GN)), "y2": (E2, (16, GN))},
         lambda L, i, o: L.ng_gemm_int8_shared_a(
             2, (C.c_void_p * 2)(o["y"].ptr, o["y2"].ptr), i["a16"].vp, (C.c_void_p * 2)(i["wq"].ptr, i["wq"].ptr),

@@ -26,10 +26,8 @@ RNG = np.random.Generator(np.random.PCG64(47))
 
 # (M, K, [n_i]): q/k/v and gate/up at Mistral-7B and Llama-2-13B sizes on the
 # GEMV kernel (M <= 4), ragged rows of B and K (K % 1024 != 0), four products,
-# one product, tiny K; q/k/v on the small-M MFMA kernel (4 < M <= 16); and sets
-# that cannot share a launch: M = 3, 4 with N >= 8192 (split kernel), a mix of
-# a GEMV product and a split-kernel one, a small-M MFMA product with a split
-# one (M = 12), and M = 64.
+# one product, tiny K; q/k/v on the small-M MFMA kernel (4 < M <= 16); then
+# the split kernel's shared forms and the sets that cannot share a launch.
 SETS = [
     (1, 4096, [4096, 1024, 1024]),
     (2, 4096, [4096, 1024, 1024]),
@@ -45,10 +43,25 @@ SETS = [
     (8, 4096, [4096, 1024, 1024]),
     (16, 4096, [4096, 1024, 1024]),
     (5, 4160, [1000, 77, 2048]),
+    # one split-kernel launch (and one reduction): q/k/v at 17-32 tokens, with
+    # a half last batch of K (K % 128 == 64), and with reductions of two forms;
+    # gate/up from 3 to 128 tokens (one slice of K, two wave groups per block)
+    (17, 4096, [4096, 1024, 1024]),
+    (32, 4096, [4096, 1024, 1024]),
+    (24, 4160, [1000, 77, 2048]),
+    (20, 2048, [1000, 1001]),
     (4, 4096, [14336, 14336]),
+    (3, 4096, [14336, 12300]),
+    (8, 4096, [14336, 14336]),
+    (20, 4096, [14336, 14336]),
+    (64, 4096, [14336, 14336]),
+    (100, 4096, [14336, 14336]),
+    # no shared launch: a small-M MFMA product with a split one, a GEMV product
+    # with a split one, k/v with token tiles beside q (M = 64), down's deep shape
     (12, 4096, [4096, 14336]),
     (3, 4096, [4096, 12300]),
     (64, 4096, [4096, 1024, 1024]),
+    (20, 14336, [4096, 4096]),
 ]
 
 
@@ -111,7 +124,9 @@ def test_shared_a_is_cuda_gemm_int8_bit_for_bit(lib, M, K, ns):
 @pytest.mark.parametrize("M,K,ns", [(1, 4096, [4096, 1024, 1024]), (4, 4096, [4096, 1024, 1024]),
                                     (1, 4096, [14336, 14336]), (2, 4112, [1000, 333, 7, 64]),
                                     (3, 2064, [17, 1, 40]), (8, 4096, [4096, 1024, 1024]),
-                                    (5, 4160, [1000, 77, 2048]), (3, 4096, [4096, 12300])])
+                                    (5, 4160, [1000, 77, 2048]), (3, 4096, [4096, 12300]),
+                                    (24, 4160, [1000, 77, 2048]), (20, 2048, [1000, 1001]),
+                                    (8, 4096, [14336, 14336]), (100, 4096, [14336, 14336])])
 def test_shared_a_exact_inputs(lib, M, K, ns):
     banner(f"gemm_int8_shared_a exact M={M} K={K} n={ns}")
     a, qs, scales = problem(M, K, ns, exact=True)
@@ -120,6 +135,17 @@ def test_shared_a_exact_inputs(lib, M, K, ns):
         S = f16val(a) @ q.astype(np.float64).T
         want = (S.astype(np.float32) * s[None, :]).astype(np.float16).view(np.uint16)
         assert_bits_equal(g, want, f"C_{i}")
+
+
+def test_shared_a_split_consecutive_calls(lib):
+    banner("gemm_int8_shared_a split kernel: a call, then a smaller one, then a larger one")
+    K = 4096
+    sets = [(32, [4096, 1024, 1024]), (17, [2000, 48, 1024]), (32, [4096, 4096, 1024, 1024])]
+    for M, ns in sets:
+        a, qs, scales = problem(M, K, ns, exact=False)
+        got = shared(lib, a, qs, scales, M, K)
+        for i, (g, w) in enumerate(zip(got, separate(lib, a, qs, scales, M, K))):
+            assert_bits_equal(g, w, f"M={M} C_{i}")
 
 
 def test_shared_a_consecutive_calls(lib):
