@@ -122,13 +122,14 @@ struct SharedSet {
 };
 
 // Per-product split-K parameters (gemm_i8w_split_shared_kernel): the
-// product's partial-sum region, its slice count, tiles of B and batches per
-// slice.
+// product's partial-sum region, its slice count, tiles of B, batches per
+// slice and token tiles.
 struct SplitSet {
     float* part[kMaxShared];
     int S[kMaxShared];
     int tiles[kMaxShared];
     int cps[kMaxShared];
+    int TT[kMaxShared];
 };
 
 // Element p of four (a select chain on a wave-uniform p).
@@ -697,7 +698,8 @@ __global__ __launch_bounds__(G * W * kWave) void gemm_i8w_split_shared_kernel(Sh
         gemm_i8w_split_block<MT, W, G>(c, a, b, scale, pick4(p, sp.part[0], sp.part[1], sp.part[2], sp.part[3]), M,
                                        n, K, pick4(p, sp.S[0], sp.S[1], sp.S[2], sp.S[3]),
                                        pick4(p, sp.tiles[0], sp.tiles[1], sp.tiles[2], sp.tiles[3]),
-                                       pick4(p, sp.cps[0], sp.cps[1], sp.cps[2], sp.cps[3]), 1, blk);
+                                       pick4(p, sp.cps[0], sp.cps[1], sp.cps[2], sp.cps[3]),
+                                       pick4(p, sp.TT[0], sp.TT[1], sp.TT[2], sp.TT[3]), blk);
     });
 }
 
@@ -1254,16 +1256,14 @@ SplitConfig split_config(int M, int K, int N) {
     return kSmallM;
 }
 
-// The kernel gemm_i8w runs for a product on the weight-streaming path, for
-// ng_gemm_int8_shared_a: the GEMV shapes 1-3 above, 4 for the small-M MFMA
-// kernel, 10 + c for split shape c that ng_gemm_int8_shared_a can share
-// (one tile of A per block), 0 for the rest (token tiles).
+// The launch shape gemm_i8w takes for a product on the weight-streaming
+// path, for ng_gemm_int8_shared_a: the GEMV shapes 1-3 above, 4 for the
+// small-M MFMA kernel, 10 + c for split shape c.
 int shared_path(int M, int K, int N) {
     const int gv = gemv_shape(M, K, N);
     if (gv != 0) return gv;
     const SplitConfig sc = split_config(M, K, N);
-    if (sc == kSmallM) return 4;
-    return sc == kSplitTokenTiles ? 0 : 10 + static_cast<int>(sc);
+    return sc == kSmallM ? 4 : 10 + static_cast<int>(sc);
 }
 
 // Kernel and tile shape by M, K and N, from sweeps on MI355X over K x N in
@@ -1464,12 +1464,12 @@ extern "C" int ng_gemm_int8_noalloc(void* c, const void* a, const void* b, const
 // launch_split).
 template <int MT, int W, int G>
 int launch_split_shared(int count, void* const* c, const uint16_t* a, const void* const* b,
-                        const void* const* scales, const int* n, int M, int K) {
+                        const void* const* scales, const int* n, int M, int K, int TT) {
     int S[kMaxShared] = {}, cps[kMaxShared] = {}, tiles[kMaxShared] = {};
     long long cols = 0;
     for (int i = 0; i < count; ++i) {
         tiles[i] = (n[i] + 16 * W - 1) / (16 * W);
-        split_slices(tiles[i], 1, G, K, S[i], cps[i]);
+        split_slices(tiles[i], TT, G, K, S[i], cps[i]);
         if (S[i] > 1) cols += static_cast<long long>(S[i]) * n[i];
     }
     NG_REQUIRE(cols < (1ll << 31), "ng_gemm_int8_shared_a: too many rows of B");
@@ -1490,11 +1490,13 @@ int launch_split_shared(int count, void* const* c, const uint16_t* a, const void
         sp.S[i] = S[j];
         sp.tiles[i] = tiles[j];
         sp.cps[i] = cps[j];
+        sp.TT[i] = TT;
         sp.part[i] = nullptr;
         set.first[i] = i < count ? static_cast<int>(blocks) : INT_MAX;
         rset.first[i] = i < count ? static_cast<int>(rblocks) : INT_MAX;
         if (i >= count) continue;
-        blocks += static_cast<long long>(tiles[i]) * S[i];
+        const long long units = static_cast<long long>(tiles[i]) * S[i];
+        blocks += TT > 1 ? (units + 7) / 8 * 8 * TT : units;  // as launch_split
         if (S[i] > 1) {
             sp.part[i] = part + off;
             off += static_cast<long long>(S[i]) * M * n[i];
@@ -1526,42 +1528,25 @@ int launch_split_shared(int count, void* const* c, const uint16_t* a, const void
     return 0;
 }
 
-// Products that share A (the engine's q/k/v and gate/up projections): when
-// every one takes the same kernel of gemm_i8w (the GEMV kernel with one
-// shape, or the small-M MFMA kernel), one launch of that kernel's shared form
-// runs them all, each product's blocks exactly as its own launch would;
-// otherwise one cuda_gemm_int8 call each. Either way the results are
-// cuda_gemm_int8's, bit for bit.
-extern "C" int ng_gemm_int8_shared_a(int count, void* const* c, const void* a, const void* const* b,
-                                     const void* const* scales, const int* n, int M, int K) {
-    NG_REQUIRE(c && a && b && scales && n, "ng_gemm_int8_shared_a: null pointer");
-    NG_REQUIRE(count >= 1 && count <= kMaxShared, "ng_gemm_int8_shared_a: count=%d must be in [1, %d]", count,
-               kMaxShared);
-    NG_REQUIRE(M > 0 && K > 0, "ng_gemm_int8_shared_a: M=%d K=%d must be > 0", M, K);
-    int path = -1;
-    for (int i = 0; i < count; ++i) {
-        NG_REQUIRE(c[i] && b[i] && scales[i], "ng_gemm_int8_shared_a: null pointer in product %d", i);
-        NG_REQUIRE(n[i] > 0, "ng_gemm_int8_shared_a: n[%d]=%d must be > 0", i, n[i]);
-        const int pi = use_i8w(a, b[i], M, K, n[i], true) ? shared_path(M, K, n[i]) : 0;
-        path = (path == -1 || path == pi) ? pi : 0;
-    }
-    if (path <= 0 || count == 1) {
-        for (int i = 0; i < count; ++i) {
-            const int r = cuda_gemm_int8(c[i], a, b[i], scales[i], M, K, n[i], true);
-            if (r != 0) return r;
+// One group of products that take the same launch shape `path` (see
+// shared_path), in one launch of that kernel's shared form; shapes without a
+// shared form, and groups of one, are one cuda_gemm_int8 call per product.
+int shared_group(int path, int count, void* const* c, const void* a, const void* const* b,
+                 const void* const* scales, const int* n, int M, int K) {
+    const auto* ap = static_cast<const uint16_t*>(a);
+    if (count > 1) {
+        switch (path) {
+            case 10 + kSplitTokenTiles:
+                return launch_split_shared<2, 4, 1>(count, c, ap, b, scales, n, M, K, (M + 31) / 32);
+            case 10 + kSplit241: return launch_split_shared<2, 4, 1>(count, c, ap, b, scales, n, M, K, 1);
+            case 10 + kSplit142: return launch_split_shared<1, 4, 2>(count, c, ap, b, scales, n, M, K, 1);
+            case 10 + kSplit242: return launch_split_shared<2, 4, 2>(count, c, ap, b, scales, n, M, K, 1);
+            case 10 + kSplit442: return launch_split_shared<4, 4, 2>(count, c, ap, b, scales, n, M, K, 1);
+            case 10 + kSplit842: return launch_split_shared<8, 4, 2>(count, c, ap, b, scales, n, M, K, 1);
+            default: break;
         }
-        return 0;
     }
-    const auto* ap0 = static_cast<const uint16_t*>(a);
-    switch (path) {
-        case 10 + kSplit241: return launch_split_shared<2, 4, 1>(count, c, ap0, b, scales, n, M, K);
-        case 10 + kSplit142: return launch_split_shared<1, 4, 2>(count, c, ap0, b, scales, n, M, K);
-        case 10 + kSplit242: return launch_split_shared<2, 4, 2>(count, c, ap0, b, scales, n, M, K);
-        case 10 + kSplit442: return launch_split_shared<4, 4, 2>(count, c, ap0, b, scales, n, M, K);
-        case 10 + kSplit842: return launch_split_shared<8, 4, 2>(count, c, ap0, b, scales, n, M, K);
-        default: break;
-    }
-    if (path >= 10) {  // split shapes no group of the engine's projections shares: one call each
+    if (count == 1 || path <= 0 || path >= 10) {
         for (int i = 0; i < count; ++i) {
             const int r = cuda_gemm_int8(c[i], a, b[i], scales[i], M, K, n[i], true);
             if (r != 0) return r;
@@ -1581,7 +1566,6 @@ extern "C" int ng_gemm_int8_shared_a(int count, void* const* c, const void* a, c
         if (i < count) blocks += (n[i] + R - 1) / R;
         NG_REQUIRE(blocks < (1ll << 31), "ng_gemm_int8_shared_a: too many rows of B");
     }
-    const auto* ap = static_cast<const uint16_t*>(a);
     const int nb = static_cast<int>(blocks);
     switch (path) {
         case 1: return launch_gemv_shared<1, 8>(set, nb, ap, M, K);
@@ -1593,4 +1577,44 @@ extern "C" int ng_gemm_int8_shared_a(int count, void* const* c, const void* a, c
             NG_CHECK_LAUNCH("ng_gemm_int8_shared_a");
             return 0;
     }
+}
+
+// Products that share A (the engine's q/k/v and gate/up projections): they
+// are grouped by the launch shape gemm_i8w would take for each, and each group
+// runs in one launch of that kernel's shared form (plus one launch of the
+// split kernel's reduction), each product's blocks exactly as its own launch
+// would. Products outside the weight-streaming path are one cuda_gemm_int8
+// call each. Either way the results are cuda_gemm_int8's, bit for bit.
+extern "C" int ng_gemm_int8_shared_a(int count, void* const* c, const void* a, const void* const* b,
+                                     const void* const* scales, const int* n, int M, int K) {
+    NG_REQUIRE(c && a && b && scales && n, "ng_gemm_int8_shared_a: null pointer");
+    NG_REQUIRE(count >= 1 && count <= kMaxShared, "ng_gemm_int8_shared_a: count=%d must be in [1, %d]", count,
+               kMaxShared);
+    NG_REQUIRE(M > 0 && K > 0, "ng_gemm_int8_shared_a: M=%d K=%d must be > 0", M, K);
+    int path[kMaxShared];
+    for (int i = 0; i < count; ++i) {
+        NG_REQUIRE(c[i] && b[i] && scales[i], "ng_gemm_int8_shared_a: null pointer in product %d", i);
+        NG_REQUIRE(n[i] > 0, "ng_gemm_int8_shared_a: n[%d]=%d must be > 0", i, n[i]);
+        path[i] = use_i8w(a, b[i], M, K, n[i], true) ? shared_path(M, K, n[i]) : 0;
+    }
+    bool done[kMaxShared] = {};
+    for (int i = 0; i < count; ++i) {
+        if (done[i]) continue;
+        void* gc[kMaxShared];
+        const void* gb[kMaxShared];
+        const void* gs[kMaxShared];
+        int gn[kMaxShared], g = 0;
+        for (int j = i; j < count; ++j) {
+            if (done[j] || path[j] != path[i] || (path[i] <= 0 && j != i)) continue;
+            gc[g] = c[j];
+            gb[g] = b[j];
+            gs[g] = scales[j];
+            gn[g] = n[j];
+            ++g;
+            done[j] = true;
+        }
+        const int r = shared_group(path[i], g, gc, a, gb, gs, gn, M, K);
+        if (r != 0) return r;
+    }
+    return 0;
 }

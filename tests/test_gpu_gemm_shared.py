@@ -3,9 +3,9 @@
 Bars:
   * every C_i is bit-identical to its own cuda_gemm_int8(c_i, a, b_i, scale_i,
     M, K, n_i, true) on the same inputs (random activations, random codes and
-    scales), whether the products ran in one launch (every product on the same
-    kernel: the GEMV kernel with one shape, or the small-M MFMA kernel) or as
-    one call each;
+    scales), whether a product ran in a shared launch (with the products of
+    the same launch shape: the GEMV kernel, the small-M MFMA kernel, or the
+    split kernel and its reduction) or as its own call;
   * exact inputs (activations on a grid 2^-e, so that every partial sum of
     A @ q is exact in fp32) give fp16(fp32(sum_k a_k q_k) * scale[n]) bit for
     bit, the weight-streaming paths' formula, checked against numpy;
@@ -56,11 +56,16 @@ SETS = [
     (20, 4096, [14336, 14336]),
     (64, 4096, [14336, 14336]),
     (100, 4096, [14336, 14336]),
-    # no shared launch: a small-M MFMA product with a split one, a GEMV product
-    # with a split one, k/v with token tiles beside q (M = 64), down's deep shape
+    # products of different shapes, grouped: k and v with token tiles in one
+    # launch beside q alone (M = 33-128), two GEMV products and two split ones
+    # in two launches, a small-M MFMA product with a split one, a GEMV product
+    # with a split one; and down's deep shape, which has no shared form
+    (64, 4096, [4096, 1024, 1024]),
+    (33, 4096, [4096, 1024, 1024]),
+    (100, 4160, [1000, 2048, 77]),
+    (3, 4096, [4096, 12300, 1024, 14336]),
     (12, 4096, [4096, 14336]),
     (3, 4096, [4096, 12300]),
-    (64, 4096, [4096, 1024, 1024]),
     (20, 14336, [4096, 4096]),
 ]
 
@@ -126,7 +131,8 @@ def test_shared_a_is_cuda_gemm_int8_bit_for_bit(lib, M, K, ns):
                                     (3, 2064, [17, 1, 40]), (8, 4096, [4096, 1024, 1024]),
                                     (5, 4160, [1000, 77, 2048]), (3, 4096, [4096, 12300]),
                                     (24, 4160, [1000, 77, 2048]), (20, 2048, [1000, 1001]),
-                                    (8, 4096, [14336, 14336]), (100, 4096, [14336, 14336])])
+                                    (8, 4096, [14336, 14336]), (100, 4096, [14336, 14336]),
+                                    (64, 4096, [4096, 1024, 1024]), (3, 4096, [4096, 12300, 1024, 14336])])
 def test_shared_a_exact_inputs(lib, M, K, ns):
     banner(f"gemm_int8_shared_a exact M={M} K={K} n={ns}")
     a, qs, scales = problem(M, K, ns, exact=True)
