@@ -131,9 +131,10 @@ int ng_gemm_int8_noalloc(void* c, const void* a, const void* b, const void* scal
  * The products that take the same launch shape of cuda_gemm_int8's
  * weight-streaming kernels (16-byte aligned A and B, M <= 128) run in one
  * launch of that kernel (plus one launch of the split kernel's reduction,
- * whose partial sums live in the stream's buffer, as for cuda_gemm_int8):
- * q/k/v together up to 32 tokens, k/v together from 33, gate/up together up to
- * 128. Every other product is one cuda_gemm_int8 call. The
+ * whose partial sums live in the stream's buffer, as for cuda_gemm_int8); at
+ * Mistral-7B's shapes q/k/v together up to 32 tokens, k/v together from 33,
+ * gate/up together up to 128. Every other product is one cuda_gemm_int8 call.
+ * The
  * arrays c, b, scales and n are host arrays. C_i must not overlap A or each
  * other. Returns 0, or -1 (null pointers, count outside 1..4, sizes <= 0, or
  * a failing cuda_gemm_int8). */
