@@ -773,8 +773,8 @@ def shared_a_extras(L, hip, stream):
     """ng_gemm_int8_shared_a against separate cuda_gemm_int8 calls for the
     projections of one Mistral-7B INT8 layer that read the same normed rows:
     q/k/v (layer.cu:487-501) and gate/up (layer.cu:575-583), at M = 1, 2, 8,
-    32 and 64 decode tokens. Both forms give the same bits; weight pools keep
-    the codes cache-cold."""
+    32 and 64 decode tokens and 512 and 2048 prefill tokens. Both forms give
+    the same bits; weight pools keep the codes cache-cold."""
     rng = np.random.Generator(np.random.PCG64(5))
     K = 4096
     sets = {"qkv": [4096, 1024, 1024], "gate_up": [14336, 14336]}
@@ -787,7 +787,7 @@ def shared_a_extras(L, hip, stream):
             pools.append((N, Pool(hip, wq.nbytes, n, wq), DB.from_array(rng.uniform(1e-3, 1e-2, N).astype(np.float32))))
             del wq
         cnt = len(ns)
-        for M in (1, 2, 8, 32, 64):
+        for M in (1, 2, 8, 32, 64, 512, 2048):
             ab = DB.from_array(W.round_to(rng.standard_normal((M, K), dtype=np.float32), "f16"))
             cps = [Pool(hip, 2 * M * N, n) for N in ns]
 
@@ -816,8 +816,8 @@ def shared_a_extras(L, hip, stream):
             sc.free()
     out["note"] = ("us: one ng_gemm_int8_shared_a call (one launch per group of products with the same launch "
                    "shape: the GEMV kernel at 1-2 tokens, the small-M MFMA kernel for q/k/v at 8, the split kernel "
-                   "and its reduction otherwise; at 64 tokens q alone and k/v together); separate_us: one "
-                   "cuda_gemm_int8 call per projection")
+                   "and its reduction up to 128 tokens (at 64 q alone and k/v together), the fused prefill kernel "
+                   "and its reduction above); separate_us: one cuda_gemm_int8 call per projection")
     return out
 
 

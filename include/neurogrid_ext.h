@@ -128,13 +128,13 @@ int ng_gemm_int8_noalloc(void* c, const void* a, const void* b, const void* scal
  * bit for bit (B_i int8 [n[i], K], per-row scales, C_i fp16 [M, n[i]]). The
  * engine's INT8 layer calls cuda_gemm_int8 three times on the same normed rows
  * for q/k/v (gpu/engine/layer.cu:487-501) and twice for gate/up (:575-583).
- * The products that take the same launch shape of cuda_gemm_int8's
- * weight-streaming kernels (16-byte aligned A and B, M <= 128) run in one
- * launch of that kernel (plus one launch of the split kernel's reduction,
- * whose partial sums live in the stream's buffer, as for cuda_gemm_int8); at
- * Mistral-7B's shapes q/k/v together up to 32 tokens, k/v together from 33,
- * gate/up together up to 128. Every other product is one cuda_gemm_int8 call.
- * The
+ * The products that take the same launch shape of cuda_gemm_int8's fused
+ * kernels (16-byte aligned A and B, M below 4096) run in one launch of that
+ * kernel (plus one launch of the split-K reduction, whose partial sums live
+ * in the stream's buffer, as for cuda_gemm_int8); at Mistral-7B's shapes
+ * q/k/v together up to 32 tokens, k/v together from 33 to 128, gate/up
+ * together up to 128, and on the prefill kernel the products of one tile
+ * shape together. Every other product is one cuda_gemm_int8 call. The
  * arrays c, b, scales and n are host arrays. C_i must not overlap A or each
  * other. Returns 0, or -1 (null pointers, count outside 1..4, sizes <= 0, or
  * a failing cuda_gemm_int8). */

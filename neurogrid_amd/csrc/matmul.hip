@@ -796,10 +796,10 @@ constexpr int kPfBlocks = 512;
 __device__ __forceinline__ int pf_slot(int row, int q) { return row * 8 + (q ^ ((row >> 1) & 7)); }
 
 template <int TM, int TN, int WM, int WN>
-__global__ __launch_bounds__(WM * WN * kWave, 1) void gemm_i8w_prefill_kernel(
+__device__ __forceinline__ void gemm_i8w_prefill_block(
     uint16_t* __restrict__ c, const uint16_t* __restrict__ a, const int8_t* __restrict__ b,
     const float* __restrict__ scale, float* __restrict__ part, int M, int N, int K, int tiles_m, int tiles_n,
-    int S, int cps) {
+    int S, int cps, int blk) {
     constexpr int kThreads = WM * WN * kWave;
     constexpr int BM = WM * TM * 16, BN = WN * TN * 16;
     constexpr int kAP = BM * 8 / kThreads;  // 16-byte pieces (8 k) of A per thread per step
@@ -810,7 +810,7 @@ __global__ __launch_bounds__(WM * WN * kWave, 1) void gemm_i8w_prefill_kernel(
     __shared__ __align__(16) u32x4 lds_b[2][BN * 8];
 
     const int ntiles = tiles_m * tiles_n;
-    int t = blockIdx.x;
+    int t = blk;
     if ((ntiles * S) % 8 == 0) t = (t % 8) * (ntiles * S / 8) + t / 8;
     const int sl = t / ntiles;
     t -= sl * ntiles;
@@ -949,6 +949,32 @@ __global__ __launch_bounds__(WM * WN * kWave, 1) void gemm_i8w_prefill_kernel(
                 }
         }
     }
+}
+
+template <int TM, int TN, int WM, int WN>
+__global__ __launch_bounds__(WM * WN * kWave, 1) void gemm_i8w_prefill_kernel(
+    uint16_t* __restrict__ c, const uint16_t* __restrict__ a, const int8_t* __restrict__ b,
+    const float* __restrict__ scale, float* __restrict__ part, int M, int N, int K, int tiles_m, int tiles_n,
+    int S, int cps) {
+    gemm_i8w_prefill_block<TM, TN, WM, WN>(c, a, b, scale, part, M, N, K, tiles_m, tiles_n, S, cps, blockIdx.x);
+}
+
+// Products that share A on one prefill tile shape (ng_gemm_int8_shared_a):
+// each product keeps its own tiles, K slices and partial-sum region. In
+// SplitSet, `tiles` holds the product's tiles along N and `TT` its tiles
+// along M. A product's blocks keep their own launch's placement on the XCDs up
+// to a rotation: the tiles that one launch gives to one XCD still share one.
+template <int TM, int TN, int WM, int WN>
+__global__ __launch_bounds__(WM * WN * kWave, 1) void gemm_i8w_prefill_shared_kernel(SharedSet s, SplitSet sp,
+                                                                                     const uint16_t* __restrict__ a,
+                                                                                     int M, int K) {
+    shared_dispatch(s, [&](uint16_t* c, const int8_t* b, const float* scale, int n, int blk, int p) {
+        gemm_i8w_prefill_block<TM, TN, WM, WN>(c, a, b, scale, pick4(p, sp.part[0], sp.part[1], sp.part[2], sp.part[3]),
+                                               M, n, K, pick4(p, sp.TT[0], sp.TT[1], sp.TT[2], sp.TT[3]),
+                                               pick4(p, sp.tiles[0], sp.tiles[1], sp.tiles[2], sp.tiles[3]),
+                                               pick4(p, sp.S[0], sp.S[1], sp.S[2], sp.S[3]),
+                                               pick4(p, sp.cps[0], sp.cps[1], sp.cps[2], sp.cps[3]), blk);
+    });
 }
 
 // ---- hipBLASLt path ----------------------------------------------------------
@@ -1309,19 +1335,24 @@ bool use_prefill(const void* a, const void* b, int M, int K, int N, bool transpo
            static_cast<long long>(M) * K * 2 < (1ll << 31) && static_cast<long long>(N) * K < (1ll << 31);
 }
 
+// K slices of a prefill launch of `tiles` tiles of `area` outputs: for about
+// kPfBlocks blocks, at most 8, each of 4 steps or more; none for 256 x 256
+// tiles, which are only chosen when there are enough of them to fill the CUs.
+void prefill_slices(int tiles, int area, int K, int& S, int& cps) {
+    const int nk = (K + kPfBK - 1) / kPfBK;
+    S = area >= 65536 ? 1 : max(1, min((kPfBlocks + tiles - 1) / tiles, min(8, nk / 4)));
+    cps = (nk + S - 1) / S;
+    S = (nk + cps - 1) / cps;
+}
+
 template <int TM, int TN, int WM, int WN>
 int launch_prefill(uint16_t* c, const uint16_t* a, const int8_t* b, const float* scale, int M, int N, int K,
                    float* scratch, size_t scratch_bytes) {
     constexpr int BM = WM * TM * 16, BN = WN * TN * 16;
     const int tiles_m = (M + BM - 1) / BM, tiles_n = (N + BN - 1) / BN;
     const int tiles = tiles_m * tiles_n;
-    const int nk = (K + kPfBK - 1) / kPfBK;
-    // K slices for about kPfBlocks blocks, at most 8, each of 4 steps or
-    // more; none for 256 x 256 tiles, which are only chosen when there are
-    // enough of them to fill the CUs.
-    int S = BM * BN >= 65536 ? 1 : max(1, min((kPfBlocks + tiles - 1) / tiles, min(8, nk / 4)));
-    const int cps = (nk + S - 1) / S;
-    S = (nk + cps - 1) / cps;
+    int S = 0, cps = 0;
+    prefill_slices(tiles, BM * BN, K, S, cps);
     const hipStream_t s = stream();
     float* part = nullptr;
     std::unique_lock<std::mutex> lock(g_mu, std::defer_lock);
@@ -1335,14 +1366,17 @@ int launch_prefill(uint16_t* c, const uint16_t* a, const int8_t* b, const float*
 // Tile shape by the number of tiles (see the prefill kernel): 256 x 256
 // when that gives at least 192 tiles (three quarters of the CUs), otherwise
 // 128 x 128 with K slices.
+bool prefill_wide_tiles(int M, int N) {
+    return static_cast<long long>((M + 255) / 256) * ((N + 255) / 256) >= 192;
+}
+
 int gemm_prefill(void* c, const void* a, const void* b, const void* scale, int M, int K, int N,
                  float* scratch = nullptr, size_t scratch_bytes = 0) {
     auto* cp = static_cast<uint16_t*>(c);
     auto* ap = static_cast<const uint16_t*>(a);
     auto* bp = static_cast<const int8_t*>(b);
     auto* sp = static_cast<const float*>(scale);
-    const long long tiles256 = static_cast<long long>((M + 255) / 256) * ((N + 255) / 256);
-    if (tiles256 >= 192) return launch_prefill<4, 4, 4, 4>(cp, ap, bp, sp, M, N, K, scratch, scratch_bytes);
+    if (prefill_wide_tiles(M, N)) return launch_prefill<4, 4, 4, 4>(cp, ap, bp, sp, M, N, K, scratch, scratch_bytes);
     return launch_prefill<4, 4, 2, 2>(cp, ap, bp, sp, M, N, K, scratch, scratch_bytes);
 }
 
@@ -1457,21 +1491,24 @@ extern "C" int ng_gemm_int8_noalloc(void* c, const void* a, const void* b, const
     return gemm_prefill(c, a, b, scale, M, K, N, part, kNoAllocScratchBytes);
 }
 
-// Products that share A on one split-kernel shape: one launch of the split
-// kernel, and one of the reduction for the products with more than one slice
-// of K, each product with its own slices and its own region of the stream's
-// partial-sum buffer (the lock is held until both kernels are enqueued, as in
-// launch_split).
-template <int MT, int W, int G>
-int launch_split_shared(int count, void* const* c, const uint16_t* a, const void* const* b,
-                        const void* const* scales, const int* n, int M, int K, int TT) {
-    int S[kMaxShared] = {}, cps[kMaxShared] = {}, tiles[kMaxShared] = {};
+// Per-product plan of a shared split-K launch: K slices, batches per slice,
+// tiles along N and along M (the split kernel: token tiles), and blocks.
+struct SharedPlan {
+    int S[kMaxShared], cps[kMaxShared], tn[kMaxShared], tm[kMaxShared];
+    long long blocks[kMaxShared];
+};
+
+// Products that share A on one split-K kernel shape: one launch of the kernel
+// (`launch(set, sp, blocks)`), then one of the reduction for the products with
+// more than one slice of K, each product with its own slices and its own
+// region of the stream's partial-sum buffer (the lock is held until both
+// kernels are enqueued, as in launch_split).
+template <typename L>
+int run_shared_split(int count, void* const* c, const void* const* b, const void* const* scales, const int* n,
+                     int M, int K, const SharedPlan& pl, L&& launch) {
     long long cols = 0;
-    for (int i = 0; i < count; ++i) {
-        tiles[i] = (n[i] + 16 * W - 1) / (16 * W);
-        split_slices(tiles[i], TT, G, K, S[i], cps[i]);
-        if (S[i] > 1) cols += static_cast<long long>(S[i]) * n[i];
-    }
+    for (int i = 0; i < count; ++i)
+        if (pl.S[i] > 1) cols += static_cast<long long>(pl.S[i]) * n[i];
     NG_REQUIRE(cols < (1ll << 31), "ng_gemm_int8_shared_a: too many rows of B");
     const hipStream_t st = stream();
     float* part = nullptr;
@@ -1487,19 +1524,18 @@ int launch_split_shared(int count, void* const* c, const uint16_t* a, const void
         set.b[i] = rset.b[i] = static_cast<const int8_t*>(b[j]);
         set.scale[i] = rset.scale[i] = static_cast<const float*>(scales[j]);
         set.n[i] = rset.n[i] = n[j];
-        sp.S[i] = S[j];
-        sp.tiles[i] = tiles[j];
-        sp.cps[i] = cps[j];
-        sp.TT[i] = TT;
+        sp.S[i] = pl.S[j];
+        sp.tiles[i] = pl.tn[j];
+        sp.cps[i] = pl.cps[j];
+        sp.TT[i] = pl.tm[j];
         sp.part[i] = nullptr;
         set.first[i] = i < count ? static_cast<int>(blocks) : INT_MAX;
         rset.first[i] = i < count ? static_cast<int>(rblocks) : INT_MAX;
         if (i >= count) continue;
-        const long long units = static_cast<long long>(tiles[i]) * S[i];
-        blocks += TT > 1 ? (units + 7) / 8 * 8 * TT : units;  // as launch_split
-        if (S[i] > 1) {
+        blocks += pl.blocks[i];
+        if (pl.S[i] > 1) {
             sp.part[i] = part + off;
-            off += static_cast<long long>(S[i]) * M * n[i];
+            off += static_cast<long long>(pl.S[i]) * M * n[i];
             const bool v4 = n[i] % 4 == 0 && aligned16(scales[i]) && aligned8(c[i]);
             vec4_all = vec4_all && v4;
             vec4_any = vec4_any || v4;
@@ -1508,8 +1544,7 @@ int launch_split_shared(int count, void* const* c, const uint16_t* a, const void
         }
         NG_REQUIRE(blocks < (1ll << 31) && rblocks < (1ll << 31), "ng_gemm_int8_shared_a: too many rows of B");
     }
-    gemm_i8w_split_shared_kernel<MT, W, G><<<dim3(static_cast<unsigned>(blocks)), dim3(G * W * kWave), 0, st>>>(
-        set, sp, a, M, K);
+    launch(set, sp, static_cast<unsigned>(blocks), st);
     NG_CHECK_LAUNCH("ng_gemm_int8_shared_a");
     if (rblocks == 0) return 0;
     if (vec4_all || !vec4_any) {
@@ -1522,11 +1557,53 @@ int launch_split_shared(int count, void* const* c, const uint16_t* a, const void
     }
     // Products whose reductions take different forms: one reduction each.
     for (int i = 0; i < count; ++i)
-        if (S[i] > 1 && launch_reduce(st, static_cast<uint16_t*>(c[i]), sp.part[i], static_cast<const float*>(scales[i]),
-                                      M, n[i], S[i]) != 0)
+        if (pl.S[i] > 1 && launch_reduce(st, static_cast<uint16_t*>(c[i]), sp.part[i],
+                                         static_cast<const float*>(scales[i]), M, n[i], pl.S[i]) != 0)
             return -1;
     return 0;
 }
+
+// The split kernel's shared form: slices and blocks as launch_split.
+template <int MT, int W, int G>
+int launch_split_shared(int count, void* const* c, const uint16_t* a, const void* const* b,
+                        const void* const* scales, const int* n, int M, int K, int TT) {
+    SharedPlan pl{};
+    for (int i = 0; i < count; ++i) {
+        pl.tn[i] = (n[i] + 16 * W - 1) / (16 * W);
+        pl.tm[i] = TT;
+        split_slices(pl.tn[i], TT, G, K, pl.S[i], pl.cps[i]);
+        const long long units = static_cast<long long>(pl.tn[i]) * pl.S[i];
+        pl.blocks[i] = TT > 1 ? (units + 7) / 8 * 8 * TT : units;
+    }
+    return run_shared_split(count, c, b, scales, n, M, K, pl,
+                            [&](const SharedSet& set, const SplitSet& sp, unsigned blocks, hipStream_t st) {
+                                gemm_i8w_split_shared_kernel<MT, W, G>
+                                    <<<dim3(blocks), dim3(G * W * kWave), 0, st>>>(set, sp, a, M, K);
+                            });
+}
+
+// The prefill kernel's shared form: tiles and slices as launch_prefill.
+template <int TM, int TN, int WM, int WN>
+int launch_prefill_shared(int count, void* const* c, const uint16_t* a, const void* const* b,
+                          const void* const* scales, const int* n, int M, int K) {
+    constexpr int BM = WM * TM * 16, BN = WN * TN * 16;
+    SharedPlan pl{};
+    for (int i = 0; i < count; ++i) {
+        pl.tm[i] = (M + BM - 1) / BM;
+        pl.tn[i] = (n[i] + BN - 1) / BN;
+        prefill_slices(pl.tm[i] * pl.tn[i], BM * BN, K, pl.S[i], pl.cps[i]);
+        pl.blocks[i] = static_cast<long long>(pl.tm[i]) * pl.tn[i] * pl.S[i];
+    }
+    return run_shared_split(count, c, b, scales, n, M, K, pl,
+                            [&](const SharedSet& set, const SplitSet& sp, unsigned blocks, hipStream_t st) {
+                                gemm_i8w_prefill_shared_kernel<TM, TN, WM, WN>
+                                    <<<dim3(blocks), dim3(WM * WN * kWave), 0, st>>>(set, sp, a, M, K);
+                            });
+}
+
+// Launch shapes of the fused prefill kernel for ng_gemm_int8_shared_a: 128 x 128
+// tiles with K slices, or 256 x 256 tiles.
+constexpr int kPathPrefill128 = 40, kPathPrefill256 = 41;
 
 // One group of products that take the same launch shape `path` (see
 // shared_path), in one launch of that kernel's shared form; shapes without a
@@ -1543,6 +1620,8 @@ int shared_group(int path, int count, void* const* c, const void* a, const void*
             case 10 + kSplit242: return launch_split_shared<2, 4, 2>(count, c, ap, b, scales, n, M, K, 1);
             case 10 + kSplit442: return launch_split_shared<4, 4, 2>(count, c, ap, b, scales, n, M, K, 1);
             case 10 + kSplit842: return launch_split_shared<8, 4, 2>(count, c, ap, b, scales, n, M, K, 1);
+            case kPathPrefill128: return launch_prefill_shared<4, 4, 2, 2>(count, c, ap, b, scales, n, M, K);
+            case kPathPrefill256: return launch_prefill_shared<4, 4, 4, 4>(count, c, ap, b, scales, n, M, K);
             default: break;
         }
     }
@@ -1595,7 +1674,11 @@ extern "C" int ng_gemm_int8_shared_a(int count, void* const* c, const void* a, c
     for (int i = 0; i < count; ++i) {
         NG_REQUIRE(c[i] && b[i] && scales[i], "ng_gemm_int8_shared_a: null pointer in product %d", i);
         NG_REQUIRE(n[i] > 0, "ng_gemm_int8_shared_a: n[%d]=%d must be > 0", i, n[i]);
-        path[i] = use_i8w(a, b[i], M, K, n[i], true) ? shared_path(M, K, n[i]) : 0;
+        // cuda_gemm_int8's fused prefill kernel runs below kLtMinM rows of A
+        path[i] = use_i8w(a, b[i], M, K, n[i], true) ? shared_path(M, K, n[i])
+                  : M < kLtMinM && use_prefill(a, b[i], M, K, n[i], true)
+                      ? (prefill_wide_tiles(M, n[i]) ? kPathPrefill256 : kPathPrefill128)
+                      : 0;
     }
     bool done[kMaxShared] = {};
     for (int i = 0; i < count; ++i) {

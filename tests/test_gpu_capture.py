@@ -177,7 +177,12 @@ def _ops():
         lambda L, i, o: L.ng_gemm_int8_noalloc(o["y"].vp, i["a64"].vp, i["wq"].vp, i["wsc"].vp, 64, GK, GN, True))
     add("ng_gemm_int8_noalloc_M200_prefill", {"y": (E2, (200, GN))},
         lambda L, i, o: L.ng_gemm_int8_noalloc(o["y"].vp, i["a200"].vp, i["wq"].vp, i["wsc"].vp, 200, GK, GN, True))
-    # products that share A in one launch: the split kernel with two K slices and the shared reduction (M = 24)
+    # products that share A in one launch: the prefill kernel with two K slices (M = 200)
+    add("ng_gemm_int8_shared_a_M200_prefill", {"y": (E2, (200, GN)), "y2": (E2, (200, GN))},
+        lambda L, i, o: L.ng_gemm_int8_shared_a(
+            2, (C.c_void_p * 2)(o["y"].ptr, o["y2"].ptr), i["a200"].vp, (C.c_void_p * 2)(i["wq"].ptr, i["wq"].ptr),
+            (C.c_void_p * 2)(i["wsc"].ptr, i["wsc"].ptr), (C.c_int * 2)(GN, GN), 200, GK))
+    # the split kernel with two K slices and the shared reduction (M = 24)
     add("ng_gemm_int8_shared_a_M24_split", {"y": (E2, (24, GN)), "y2": (E2, (24, GN))},
         lambda L, i, o: L.ng_gemm_int8_shared_a(
             2, (C.c_void_p * 2)(o["y"].ptr, o["y2"].ptr), i["a24"].vp, (C.c_void_p * 2)(i["wq"].ptr, i["wq"].ptr),

@@ -56,6 +56,17 @@ SETS = [
     (20, 4096, [14336, 14336]),
     (64, 4096, [14336, 14336]),
     (100, 4096, [14336, 14336]),
+    # the fused prefill kernel (129-4095 tokens): q/k/v on 128 x 128 tiles with
+    # K slices of several counts, ragged shapes, gate/up on 256 x 256 tiles,
+    # and q on 256 x 256 tiles beside k/v on 128 x 128 (two launches); from
+    # 4096 tokens on hipBLASLt, one call each
+    (512, 4096, [4096, 1024, 1024]),
+    (300, 1040, [4100, 1000, 77]),
+    (200, 4096, [14336, 4096]),
+    (1024, 4096, [14336, 14336]),
+    (2048, 4096, [4096, 1024, 1024]),
+    (3000, 4096, [4096, 1024, 1024]),
+    (4096, 4096, [4096, 1024]),
     # products of different shapes, grouped: k and v with token tiles in one
     # launch beside q alone (M = 33-128), two GEMV products and two split ones
     # in two launches, a small-M MFMA product with a split one, a GEMV product
@@ -132,7 +143,8 @@ def test_shared_a_is_cuda_gemm_int8_bit_for_bit(lib, M, K, ns):
                                     (5, 4160, [1000, 77, 2048]), (3, 4096, [4096, 12300]),
                                     (24, 4160, [1000, 77, 2048]), (20, 2048, [1000, 1001]),
                                     (8, 4096, [14336, 14336]), (100, 4096, [14336, 14336]),
-                                    (64, 4096, [4096, 1024, 1024]), (3, 4096, [4096, 12300, 1024, 14336])])
+                                    (64, 4096, [4096, 1024, 1024]), (3, 4096, [4096, 12300, 1024, 14336]),
+                                    (512, 4096, [4096, 1024, 1024]), (300, 1040, [4100, 1000, 77])])
 def test_shared_a_exact_inputs(lib, M, K, ns):
     banner(f"gemm_int8_shared_a exact M={M} K={K} n={ns}")
     a, qs, scales = problem(M, K, ns, exact=True)
