@@ -1284,7 +1284,8 @@ SplitConfig split_config(int M, int K, int N) {
 
 // The launch shape gemm_i8w takes for a product on the weight-streaming
 // path, for ng_gemm_int8_shared_a: the GEMV shapes 1-3 above, 4 for the
-// small-M MFMA kernel, 10 + c for split shape c.
+// small-M MFMA kernel, 10 + c for split shape c (10-22; the prefill kernel's
+// shapes are kPathPrefill128 and kPathPrefill256).
 int shared_path(int M, int K, int N) {
     const int gv = gemv_shape(M, K, N);
     if (gv != 0) return gv;
@@ -1499,7 +1500,7 @@ struct SharedPlan {
 };
 
 // Products that share A on one split-K kernel shape: one launch of the kernel
-// (`launch(set, sp, blocks)`), then one of the reduction for the products with
+// (`launch(set, sp, blocks, stream)`), then one of the reduction for the products with
 // more than one slice of K, each product with its own slices and its own
 // region of the stream's partial-sum buffer (the lock is held until both
 // kernels are enqueued, as in launch_split).
