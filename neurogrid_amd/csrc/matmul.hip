@@ -30,6 +30,9 @@
 // way into LDS (see the prefill section); from 4096 rows on (kLtMinM) the
 // reference's composition through hipBLASLt, which is faster there. B stored
 // [K, N] always goes through the composition (dequantize, then hipBLASLt).
+// Each fused kernel also has a shared form (ng_gemm_int8_shared_a) that runs
+// several products with the same A and the same launch shape in one launch,
+// each product's blocks as in its own launch.
 // MFMA layout: v_mfma_f32_16x16x32_f16 multiplies a 16 x 32 tile of A (rows
 // m) by a 32 x 16 tile of B^T (columns n). Lane l supplies row (l % 16) of
 // each operand and 8 values of k; the accumulator lane l holds rows
