@@ -670,6 +670,7 @@ def extra_kernels(L, hip, stream):
         x.free()
     out["gemm_int8"] = gemm_extras(L, hip, stream)
     out["gemm_int8_shared_a"] = sh = shared_a_extras(L, hip, stream)
+    out["norm_gemm_int8_shared_a"] = norm_shared_extras(L, hip, stream)
     g = out["gemm_int8"]
     g["mistral7b_layer_M1"]["shared_a_us"] = (sh["qkv_M1"]["us"] + g["q_proj_M1"]["us"] + sh["gate_up_M1"]["us"]
                                               + g["down_proj_M1"]["us"])
@@ -818,6 +819,70 @@ def shared_a_extras(L, hip, stream):
                    "shape: the GEMV kernel at 1-2 tokens, the small-M MFMA kernel for q/k/v at 8, the split kernel "
                    "and its reduction up to 128 tokens (at 64 q alone and k/v together), the fused prefill kernel "
                    "and its reduction above); separate_us: one cuda_gemm_int8 call per projection")
+    return out
+
+
+def norm_shared_extras(L, hip, stream):
+    """The decode steps norm -> projections of one Mistral-7B INT8 layer as one
+    call against the two calls it replaces: RMSNorm then q/k/v
+    (layer.cu:467,487-501); residual add + RMSNorm then q/k/v (the previous
+    layer's last residual add folded into the attention norm); residual add +
+    RMSNorm then gate/up (layer.cu:559-583); at M = 1, 2 and 4 tokens. us:
+    ng_rmsnorm_gemm_int8_shared_a / ng_add_rmsnorm_gemm_int8_shared_a;
+    two_calls_us: cuda_rmsnorm / cuda_add_rmsnorm, then ng_gemm_int8_shared_a.
+    The call is one launch where the products take at most 1024 GEMV blocks
+    (q/k/v at 1-2 tokens) and the two calls otherwise. Both give the same
+    bits; weight pools keep the codes cache-cold."""
+    rng = np.random.Generator(np.random.PCG64(6))
+    K = 4096
+    out = {}
+    w = DB.from_array(W.round_to(1 + 0.05 * rng.standard_normal(K, dtype=np.float32), "f16"))
+    for name, ns, add in (("rmsnorm_qkv", [4096, 1024, 1024], False), ("add_rmsnorm_qkv", [4096, 1024, 1024], True),
+                          ("add_rmsnorm_gate_up", [14336, 14336], True)):
+        n = pool_slots(sum(ns) * K)
+        pools = []
+        for N in ns:
+            wq = rng.integers(-128, 128, (N, K)).astype(np.int8)
+            pools.append((N, Pool(hip, wq.nbytes, n, wq), DB.from_array(rng.uniform(1e-3, 1e-2, N).astype(np.float32))))
+            del wq
+        cnt = len(ns)
+        scv = (C.c_void_p * cnt)(*[sc.ptr for _, _, sc in pools])
+        nv = (C.c_int * cnt)(*ns)
+        for M in (1, 2, 4):
+            xb = DB.from_array(W.round_to(rng.standard_normal((M, K), dtype=np.float32), "f16"))
+            rb = DB.from_array(W.round_to(rng.standard_normal((M, K), dtype=np.float32), "f16"))
+            yb, rob = DB(2 * M * K), DB(2 * M * K)
+            cps = [Pool(hip, 2 * M * N, n) for N in ns]
+            args = [((C.c_void_p * cnt)(*[cp.at(j) for cp in cps]), (C.c_void_p * cnt)(*[wp.at(j) for _, wp, _ in pools]))
+                    for j in range(n)]
+            eps = C.c_float(1e-5)
+
+            def one(j, M=M, xb=xb, rb=rb, yb=yb, rob=rob):
+                if add:
+                    return L.ng_add_rmsnorm_gemm_int8_shared_a(cnt, yb.vp, rob.vp, args[j][0], xb.vp, rb.vp, w.vp, eps,
+                                                               args[j][1], scv, nv, M, K)
+                return L.ng_rmsnorm_gemm_int8_shared_a(cnt, yb.vp, args[j][0], xb.vp, w.vp, eps, args[j][1], scv, nv,
+                                                       M, K)
+
+            def two(j, M=M, xb=xb, rb=rb, yb=yb, rob=rob):
+                rc = (L.cuda_add_rmsnorm(yb.vp, rob.vp, xb.vp, rb.vp, w.vp, M, K, eps) if add
+                      else L.cuda_rmsnorm(yb.vp, xb.vp, w.vp, M, K, eps))
+                return rc or L.ng_gemm_int8_shared_a(cnt, args[j][0], yb.vp, args[j][1], scv, nv, M, K)
+
+            us_two = time_pool_kernel(hip, stream, [("two_calls", (lambda j=j: two(j))) for j in range(n)])
+            us_one = time_pool_kernel(hip, stream, [("fused", (lambda j=j: one(j))) for j in range(n)])
+            rows = 2 * M * K * ((3 if add else 1) + (2 if add else 1)) + 2 * K   # x (+res) in, normed (+res_out) out, w
+            b = sum(N * K + 2 * M * N + 4 * N for N in ns) + rows
+            out[f"{name}_M{M}"] = {"us": us_one, "two_calls_us": us_two, "GBps": b / us_one / 1e3,
+                                   "frac": b / us_one / 1e3 / PEAK_GBPS, "bytes": b, "buffer_sets": n}
+            for cp in cps:
+                cp.free()
+            for x in (xb, rb, yb, rob):
+                x.free()
+        for _, wp, sc in pools:
+            wp.free()
+            sc.free()
+    w.free()
     return out
 
 
@@ -1394,7 +1459,8 @@ def main():
         return
     if args.gemm_only:
         print(json.dumps({"gemm_int8": gemm_extras(L, hip, stream),
-                          "gemm_int8_shared_a": shared_a_extras(L, hip, stream)}), flush=True)
+                          "gemm_int8_shared_a": shared_a_extras(L, hip, stream),
+                          "norm_gemm_int8_shared_a": norm_shared_extras(L, hip, stream)}), flush=True)
         return
     if args.floors_only:
         print(json.dumps({"floors": floor_extras(hip, stream)}), flush=True)

@@ -141,6 +141,30 @@ int ng_gemm_int8_noalloc(void* c, const void* a, const void* b, const void* scal
 int ng_gemm_int8_shared_a(int count, void* const* c, const void* a, const void* const* b,
                           const void* const* scales, const int* n, int M, int K);
 
+/* cuda_rmsnorm(normed, x, norm_weight, M, K, eps) followed by
+ * ng_gemm_int8_shared_a(count, c, normed, b, scales, n, M, K), bit for bit:
+ * the engine's INT8 layer normalises its input (gpu/engine/layer.cu:467) and
+ * then runs q/k/v on it (:487-501). When every product takes the GEMV kernel
+ * with one shape (M <= 4, aligned pointers), K <= 8192 and no output
+ * overlaps an input, the norm is folded into the products' launch: each block
+ * normalises the rows itself, and normed is still written. Otherwise this is
+ * the two calls. Returns 0 or -1. */
+int ng_rmsnorm_gemm_int8_shared_a(int count, void* normed, void* const* c, const void* x,
+                                  const void* norm_weight, float eps, const void* const* b,
+                                  const void* const* scales, const int* n, int M, int K);
+
+/* cuda_add_rmsnorm(normed, residual_out, x, residual_in, norm_weight, M, K,
+ * eps) followed by ng_gemm_int8_shared_a(count, c, normed, ...), bit for bit:
+ * the residual add and FFN norm of the INT8 layer (gpu/engine/layer.cu:559-570,
+ * fused as cuda_add_rmsnorm) and then gate/up (:575-583). Folded into one
+ * launch under the conditions above, where also residual_out and normed must
+ * not overlap x, residual_in or each other (an in-place call is the two
+ * calls). Returns 0 or -1. */
+int ng_add_rmsnorm_gemm_int8_shared_a(int count, void* normed, void* residual_out, void* const* c,
+                                      const void* x, const void* residual_in, const void* norm_weight,
+                                      float eps, const void* const* b, const void* const* scales,
+                                      const int* n, int M, int K);
+
 #ifdef __cplusplus
 }
 #endif

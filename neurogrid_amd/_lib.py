@@ -93,6 +93,10 @@ SIGNATURES: dict[str, tuple] = {
     "cuda_gemm_int8": (_i, [_vp, _cvp, _cvp, _cvp, _i, _i, _i, C.c_bool]),
     "ng_gemm_int8_noalloc": (_i, [_vp, _cvp, _cvp, _cvp, _i, _i, _i, C.c_bool]),
     "ng_gemm_int8_shared_a": (_i, [_i, C.POINTER(_vp), _cvp, C.POINTER(_cvp), C.POINTER(_cvp), _ip, _i, _i]),
+    "ng_rmsnorm_gemm_int8_shared_a": (_i, [_i, _vp, C.POINTER(_vp), _cvp, _cvp, _f, C.POINTER(_cvp),
+                                           C.POINTER(_cvp), _ip, _i, _i]),
+    "ng_add_rmsnorm_gemm_int8_shared_a": (_i, [_i, _vp, _vp, C.POINTER(_vp), _cvp, _cvp, _cvp, _f,
+                                               C.POINTER(_cvp), C.POINTER(_cvp), _ip, _i, _i]),
 }
 
 _LIB = None

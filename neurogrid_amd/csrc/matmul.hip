@@ -32,7 +32,9 @@
 // [K, N] always goes through the composition (dequantize, then hipBLASLt).
 // Each fused kernel also has a shared form (ng_gemm_int8_shared_a) that runs
 // several products with the same A and the same launch shape in one launch,
-// each product's blocks as in its own launch.
+// each product's blocks as in its own launch; the GEMV kernel's shared form
+// can also normalise A itself (ng_rmsnorm_gemm_int8_shared_a and the add +
+// RMSNorm form), each block in registers, for the decode steps norm -> q/k/v.
 // MFMA layout: v_mfma_f32_16x16x32_f16 multiplies a 16 x 32 tile of A (rows
 // m) by a 32 x 16 tile of B^T (columns n). Lane l supplies row (l % 16) of
 // each operand and 8 values of k; the accumulator lane l holds rows
@@ -46,6 +48,8 @@
 // Every sum is taken in a fixed order (partial sums meet in LDS or in the
 // slice buffer, never through atomics), so results do not depend on timing.
 #include "ng_common.hpp"
+#include "ng_exact.hpp"
+#include "../../include/kernels.h"
 #include "../../include/matmul.h"
 #include "../../include/neurogrid_ext.h"
 
@@ -299,15 +303,79 @@ int launch_i8w(uint16_t* c, const uint16_t* a, const int8_t* b, const float* sca
 constexpr int kGvWaves = 4;
 constexpr int kGvSeg = 1024;  // codes per wave step: 64 lanes x 16
 
+// The products of one 1024-code segment in one lane: R rows of B (codes
+// bv[r]) against the lane's 16 values of each of MR rows of A (av[m]). Lanes
+// past K pass zeros in both operands: an inf activation times a zero code
+// would give NaN.
+template <int MR, int R>
+__device__ __forceinline__ void gemv_segment(float (&acc)[R][MR], u32x4 (&av)[MR][2], const u32x4 (&bv)[R],
+                                             bool kin) {
+    if (!kin) {
+#pragma unroll
+        for (int m = 0; m < MR; ++m) av[m][0] = av[m][1] = u32x4{0u, 0u, 0u, 0u};
+    }
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+        const u32x4 q = kin ? bv[r] : u32x4{0u, 0u, 0u, 0u};
+        f16x8 w0, w1;
+        codes16_to_operands(q, w0, w1);
+        const u32x4 wl = __builtin_bit_cast(u32x4, w0), wh = __builtin_bit_cast(u32x4, w1);
+#pragma unroll
+        for (int m = 0; m < MR; ++m) {
+            float s = acc[r][m];
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                s = __builtin_amdgcn_fdot2(as_f16x2(av[m][0][j]), as_f16x2(wl[j]), s, false);
+                s = __builtin_amdgcn_fdot2(as_f16x2(av[m][1][j]), as_f16x2(wh[j]), s, false);
+            }
+            acc[r][m] = s;
+        }
+    }
+}
+
+// The block's sums: output o = r * MR + m adds red[(w * V + o) * 64 + l] over
+// waves w and lanes l; kParts threads add 256 / kParts values each, then one
+// thread adds the parts, both in a fixed order; C = fp16(sum * scale).
+template <int MR, int R>
+__device__ __forceinline__ void gemv_finish(const float (&acc)[R][MR], uint16_t* __restrict__ c,
+                                            const float* __restrict__ scale, int M, int N, int n0) {
+    constexpr int V = R * MR;                 // outputs per block
+    constexpr int kParts = kGvWaves * kWave / V;  // threads that share one output in the first reduction stage
+    static_assert(kGvWaves * kWave % V == 0 && kWave % kParts == 0, "reduction shape");
+    __shared__ float red[kGvWaves * V * kWave];
+    const int tid = threadIdx.x;
+    const int lane = tid & (kWave - 1);
+    const int wave = __builtin_amdgcn_readfirstlane(tid / kWave);
+#pragma unroll
+    for (int r = 0; r < R; ++r)
+#pragma unroll
+        for (int m = 0; m < MR; ++m) red[(wave * V + r * MR + m) * kWave + lane] = acc[r][m];
+    __syncthreads();
+    const int o = tid % V;
+    const int part = tid / V;
+    constexpr int kPerPart = kGvWaves * kWave / kParts;  // values summed by one thread
+    float sum = 0.0f;
+#pragma unroll 4
+    for (int j = 0; j < kPerPart; ++j) {
+        const int idx = part * kPerPart + j;  // (wave, lane) pair
+        sum += red[((idx / kWave) * V + o) * kWave + idx % kWave];
+    }
+    __syncthreads();
+    red[o * kParts + part] = sum;
+    __syncthreads();
+    if (tid < V) {
+        float v = 0.0f;
+        for (int q = 0; q < kParts; ++q) v += red[tid * kParts + q];
+        const int r = tid / MR, m = tid % MR, n = n0 + r;
+        if (m < M && n < N) c[static_cast<size_t>(m) * N + n] = from_f32<f16>(v * scale[n]);
+    }
+}
+
 // One block of the GEMV kernels: rows blk R .. blk R + R - 1 of B.
 template <int MR, int R>
 __device__ __forceinline__ void gemv_i8w_block(uint16_t* __restrict__ c, const uint16_t* __restrict__ a,
                                                const int8_t* __restrict__ b, const float* __restrict__ scale,
                                                int M, int N, int K, int blk) {
-    constexpr int V = R * MR;                 // outputs per block
-    constexpr int kParts = kGvWaves * kWave / V;  // threads that share one output in the first reduction stage
-    static_assert(kGvWaves * kWave % V == 0 && kWave % kParts == 0, "reduction shape");
-    __shared__ float red[kGvWaves * V * kWave];
     const int tid = threadIdx.x;
     const int lane = tid & (kWave - 1);
     const int wave = __builtin_amdgcn_readfirstlane(tid / kWave);
@@ -335,57 +403,9 @@ __device__ __forceinline__ void gemv_i8w_block(uint16_t* __restrict__ c, const u
 #pragma unroll
         for (int r = 0; r < R; ++r) bv[r] = ld16_stream(b + static_cast<size_t>(min(n0 + r, N - 1)) * K + kc);
         __builtin_amdgcn_sched_barrier(0);
-        // Lanes past K zero both operands: an inf activation times a zero code
-        // would give NaN.
-        if (!kin) {
-#pragma unroll
-            for (int m = 0; m < MR; ++m) av[m][0] = av[m][1] = u32x4{0u, 0u, 0u, 0u};
-        }
-#pragma unroll
-        for (int r = 0; r < R; ++r) {
-            const u32x4 q = kin ? bv[r] : u32x4{0u, 0u, 0u, 0u};
-            f16x8 w0, w1;
-            codes16_to_operands(q, w0, w1);
-            const u32x4 wl = __builtin_bit_cast(u32x4, w0), wh = __builtin_bit_cast(u32x4, w1);
-#pragma unroll
-            for (int m = 0; m < MR; ++m) {
-                float s = acc[r][m];
-#pragma unroll
-                for (int j = 0; j < 4; ++j) {
-                    s = __builtin_amdgcn_fdot2(as_f16x2(av[m][0][j]), as_f16x2(wl[j]), s, false);
-                    s = __builtin_amdgcn_fdot2(as_f16x2(av[m][1][j]), as_f16x2(wh[j]), s, false);
-                }
-                acc[r][m] = s;
-            }
-        }
+        gemv_segment<MR, R>(acc, av, bv, kin);
     }
-
-    // Output o = r * MR + m sums red[(w * V + o) * 64 + l] over waves w and
-    // lanes l: kParts threads add 256 / kParts values each, then one thread adds
-    // the parts, both in a fixed order.
-#pragma unroll
-    for (int r = 0; r < R; ++r)
-#pragma unroll
-        for (int m = 0; m < MR; ++m) red[(wave * V + r * MR + m) * kWave + lane] = acc[r][m];
-    __syncthreads();
-    const int o = tid % V;
-    const int part = tid / V;
-    constexpr int kPerPart = kGvWaves * kWave / kParts;  // values summed by one thread
-    float sum = 0.0f;
-#pragma unroll 4
-    for (int j = 0; j < kPerPart; ++j) {
-        const int idx = part * kPerPart + j;  // (wave, lane) pair
-        sum += red[((idx / kWave) * V + o) * kWave + idx % kWave];
-    }
-    __syncthreads();
-    red[o * kParts + part] = sum;
-    __syncthreads();
-    if (tid < V) {
-        float v = 0.0f;
-        for (int q = 0; q < kParts; ++q) v += red[tid * kParts + q];
-        const int r = tid / MR, m = tid % MR, n = n0 + r;
-        if (m < M && n < N) c[static_cast<size_t>(m) * N + n] = from_f32<f16>(v * scale[n]);
-    }
+    gemv_finish<MR, R>(acc, c, scale, M, N, n0);
 }
 
 template <int MR, int R>
@@ -405,11 +425,247 @@ __global__ __launch_bounds__(kGvWaves * kWave) void gemv_i8w_shared_kernel(Share
     });
 }
 
+// RMSNorm (or residual add + RMSNorm) folded into the shared GEMV launch
+// (ng_rmsnorm_gemm_int8_shared_a, ng_add_rmsnorm_gemm_int8_shared_a), for
+// M <= 4 rows of K <= 8192. Every block normalises the rows itself, and each
+// thread normalises exactly the 16-value pieces of A that its lane multiplies
+// in the GEMV (segment sg = wave + 4 s, values 16 lane .. 16 lane + 15), so A
+// stays in registers: the thread loads its pieces of x (and the residual) and
+// of the norm weight, then its rows of B, and the row statistic (one block
+// barrier for all rows) and the scaling run while the codes are in flight.
+// Each block gets cuda_rmsnorm's (cuda_add_rmsnorm's) bits: the statistic is
+// the sum of squares rounded once to fp32 (fp64 sums resolved with their
+// error bound, else exact limb sums), which does not depend on the order of
+// summation, and the scaling is the same expression. The products are the
+// GEMV block's own segment and reduction code, so C is bit-identical too. The
+// first block of the launch stores the normalised rows (and the residual sums).
+struct NormArgs {
+    const uint16_t* x;
+    const uint16_t* res;  // residual input (ADD)
+    const uint16_t* w;    // norm weight [K]
+    uint16_t* normed;     // [M, K]
+    uint16_t* res_out;    // [M, K] (ADD)
+    float eps;
+};
+
+// Row m's exact statistic from the limb sums of the whole row, read from
+// memory by every thread of the block (the fast path's rare fallback; the
+// decision is uniform over the block).
+template <bool ADD>
+__device__ __noinline__ float norm_row_ss_exact(const NormArgs& na, int m, int K) {
+    constexpr int kT = kGvWaves * kWave;
+    __shared__ double s_limb[kGvWaves][3];
+    __shared__ int s_flag[kGvWaves];
+    const int tid = threadIdx.x, lane = tid & (kWave - 1), wid = tid / kWave;
+    const uint16_t* xr = na.x + static_cast<size_t>(m) * K;
+    const uint16_t* rr = ADD ? na.res + static_cast<size_t>(m) * K : nullptr;
+    Limbs Lm{0.0, 0.0, 0.0, 0};
+    for (int vi = tid; vi < K / 8; vi += kT) {
+        float fx[8];
+        unpack8<f16>(ld16(xr + vi * 8), fx);
+        if (ADD) {
+            float fr[8];
+            unpack8<f16>(ld16(rr + vi * 8), fr);
+#pragma unroll
+            for (int i = 0; i < 8; ++i) fx[i] = fx[i] + fr[i];
+        }
+#pragma unroll
+        for (int i = 0; i < 8; ++i) limbs_add(Lm, fx[i]);
+    }
+    double t = wave_sum_f64_dpp(Lm.t), u = wave_sum_f64_dpp(Lm.u), w = wave_sum_f64_dpp(Lm.w);
+    int bad = static_cast<int>(wave_max_u32_dpp(static_cast<uint32_t>(Lm.bad)));
+    __syncthreads();  // a previous row's readers are done with s_limb
+    if (lane == 0) {
+        s_limb[wid][0] = t;
+        s_limb[wid][1] = u;
+        s_limb[wid][2] = w;
+        s_flag[wid] = bad;
+    }
+    __syncthreads();
+    t = u = w = 0.0;
+    bad = 0;
+    for (int j = 0; j < kGvWaves; ++j) {
+        t += s_limb[j][0];
+        u += s_limb[j][1];
+        w += s_limb[j][2];
+        bad |= s_flag[j];
+    }
+    return bad ? -1.0f : limbs_to_f32(t, u, w);
+}
+
+// One block of the fused kernels: the rows of A normalised in registers, then
+// the products of the GEMV kernel's block blk (rows blk R .. blk R + R - 1 of
+// B), exactly as that block computes them. SEGS: the most 1024-value segments
+// of K one wave takes (K <= 4096 SEGS).
+template <int MR, int R, int SEGS, bool ADD>
+__device__ __forceinline__ void gemv_i8w_norm_block(uint16_t* __restrict__ c, const int8_t* __restrict__ b,
+                                                    const float* __restrict__ scale, const NormArgs& na, int M,
+                                                    int N, int K, int blk, bool store) {
+    __shared__ double s_part[kGvWaves][MR];
+    const int tid = threadIdx.x;
+    const int lane = tid & (kWave - 1);
+    const int wave = __builtin_amdgcn_readfirstlane(tid / kWave);
+    const int n0 = blk * R;
+    const int nseg = (K + kGvSeg - 1) / kGvSeg;
+
+    // Loads: the lane's pieces of x (res) and w, then its rows of B. They are
+    // issued without branches, so that waiting for the first ones does not
+    // wait for the codes: a wave with no segment s (sg >= nseg) has every lane
+    // past K, at K - 16, and its loads of that segment hit one line per row.
+    bool kin[SEGS];
+    int kc[SEGS];
+    u32x4 xv[SEGS][MR][2], rv[SEGS][MR][2], wv[SEGS][2], bv[SEGS][R];
+#pragma unroll
+    for (int s = 0; s < SEGS; ++s) {
+        const int k = (wave + s * kGvWaves) * kGvSeg + 16 * lane;
+        kin[s] = k < K;
+        kc[s] = kin[s] ? k : K - 16;
+#pragma unroll
+        for (int m = 0; m < MR; ++m) {
+            const size_t off = static_cast<size_t>(min(m, M - 1)) * K + kc[s];
+            xv[s][m][0] = ld16(na.x + off);
+            xv[s][m][1] = ld16(na.x + off + 8);
+            if (ADD) {
+                rv[s][m][0] = ld16(na.res + off);
+                rv[s][m][1] = ld16(na.res + off + 8);
+            }
+        }
+        wv[s][0] = ld16(na.w + kc[s]);
+        wv[s][1] = ld16(na.w + kc[s] + 8);
+    }
+#pragma unroll
+    for (int s = 0; s < SEGS; ++s)
+#pragma unroll
+        for (int r = 0; r < R; ++r) bv[s][r] = ld16_stream(b + static_cast<size_t>(min(n0 + r, N - 1)) * K + kc[s]);
+    __builtin_amdgcn_sched_barrier(0);
+
+    // o = x, or the rounded sum x + res; squares of x, or of the unrounded
+    // fp32 sum, as the row kernels take them. Lanes past K add nothing.
+    double ssq[MR];
+#pragma unroll
+    for (int m = 0; m < MR; ++m) ssq[m] = 0.0;
+#pragma unroll
+    for (int s = 0; s < SEGS; ++s) {
+        if (wave + s * kGvWaves >= nseg) continue;
+#pragma unroll
+        for (int m = 0; m < MR; ++m)
+#pragma unroll
+            for (int h = 0; h < 2; ++h)
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    float s0, s1;
+                    if (ADD) {
+                        s0 = el_add<f16, 0>(xv[s][m][h][i], rv[s][m][h][i]);
+                        s1 = el_add<f16, 1>(xv[s][m][h][i], rv[s][m][h][i]);
+                        xv[s][m][h][i] = pack2<f16>(s0, s1);
+                    } else {
+                        s0 = el_get<f16, 0>(xv[s][m][h][i]);
+                        s1 = el_get<f16, 1>(xv[s][m][h][i]);
+                    }
+                    const double d0 = kin[s] ? static_cast<double>(s0) : 0.0;
+                    const double d1 = kin[s] ? static_cast<double>(s1) : 0.0;
+                    ssq[m] = __builtin_fma(d0, d0, ssq[m]);
+                    ssq[m] = __builtin_fma(d1, d1, ssq[m]);
+                }
+    }
+    if (ADD && store) {
+#pragma unroll
+        for (int s = 0; s < SEGS; ++s)
+#pragma unroll
+            for (int m = 0; m < MR; ++m)
+                if (kin[s] && m < M) {
+                    uint16_t* ro = na.res_out + static_cast<size_t>(m) * K + kc[s];
+                    st16(ro, xv[s][m][0]);
+                    st16(ro + 8, xv[s][m][1]);
+                }
+    }
+#pragma unroll
+    for (int m = 0; m < MR; ++m) {
+        const double S = wave_sum_f64_dpp(ssq[m]);
+        if (lane == 0) s_part[wave][m] = S;
+    }
+    __syncthreads();
+    float rs[MR];
+#pragma unroll
+    for (int m = 0; m < MR; ++m) {
+        double S = s_part[0][m];
+        for (int j = 1; j < kGvWaves; ++j) S += s_part[j][m];
+        // Tree height: 16 SEGS terms in one lane, 6 across the wave, 3 across the waves.
+        float ss;
+        if (!ss_fast_resolve(S, 16 * SEGS + 10, ss)) {
+            const float e = norm_row_ss_exact<ADD>(na, min(m, M - 1), K);
+            if (e >= 0.0f) ss = e;
+        }
+        rs[m] = 1.0f / __builtin_sqrtf(ss / static_cast<float>(K) + na.eps);
+    }
+
+    // y = RN_f16(RN(o * r) * w): the GEMV's A, in registers.
+    float acc[R][MR];
+#pragma unroll
+    for (int r = 0; r < R; ++r)
+#pragma unroll
+        for (int m = 0; m < MR; ++m) acc[r][m] = 0.0f;
+#pragma unroll
+    for (int s = 0; s < SEGS; ++s) {
+        if (wave + s * kGvWaves >= nseg) continue;
+        u32x4 av[MR][2];
+#pragma unroll
+        for (int m = 0; m < MR; ++m)
+#pragma unroll
+            for (int h = 0; h < 2; ++h)
+#pragma unroll
+                for (int i = 0; i < 4; ++i)
+                    av[m][h][i] = pack2<f16>(el_mul<f16, 0>(wv[s][h][i], el_mul<f16, 0>(xv[s][m][h][i], rs[m])),
+                                             el_mul<f16, 1>(wv[s][h][i], el_mul<f16, 1>(xv[s][m][h][i], rs[m])));
+        if (store) {
+#pragma unroll
+            for (int m = 0; m < MR; ++m)
+                if (kin[s] && m < M) {
+                    uint16_t* yo = na.normed + static_cast<size_t>(m) * K + kc[s];
+                    st16(yo, av[m][0]);
+                    st16(yo + 8, av[m][1]);
+                }
+        }
+        gemv_segment<MR, R>(acc, av, bv[s], kin[s]);
+    }
+    gemv_finish<MR, R>(acc, c, scale, M, N, n0);
+}
+
+template <int MR, int R, int SEGS, bool ADD>
+__global__ __launch_bounds__(kGvWaves * kWave) void gemv_i8w_norm_shared_kernel(SharedSet s, NormArgs na, int M,
+                                                                                int K) {
+    shared_dispatch(s, [&](uint16_t* c, const int8_t* b, const float* scale, int n, int blk, int) {
+        gemv_i8w_norm_block<MR, R, SEGS, ADD>(c, b, scale, na, M, n, K, blk, blockIdx.x == 0);
+    });
+}
+
 template <int MR, int R>
 int launch_gemv_shared(const SharedSet& set, int blocks, const uint16_t* a, int M, int K) {
     gemv_i8w_shared_kernel<MR, R><<<dim3(static_cast<unsigned>(blocks)), dim3(kGvWaves * kWave), 0, stream()>>>(
         set, a, M, K);
     NG_CHECK_LAUNCH("ng_gemm_int8_shared_a");
+    return 0;
+}
+
+// Longest rows the fused norm kernels take: two segments per wave.
+constexpr int kNormSharedMaxK = 2 * kGvWaves * kGvSeg;
+// Most GEMV blocks of a fused norm launch. The fused kernel holds more
+// registers than the GEMV kernel (5 waves per SIMD against 8 at one row):
+// where the launch fits the GPU in about one round of blocks, folding the
+// norm in saves its launch and its latency; with more blocks the launch is
+// bound by the codes in flight, and the two calls are faster (measured on
+// MI355X at Mistral-7B: q/k/v, 768 blocks, 7.2 against 8.3 us at one token;
+// gate/up, 3584 blocks, 23.1 against 21.8 us).
+constexpr int kNormSharedMaxBlocks = 1024;
+
+template <int MR, int R, bool ADD>
+int launch_gemv_norm_shared(const SharedSet& set, int blocks, const NormArgs& na, int M, int K) {
+    const dim3 grid(static_cast<unsigned>(blocks)), block(kGvWaves * kWave);
+    if (K <= kGvWaves * kGvSeg)
+        gemv_i8w_norm_shared_kernel<MR, R, 1, ADD><<<grid, block, 0, stream()>>>(set, na, M, K);
+    else
+        gemv_i8w_norm_shared_kernel<MR, R, 2, ADD><<<grid, block, 0, stream()>>>(set, na, M, K);
+    NG_CHECK_LAUNCH(ADD ? "ng_add_rmsnorm_gemm_int8_shared_a" : "ng_rmsnorm_gemm_int8_shared_a");
     return 0;
 }
 
@@ -1704,4 +1960,88 @@ extern "C" int ng_gemm_int8_shared_a(int count, void* const* c, const void* a, c
         if (r != 0) return r;
     }
     return 0;
+}
+
+// [p, p + pn) and [q, q + qn) share a byte.
+static bool overlaps(const void* p, size_t pn, const void* q, size_t qn) {
+    const auto a = reinterpret_cast<uintptr_t>(p), b = reinterpret_cast<uintptr_t>(q);
+    return a < b + qn && b < a + pn;
+}
+
+// RMSNorm (ADD: residual add + RMSNorm) of A, then the products that share
+// the normalised A: one launch of gemv_i8w_norm_shared_kernel when every
+// product takes the same GEMV shape, K <= 8192, the launch has at most
+// kNormSharedMaxBlocks blocks and no output overlaps an input (the kernel's
+// blocks read the inputs while the first one stores); otherwise the norm
+// entry point followed by ng_gemm_int8_shared_a.
+// The same bits either way.
+template <bool ADD>
+static int norm_shared(const char* name, int count, void* normed, void* res_out, void* const* c, const void* x,
+                       const void* res, const void* w, float eps, const void* const* b, const void* const* scales,
+                       const int* n, int M, int K) {
+    NG_REQUIRE(normed && x && w && c && b && scales && n && (!ADD || (res && res_out)), "%s: null pointer", name);
+    NG_REQUIRE(count >= 1 && count <= kMaxShared, "%s: count=%d must be in [1, %d]", name, count, kMaxShared);
+    NG_REQUIRE(M > 0 && K > 0, "%s: M=%d K=%d must be > 0", name, M, K);
+    const size_t rows = static_cast<size_t>(M) * K * 2;
+    int path = -1;
+    const size_t wb = static_cast<size_t>(K) * 2;
+    // Nothing the blocks read may share a byte with what the first block
+    // writes (normed, residual_out) or what any block writes (c).
+    const auto clear_of_writes = [&](const void* p, size_t pn) {
+        return !overlaps(p, pn, normed, rows) && (!ADD || !overlaps(p, pn, res_out, rows));
+    };
+    bool apart = clear_of_writes(x, rows) && clear_of_writes(w, wb) &&
+                 (!ADD || (clear_of_writes(res, rows) && !overlaps(res_out, rows, normed, rows)));
+    for (int i = 0; i < count; ++i) {
+        NG_REQUIRE(c[i] && b[i] && scales[i], "%s: null pointer in product %d", name, i);
+        NG_REQUIRE(n[i] > 0, "%s: n[%d]=%d must be > 0", name, i, n[i]);
+        const int pi = use_i8w(normed, b[i], M, K, n[i], true) ? gemv_shape(M, K, n[i]) : 0;
+        path = (path == -1 || path == pi) ? pi : 0;
+        const size_t cb = static_cast<size_t>(M) * n[i] * 2;
+        apart = apart && clear_of_writes(b[i], static_cast<size_t>(n[i]) * K) &&
+                clear_of_writes(scales[i], static_cast<size_t>(n[i]) * 4) && clear_of_writes(c[i], cb) &&
+                !overlaps(c[i], cb, x, rows) && !overlaps(c[i], cb, w, wb) && (!ADD || !overlaps(c[i], cb, res, rows));
+    }
+    // GEMV blocks of the fused launch (rows of B per block as the GEMV kernel's).
+    const int R = path == 3 ? 4 : 8;
+    long long blocks = 0;
+    for (int i = 0; i < count; ++i) blocks += (n[i] + R - 1) / R;
+    const bool fused = path >= 1 && apart && K <= kNormSharedMaxK && blocks <= kNormSharedMaxBlocks && aligned16(x) &&
+                       aligned16(w) && aligned16(normed) && (!ADD || (aligned16(res) && aligned16(res_out)));
+    if (!fused) {
+        const int r = ADD ? cuda_add_rmsnorm(normed, res_out, x, res, w, M, K, eps) : cuda_rmsnorm(normed, x, w, M, K, eps);
+        if (r != 0) return r;
+        return ng_gemm_int8_shared_a(count, c, normed, b, scales, n, M, K);
+    }
+    SharedSet set{};
+    int first = 0;
+    for (int i = 0; i < kMaxShared; ++i) {
+        const int j = i < count ? i : 0;  // unused slots repeat product 0 and are never selected
+        set.c[i] = static_cast<uint16_t*>(c[j]);
+        set.b[i] = static_cast<const int8_t*>(b[j]);
+        set.scale[i] = static_cast<const float*>(scales[j]);
+        set.n[i] = n[j];
+        set.first[i] = i < count ? first : INT_MAX;
+        if (i < count) first += (n[i] + R - 1) / R;
+    }
+    const NormArgs na{static_cast<const uint16_t*>(x), static_cast<const uint16_t*>(res), static_cast<const uint16_t*>(w),
+                      static_cast<uint16_t*>(normed), static_cast<uint16_t*>(res_out), eps};
+    if (path == 1) return launch_gemv_norm_shared<1, 8, ADD>(set, first, na, M, K);
+    if (path == 2) return launch_gemv_norm_shared<2, 8, ADD>(set, first, na, M, K);
+    return launch_gemv_norm_shared<4, 4, ADD>(set, first, na, M, K);
+}
+
+extern "C" int ng_rmsnorm_gemm_int8_shared_a(int count, void* normed, void* const* c, const void* x,
+                                             const void* norm_weight, float eps, const void* const* b,
+                                             const void* const* scales, const int* n, int M, int K) {
+    return norm_shared<false>("ng_rmsnorm_gemm_int8_shared_a", count, normed, nullptr, c, x, nullptr, norm_weight, eps,
+                              b, scales, n, M, K);
+}
+
+extern "C" int ng_add_rmsnorm_gemm_int8_shared_a(int count, void* normed, void* residual_out, void* const* c,
+                                                 const void* x, const void* residual_in, const void* norm_weight,
+                                                 float eps, const void* const* b, const void* const* scales,
+                                                 const int* n, int M, int K) {
+    return norm_shared<true>("ng_add_rmsnorm_gemm_int8_shared_a", count, normed, residual_out, c, x, residual_in,
+                             norm_weight, eps, b, scales, n, M, K);
 }

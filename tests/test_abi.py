@@ -106,6 +106,14 @@ def test_argument_errors_return_minus_one_without_touching_the_gpu(capfd):
     assert L.ng_gemm_int8_shared_a(2, pv, p, pn, pv, nv, 1, 64) == -1    # null weights of product 1
     assert L.ng_gemm_int8_shared_a(2, pv, p, pv, pv, nv, 1, 64) == -1    # n[1] == 0
     assert L.ng_gemm_int8_shared_a(1, None, p, pv, pv, nv, 1, 64) == -1
+    e = C.c_float(1e-5)
+    assert L.ng_rmsnorm_gemm_int8_shared_a(0, p, pv, p, p, e, pv, pv, nv, 1, 64) == -1   # count outside 1..4
+    assert L.ng_rmsnorm_gemm_int8_shared_a(1, None, pv, p, p, e, pv, pv, nv, 1, 64) == -1  # null normed
+    assert L.ng_rmsnorm_gemm_int8_shared_a(2, p, pv, p, p, e, pv, pv, nv, 1, 64) == -1   # n[1] == 0
+    assert L.ng_rmsnorm_gemm_int8_shared_a(1, p, pv, p, p, e, pv, pv, nv, 0, 64) == -1   # M == 0
+    assert L.ng_add_rmsnorm_gemm_int8_shared_a(1, p, None, pv, p, p, p, e, pv, pv, nv, 1, 64) == -1  # null residual_out
+    assert L.ng_add_rmsnorm_gemm_int8_shared_a(2, p, p, pv, p, p, p, e, pn, pv, nv, 1, 64) == -1  # null weights of product 1
+    assert L.ng_add_rmsnorm_gemm_int8_shared_a(5, p, p, pv, p, p, p, e, pv, pv, nv, 1, 64) == -1
     err = capfd.readouterr().err
     assert "neurogrid-amd:" in err and "null pointer" in err
 

@@ -196,6 +196,23 @@ def _ops():
         lambda L, i, o: L.ng_gemm_int8_shared_a(
             2, (C.c_void_p * 2)(o["y"].ptr, o["y2"].ptr), i["a1"].vp, (C.c_void_p * 2)(i["wq"].ptr, i["wq_wide"].ptr),
             (C.c_void_p * 2)(i["wsc"].ptr, i["wsc_wide"].ptr), (C.c_int * 2)(GN, GNW), 1, GK))
+    # RMSNorm (add + RMSNorm) folded into the shared GEMV launch (M = 2, 1), and
+    # a set with more GEMV blocks than the fused launch takes: the two calls
+    add("ng_rmsnorm_gemm_int8_shared_a_M2", {"n": (E2, (2, GK)), "y": (E2, (2, GN)), "y2": (E2, (2, GN))},
+        lambda L, i, o: L.ng_rmsnorm_gemm_int8_shared_a(
+            2, o["n"].vp, (C.c_void_p * 2)(o["y"].ptr, o["y2"].ptr), i["xh"].vp, i["wh"].vp, EPS,
+            (C.c_void_p * 2)(i["wq"].ptr, i["wq"].ptr), (C.c_void_p * 2)(i["wsc"].ptr, i["wsc"].ptr),
+            (C.c_int * 2)(GN, GN), 2, GK))
+    add("ng_add_rmsnorm_gemm_int8_shared_a_M1", {"n": (E2, (1, GK)), "ro": (E2, (1, GK)), "y": (E2, (1, GN))},
+        lambda L, i, o: L.ng_add_rmsnorm_gemm_int8_shared_a(
+            1, o["n"].vp, o["ro"].vp, (C.c_void_p * 1)(o["y"].ptr), i["xh"].vp, i["rh"].vp, i["wh"].vp, EPS,
+            (C.c_void_p * 1)(i["wq"].ptr), (C.c_void_p * 1)(i["wsc"].ptr), (C.c_int * 1)(GN), 1, GK))
+    add("ng_add_rmsnorm_gemm_int8_shared_a_M1_two_calls",
+        {"n": (E2, (1, GK)), "ro": (E2, (1, GK)), "y": (E2, (1, GN)), "y2": (E2, (1, GNW))},
+        lambda L, i, o: L.ng_add_rmsnorm_gemm_int8_shared_a(
+            2, o["n"].vp, o["ro"].vp, (C.c_void_p * 2)(o["y"].ptr, o["y2"].ptr), i["xh"].vp, i["rh"].vp, i["wh"].vp,
+            EPS, (C.c_void_p * 2)(i["wq"].ptr, i["wq_wide"].ptr), (C.c_void_p * 2)(i["wsc"].ptr, i["wsc_wide"].ptr),
+            (C.c_int * 2)(GN, GNW), 1, GK))
     # from 4096 rows of A on: B dequantized into the stream's fp16 buffer, then hipBLASLt
     add("cuda_gemm_int8_M4096_library", {"y": (E2, (4096, GN))},
         lambda L, i, o: L.cuda_gemm_int8(o["y"].vp, i["a4096"].vp, i["wq"].vp, i["wsc"].vp, 4096, GK, GN, True),
