@@ -671,6 +671,7 @@ def extra_kernels(L, hip, stream):
     out["gemm_int8"] = gemm_extras(L, hip, stream)
     out["gemm_int8_shared_a"] = sh = shared_a_extras(L, hip, stream)
     out["norm_gemm_int8_shared_a"] = norm_shared_extras(L, hip, stream)
+    out["gemm_int8_silu_mul"] = silu_mul_gemm_extras(L, hip, stream)
     g = out["gemm_int8"]
     g["mistral7b_layer_M1"]["shared_a_us"] = (sh["qkv_M1"]["us"] + g["q_proj_M1"]["us"] + sh["gate_up_M1"]["us"]
                                               + g["down_proj_M1"]["us"])
@@ -883,6 +884,50 @@ def norm_shared_extras(L, hip, stream):
             wp.free()
             sc.free()
     w.free()
+    return out
+
+
+def silu_mul_gemm_extras(L, hip, stream, K=4096, N=14336):
+    """Mistral-7B's gate/up projections and SwiGLU (layer.cu:575-588) at M = 1,
+    2 and 4 tokens. us: ng_gemm_int8_silu_mul (one launch where both products
+    take the GEMV kernel, M <= 2 here); two_calls_us: ng_gemm_int8_shared_a,
+    then cuda_silu_mul. Both give the same bits; weight pools keep the codes
+    cache-cold."""
+    rng = np.random.Generator(np.random.PCG64(8))
+    n = pool_slots(2 * N * K)
+    pools = []
+    for _ in range(2):
+        wq = rng.integers(-128, 128, (N, K)).astype(np.int8)
+        pools.append((Pool(hip, wq.nbytes, n, wq), DB.from_array(rng.uniform(1e-3, 1e-2, N).astype(np.float32))))
+        del wq
+    (gp, gs), (up_, us_) = pools
+    out = {}
+    for M in (1, 2, 4):
+        ab = DB.from_array(W.round_to(rng.standard_normal((M, K), dtype=np.float32), "f16"))
+        gb, ub, ob = (Pool(hip, 2 * M * N, n) for _ in range(3))
+        scv = (C.c_void_p * 2)(gs.ptr, us_.ptr)
+        nv = (C.c_int * 2)(N, N)
+
+        def one(j, M=M, ab=ab, gb=gb, ub=ub, ob=ob):
+            return L.ng_gemm_int8_silu_mul(ob.at(j), gb.at(j), ub.at(j), ab.vp, gp.at(j), gs.vp, up_.at(j), us_.vp,
+                                           M, K, N)
+
+        def two(j, M=M, ab=ab, gb=gb, ub=ub, ob=ob):
+            rc = L.ng_gemm_int8_shared_a(2, (C.c_void_p * 2)(gb.at(j), ub.at(j)), ab.vp,
+                                         (C.c_void_p * 2)(gp.at(j), up_.at(j)), scv, nv, M, K)
+            return rc or L.cuda_silu_mul(ob.at(j), gb.at(j), ub.at(j), M * N)
+
+        us_two = time_pool_kernel(hip, stream, [("two_calls", (lambda j=j: two(j))) for j in range(n)])
+        us_one = time_pool_kernel(hip, stream, [("fused", (lambda j=j: one(j))) for j in range(n)])
+        b = 2 * (N * K + 4 * N) + 2 * M * K + 3 * 2 * M * N
+        out[f"gate_up_silu_mul_M{M}"] = {"us": us_one, "two_calls_us": us_two, "GBps": b / us_one / 1e3,
+                                         "frac": b / us_one / 1e3 / PEAK_GBPS, "bytes": b, "buffer_sets": n}
+        for x in (gb, ub, ob):
+            x.free()
+        ab.free()
+    for p, s in pools:
+        p.free()
+        s.free()
     return out
 
 
@@ -1460,7 +1505,8 @@ def main():
     if args.gemm_only:
         print(json.dumps({"gemm_int8": gemm_extras(L, hip, stream),
                           "gemm_int8_shared_a": shared_a_extras(L, hip, stream),
-                          "norm_gemm_int8_shared_a": norm_shared_extras(L, hip, stream)}), flush=True)
+                          "norm_gemm_int8_shared_a": norm_shared_extras(L, hip, stream),
+                          "gemm_int8_silu_mul": silu_mul_gemm_extras(L, hip, stream)}), flush=True)
         return
     if args.floors_only:
         print(json.dumps({"floors": floor_extras(hip, stream)}), flush=True)

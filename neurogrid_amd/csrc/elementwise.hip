@@ -19,17 +19,12 @@ namespace ng {
 
 enum EwOp : int { EW_ADD = 0, EW_MUL = 1, EW_SILU = 2, EW_SILU_MUL = 3, EW_SCALE = 4 };
 
-__device__ __forceinline__ float sigmoid_fast(float x) {
-    const float e = __builtin_amdgcn_exp2f(-x * 1.4426950408889634f);
-    return __builtin_amdgcn_rcpf(1.0f + e);
-}
-
 template <int OP>
 __device__ __forceinline__ float ew_apply(float a, float b, float s) {
     if (OP == EW_ADD) return a + b;
     if (OP == EW_MUL) return a * b;
     if (OP == EW_SILU) return a * sigmoid_fast(a);
-    if (OP == EW_SILU_MUL) return (a * sigmoid_fast(a)) * b;
+    if (OP == EW_SILU_MUL) return swiglu_f32(a, b);
     return a * s;  // EW_SCALE
 }
 

@@ -335,10 +335,10 @@ __device__ __forceinline__ void gemv_segment(float (&acc)[R][MR], u32x4 (&av)[MR
 
 // The block's sums: output o = r * MR + m adds red[(w * V + o) * 64 + l] over
 // waves w and lanes l; kParts threads add 256 / kParts values each, then one
-// thread adds the parts, both in a fixed order; C = fp16(sum * scale).
+// thread adds the parts, both in a fixed order. Thread o < V returns output
+// o's sum (others 0). The reduction buffer is free again after a barrier.
 template <int MR, int R>
-__device__ __forceinline__ void gemv_finish(const float (&acc)[R][MR], uint16_t* __restrict__ c,
-                                            const float* __restrict__ scale, int M, int N, int n0) {
+__device__ __forceinline__ float gemv_reduce(const float (&acc)[R][MR]) {
     constexpr int V = R * MR;                 // outputs per block
     constexpr int kParts = kGvWaves * kWave / V;  // threads that share one output in the first reduction stage
     static_assert(kGvWaves * kWave % V == 0 && kWave % kParts == 0, "reduction shape");
@@ -363,9 +363,19 @@ __device__ __forceinline__ void gemv_finish(const float (&acc)[R][MR], uint16_t*
     __syncthreads();
     red[o * kParts + part] = sum;
     __syncthreads();
-    if (tid < V) {
-        float v = 0.0f;
+    float v = 0.0f;
+    if (tid < V)
         for (int q = 0; q < kParts; ++q) v += red[tid * kParts + q];
+    return v;
+}
+
+// C = fp16(sum * scale) for the block's rows n0 .. n0 + R - 1 of B.
+template <int MR, int R>
+__device__ __forceinline__ void gemv_finish(const float (&acc)[R][MR], uint16_t* __restrict__ c,
+                                            const float* __restrict__ scale, int M, int N, int n0) {
+    const float v = gemv_reduce<MR, R>(acc);
+    const int tid = threadIdx.x;
+    if (tid < R * MR) {
         const int r = tid / MR, m = tid % MR, n = n0 + r;
         if (m < M && n < N) c[static_cast<size_t>(m) * N + n] = from_f32<f16>(v * scale[n]);
     }
@@ -423,6 +433,72 @@ __global__ __launch_bounds__(kGvWaves * kWave) void gemv_i8w_shared_kernel(Share
     shared_dispatch(s, [&](uint16_t* c, const int8_t* b, const float* scale, int n, int blk, int) {
         gemv_i8w_block<MR, R>(c, a, b, scale, M, n, K, blk);
     });
+}
+
+// gate/up and SwiGLU in one launch (ng_gemm_int8_silu_mul): block blk runs
+// the GEMV kernel's block blk of the gate product and of the up product (the
+// same R rows of each, both against one load of A), reduces each exactly as
+// that block does, and writes gate = fp16(sum * scale), up likewise, and
+// out = fp16(silu(gate) * up) with the element-wise kernel's expression. out
+// may be gate or up itself: each element is written by one thread, out last.
+struct SwigluArgs {
+    uint16_t* out;
+    uint16_t* gate;
+    uint16_t* up;
+    const int8_t* bg;
+    const int8_t* bu;
+    const float* sg;
+    const float* su;
+};
+
+template <int MR, int R>
+__global__ __launch_bounds__(kGvWaves * kWave) void gemv_i8w_swiglu_kernel(SwigluArgs sa, const uint16_t* __restrict__ a,
+                                                                           int M, int N, int K) {
+    const int tid = threadIdx.x;
+    const int lane = tid & (kWave - 1);
+    const int wave = __builtin_amdgcn_readfirstlane(tid / kWave);
+    const int n0 = blockIdx.x * R;
+    const int nseg = (K + kGvSeg - 1) / kGvSeg;
+    float accg[R][MR], accu[R][MR];
+#pragma unroll
+    for (int r = 0; r < R; ++r)
+#pragma unroll
+        for (int m = 0; m < MR; ++m) accg[r][m] = accu[r][m] = 0.0f;
+    for (int sg = wave; sg < nseg; sg += kGvWaves) {
+        const int k = sg * kGvSeg + 16 * lane;
+        const bool kin = k < K;
+        const int kc = kin ? k : K - 16;
+        u32x4 av[MR][2];
+#pragma unroll
+        for (int m = 0; m < MR; ++m) {
+            const uint16_t* ar = a + static_cast<size_t>(min(m, M - 1)) * K + kc;
+            av[m][0] = ld16(ar);
+            av[m][1] = ld16(ar + 8);
+        }
+        u32x4 bvg[R], bvu[R];
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            const size_t row = static_cast<size_t>(min(n0 + r, N - 1)) * K + kc;
+            bvg[r] = ld16_stream(sa.bg + row);
+            bvu[r] = ld16_stream(sa.bu + row);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+        gemv_segment<MR, R>(accg, av, bvg, kin);
+        gemv_segment<MR, R>(accu, av, bvu, kin);
+    }
+    const float vg = gemv_reduce<MR, R>(accg);
+    __syncthreads();  // the reduction buffer is reused
+    const float vu = gemv_reduce<MR, R>(accu);
+    if (tid < R * MR) {
+        const int r = tid / MR, m = tid % MR, n = n0 + r;
+        if (m < M && n < N) {
+            const size_t o = static_cast<size_t>(m) * N + n;
+            const uint16_t g = from_f32<f16>(vg * sa.sg[n]), u = from_f32<f16>(vu * sa.su[n]);
+            sa.gate[o] = g;
+            sa.up[o] = u;
+            sa.out[o] = from_f32<f16>(swiglu_f32(to_f32<f16>(g), to_f32<f16>(u)));
+        }
+    }
 }
 
 // RMSNorm (or residual add + RMSNorm) folded into the shared GEMV launch
@@ -2044,4 +2120,47 @@ extern "C" int ng_add_rmsnorm_gemm_int8_shared_a(int count, void* normed, void* 
                                                  const int* n, int M, int K) {
     return norm_shared<true>("ng_add_rmsnorm_gemm_int8_shared_a", count, normed, residual_out, c, x, residual_in,
                              norm_weight, eps, b, scales, n, M, K);
+}
+
+// gate/up (cuda_gemm_int8 on one A, as ng_gemm_int8_shared_a) and SwiGLU
+// (cuda_silu_mul): one launch of gemv_i8w_swiglu_kernel when both products
+// take the GEMV kernel and no output overlaps an input or another output
+// (out may be gate or up exactly); otherwise the two calls. The same bits
+// either way.
+extern "C" int ng_gemm_int8_silu_mul(void* out, void* gate, void* up, const void* a, const void* b_gate,
+                                     const void* scale_gate, const void* b_up, const void* scale_up, int M, int K,
+                                     int N) {
+    NG_REQUIRE(out && gate && up && a && b_gate && scale_gate && b_up && scale_up, "ng_gemm_int8_silu_mul: null pointer");
+    NG_REQUIRE(M > 0 && K > 0 && N > 0, "ng_gemm_int8_silu_mul: M=%d K=%d N=%d must be > 0", M, K, N);
+    const size_t cb = static_cast<size_t>(M) * N * 2, ab = static_cast<size_t>(M) * K * 2;
+    const size_t bb = static_cast<size_t>(N) * K, sb = static_cast<size_t>(N) * 4;
+    const int path = use_i8w(a, b_gate, M, K, N, true) && use_i8w(a, b_up, M, K, N, true) ? gemv_shape(M, K, N) : 0;
+    bool apart = !overlaps(gate, cb, up, cb) && (out == gate || out == up || (!overlaps(out, cb, gate, cb) &&
+                                                                              !overlaps(out, cb, up, cb)));
+    for (const void* o : {out, gate, up})
+        apart = apart && !overlaps(o, cb, a, ab) && !overlaps(o, cb, b_gate, bb) && !overlaps(o, cb, b_up, bb) &&
+                !overlaps(o, cb, scale_gate, sb) && !overlaps(o, cb, scale_up, sb);
+    if (path < 1 || !apart) {
+        void* c[2] = {gate, up};
+        const void* b[2] = {b_gate, b_up};
+        const void* sc[2] = {scale_gate, scale_up};
+        const int n[2] = {N, N};
+        const int r = ng_gemm_int8_shared_a(2, c, a, b, sc, n, M, K);
+        if (r != 0) return r;
+        return cuda_silu_mul(out, gate, up, static_cast<size_t>(M) * N);
+    }
+    const SwigluArgs sa{static_cast<uint16_t*>(out), static_cast<uint16_t*>(gate), static_cast<uint16_t*>(up),
+                        static_cast<const int8_t*>(b_gate), static_cast<const int8_t*>(b_up),
+                        static_cast<const float*>(scale_gate), static_cast<const float*>(scale_up)};
+    const auto ap = static_cast<const uint16_t*>(a);
+    const dim3 block(kGvWaves * kWave);
+    if (path == 3) {
+        gemv_i8w_swiglu_kernel<4, 4><<<dim3(static_cast<unsigned>((N + 3) / 4)), block, 0, stream()>>>(sa, ap, M, N, K);
+    } else if (path == 2) {
+        gemv_i8w_swiglu_kernel<2, 8><<<dim3(static_cast<unsigned>((N + 7) / 8)), block, 0, stream()>>>(sa, ap, M, N, K);
+    } else {
+        gemv_i8w_swiglu_kernel<1, 8><<<dim3(static_cast<unsigned>((N + 7) / 8)), block, 0, stream()>>>(sa, ap, M, N, K);
+    }
+    NG_CHECK_LAUNCH("ng_gemm_int8_silu_mul");
+    return 0;
 }

@@ -149,6 +149,17 @@ __device__ __forceinline__ u32x4 pack8(const float (&f)[8]) {
     return v;
 }
 
+// sig(x) = 1 / (1 + exp(-x)) with the hardware exp2 and reciprocal
+// (v_exp_f32 / v_rcp_f32: a few fp32 ulp, far below half an ulp of a 16-bit
+// result), and SwiGLU's element silu(g) * u = (g * sig(g)) * u in fp32. The
+// element-wise kernels and the GEMV's SwiGLU epilogue share these, so both
+// round the same fp32 value.
+__device__ __forceinline__ float sigmoid_fast(float x) {
+    const float e = __builtin_amdgcn_exp2f(-x * 1.4426950408889634f);
+    return __builtin_amdgcn_rcpf(1.0f + e);
+}
+__device__ __forceinline__ float swiglu_f32(float g, float u) { return (g * sigmoid_fast(g)) * u; }
+
 __device__ __forceinline__ uint16_t lane16(const u32x4 v, int i) {
     return static_cast<uint16_t>((v[i >> 1] >> ((i & 1) * 16)) & 0xffffu);
 }

@@ -213,6 +213,13 @@ def _ops():
             2, o["n"].vp, o["ro"].vp, (C.c_void_p * 2)(o["y"].ptr, o["y2"].ptr), i["xh"].vp, i["rh"].vp, i["wh"].vp,
             EPS, (C.c_void_p * 2)(i["wq"].ptr, i["wq_wide"].ptr), (C.c_void_p * 2)(i["wsc"].ptr, i["wsc_wide"].ptr),
             (C.c_int * 2)(GN, GNW), 1, GK))
+    # gate/up and SwiGLU: one launch at M = 1 (in place on gate), the two calls at M = 16
+    add("ng_gemm_int8_silu_mul_M1", {"g": (E2, (1, GN)), "u": (E2, (1, GN))},
+        lambda L, i, o: L.ng_gemm_int8_silu_mul(o["g"].vp, o["g"].vp, o["u"].vp, i["a1"].vp, i["wq"].vp, i["wsc"].vp,
+                                                i["wq"].vp, i["wsc"].vp, 1, GK, GN))
+    add("ng_gemm_int8_silu_mul_M16", {"o": (E2, (16, GN)), "g": (E2, (16, GN)), "u": (E2, (16, GN))},
+        lambda L, i, o: L.ng_gemm_int8_silu_mul(o["o"].vp, o["g"].vp, o["u"].vp, i["a16"].vp, i["wq"].vp, i["wsc"].vp,
+                                                i["wq"].vp, i["wsc"].vp, 16, GK, GN))
     # from 4096 rows of A on: B dequantized into the stream's fp16 buffer, then hipBLASLt
     add("cuda_gemm_int8_M4096_library", {"y": (E2, (4096, GN))},
         lambda L, i, o: L.cuda_gemm_int8(o["y"].vp, i["a4096"].vp, i["wq"].vp, i["wsc"].vp, 4096, GK, GN, True),

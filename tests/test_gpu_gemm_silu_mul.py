@@ -1,0 +1,101 @@
+"""ng_gemm_int8_silu_mul on the GPU: gate/up and SwiGLU in one call.
+
+Bar: out, gate and up are bit-identical to the calls they replace,
+ng_gemm_int8_shared_a (gate and up on one A, each bit for bit its own
+cuda_gemm_int8) and then cuda_silu_mul(out, gate, up), on the same inputs:
+in the fused launch (both products on the GEMV kernel, M <= 4) and where the
+call is the two calls (M > 4, M = 3-4 with N >= 8192, K not a multiple of
+16), with out apart from gate and up or in place on either, as the engine
+runs SwiGLU in place on gate (layer.cu:585-588).
+"""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+from gpu_util import C, assert_bits_equal, banner, dev, empty, get, ok
+
+pytestmark = pytest.mark.gpu
+
+RNG = np.random.Generator(np.random.PCG64(71))
+
+# (M, K, N): Mistral-7B and Llama-2-7B gate/up at 1-2 tokens, M = 3-4 below
+# N = 8192, ragged N and K (K % 1024 != 0), tiny shapes; then shapes that are
+# the two calls.
+FUSED = [(1, 4096, 14336), (2, 4096, 14336), (1, 4096, 11008), (2, 5120, 13824), (3, 4096, 4096), (4, 2048, 5000),
+         (1, 4112, 1000), (3, 2064, 17), (1, 16, 5)]
+TWO_CALLS = [(4, 4096, 14336), (8, 4096, 14336), (1, 4104, 64), (40, 1024, 2048)]
+
+
+def f16bits(x) -> np.ndarray:
+    return np.asarray(x, np.float32).astype(np.float16).view(np.uint16)
+
+
+def problem(M, K, N, big=False):
+    a = f16bits(RNG.standard_normal((M, K)) * (8 if big else 1))
+    bg = RNG.integers(-128, 128, size=(N, K)).astype(np.int8)
+    bu = RNG.integers(-128, 128, size=(N, K)).astype(np.int8)
+    sg = RNG.uniform(1e-3, 1e-2, N).astype(np.float16).astype(np.float32)
+    su = RNG.uniform(1e-3, 1e-2, N).astype(np.float16).astype(np.float32)
+    return a, bg, bu, sg, su
+
+
+def run(lib, a, bg, bu, sg, su, fused: bool, alias: str = ""):
+    M, K = a.shape
+    N = bg.shape[0]
+    ab, bgb, bub, sgb, sub = dev(a), dev(bg), dev(bu), dev(sg), dev(su)
+    gb, ub = empty(M * N * 2), empty(M * N * 2)
+    ob = gb if alias == "gate" else ub if alias == "up" else empty(M * N * 2)
+    if fused:
+        ok(lib.ng_gemm_int8_silu_mul(ob.vp, gb.vp, ub.vp, ab.vp, bgb.vp, sgb.vp, bub.vp, sub.vp, M, K, N),
+           "ng_gemm_int8_silu_mul")
+    else:
+        cnt = 2
+        ok(lib.ng_gemm_int8_shared_a(cnt, (C.c_void_p * 2)(gb.ptr, ub.ptr), ab.vp, (C.c_void_p * 2)(bgb.ptr, bub.ptr),
+                                     (C.c_void_p * 2)(sgb.ptr, sub.ptr), (C.c_int * 2)(N, N), M, K),
+           "ng_gemm_int8_shared_a")
+        ok(lib.cuda_silu_mul(ob.vp, gb.vp, ub.vp, M * N), "cuda_silu_mul")
+    out = {"out": get(ob, np.uint16, (M, N))}
+    if alias != "gate":
+        out["gate"] = get(gb, np.uint16, (M, N))
+    if alias != "up":
+        out["up"] = get(ub, np.uint16, (M, N))
+    return out
+
+
+def check(got, want):
+    assert got.keys() == want.keys()
+    for k in want:
+        assert_bits_equal(got[k], want[k], k)
+
+
+@pytest.mark.parametrize("M,K,N", FUSED + TWO_CALLS)
+def test_silu_mul_is_the_two_calls(lib, M, K, N):
+    banner(f"gemm_int8_silu_mul M={M} K={K} N={N}")
+    p = problem(M, K, N)
+    check(run(lib, *p, fused=True), run(lib, *p, fused=False))
+
+
+@pytest.mark.parametrize("alias", ["gate", "up"])
+@pytest.mark.parametrize("M,K,N", [(1, 4096, 14336), (2, 4112, 1000), (8, 1024, 2048)])
+def test_silu_mul_in_place(lib, M, K, N, alias):
+    banner(f"gemm_int8_silu_mul in place on {alias} M={M} K={K} N={N}")
+    p = problem(M, K, N)
+    check(run(lib, *p, fused=True, alias=alias), run(lib, *p, fused=False, alias=alias))
+
+
+def test_silu_mul_large_and_nonfinite(lib):
+    """Large activations (gate values that overflow fp16 to inf, sig at its
+    limits) and inf / NaN in A: the same bits as the two calls."""
+    banner("gemm_int8_silu_mul large and non-finite")
+    a, bg, bu, sg, su = problem(2, 4096, 4096, big=True)
+    a[0, 5] = 0x7C00
+    a[1, 77] = 0x7E00
+    check(run(lib, a, bg, bu, sg, su, fused=True), run(lib, a, bg, bu, sg, su, fused=False))
+
+
+def test_silu_mul_consecutive_calls(lib):
+    banner("gemm_int8_silu_mul: a call, then a smaller one")
+    for M, K, N in ((2, 4096, 14336), (1, 2048, 300)):
+        p = problem(M, K, N)
+        check(run(lib, *p, fused=True), run(lib, *p, fused=False))
