@@ -672,6 +672,7 @@ def extra_kernels(L, hip, stream):
     out["gemm_int8_shared_a"] = sh = shared_a_extras(L, hip, stream)
     out["norm_gemm_int8_shared_a"] = norm_shared_extras(L, hip, stream)
     out["gemm_int8_silu_mul"] = silu_mul_gemm_extras(L, hip, stream)
+    out["gemm_int8_add"] = gemm_add_extras(L, hip, stream)
     g = out["gemm_int8"]
     g["mistral7b_layer_M1"]["shared_a_us"] = (sh["qkv_M1"]["us"] + g["q_proj_M1"]["us"] + sh["gate_up_M1"]["us"]
                                               + g["down_proj_M1"]["us"])
@@ -928,6 +929,45 @@ def silu_mul_gemm_extras(L, hip, stream, K=4096, N=14336):
     for p, s in pools:
         p.free()
         s.free()
+    return out
+
+
+def gemm_add_extras(L, hip, stream, K=14336, N=4096):
+    """Mistral-7B's down projection and the layer's final residual add
+    (layer.cu:593-598) at M = 1, 2 and 4 tokens. us: ng_gemm_int8_add (one
+    launch on the GEMV kernel's shapes, M <= 2 here); two_calls_us:
+    cuda_gemm_int8, then cuda_add. Both give the same bits; weight pools keep
+    the codes cache-cold."""
+    rng = np.random.Generator(np.random.PCG64(9))
+    n = pool_slots(N * K)
+    wq = rng.integers(-128, 128, (N, K)).astype(np.int8)
+    wp = Pool(hip, wq.nbytes, n, wq)
+    del wq
+    sc = DB.from_array(rng.uniform(1e-3, 1e-2, N).astype(np.float32))
+    out = {}
+    for M in (1, 2, 4):
+        ab = DB.from_array(W.round_to(rng.standard_normal((M, K), dtype=np.float32), "f16"))
+        rb = DB.from_array(W.round_to(rng.standard_normal((M, N), dtype=np.float32), "f16"))
+        cb, ob = Pool(hip, 2 * M * N, n), Pool(hip, 2 * M * N, n)
+
+        def one(j, M=M, ab=ab, rb=rb, cb=cb, ob=ob):
+            return L.ng_gemm_int8_add(ob.at(j), cb.at(j), ab.vp, wp.at(j), sc.vp, rb.vp, M, K, N)
+
+        def two(j, M=M, ab=ab, rb=rb, cb=cb, ob=ob):
+            return (L.cuda_gemm_int8(cb.at(j), ab.vp, wp.at(j), sc.vp, M, K, N, True)
+                    or L.cuda_add(ob.at(j), cb.at(j), rb.vp, M * N))
+
+        us_two = time_pool_kernel(hip, stream, [("two_calls", (lambda j=j: two(j))) for j in range(n)])
+        us_one = time_pool_kernel(hip, stream, [("fused", (lambda j=j: one(j))) for j in range(n)])
+        b = N * K + 4 * N + 2 * M * K + 3 * 2 * M * N
+        out[f"down_add_M{M}"] = {"us": us_one, "two_calls_us": us_two, "GBps": b / us_one / 1e3,
+                                 "frac": b / us_one / 1e3 / PEAK_GBPS, "bytes": b, "buffer_sets": n}
+        for x in (cb, ob):
+            x.free()
+        ab.free()
+        rb.free()
+    wp.free()
+    sc.free()
     return out
 
 
@@ -1506,7 +1546,8 @@ def main():
         print(json.dumps({"gemm_int8": gemm_extras(L, hip, stream),
                           "gemm_int8_shared_a": shared_a_extras(L, hip, stream),
                           "norm_gemm_int8_shared_a": norm_shared_extras(L, hip, stream),
-                          "gemm_int8_silu_mul": silu_mul_gemm_extras(L, hip, stream)}), flush=True)
+                          "gemm_int8_silu_mul": silu_mul_gemm_extras(L, hip, stream),
+                          "gemm_int8_add": gemm_add_extras(L, hip, stream)}), flush=True)
         return
     if args.floors_only:
         print(json.dumps({"floors": floor_extras(hip, stream)}), flush=True)

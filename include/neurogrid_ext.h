@@ -177,6 +177,15 @@ int ng_add_rmsnorm_gemm_int8_shared_a(int count, void* normed, void* residual_ou
 int ng_gemm_int8_silu_mul(void* out, void* gate, void* up, const void* a, const void* b_gate,
                           const void* scale_gate, const void* b_up, const void* scale_up, int M, int K, int N);
 
+/* The INT8 layer's down projection and final residual add
+ * (gpu/engine/layer.cu:593-598): cuda_gemm_int8(c, a, b, scale, M, K, N,
+ * true), then cuda_add(out, c, residual, M N), bit for bit. On the GEMV
+ * kernel's shapes (M <= 4, aligned pointers), with no output overlapping an
+ * input or the other output (out may be c or residual itself), one launch
+ * writes both; otherwise this is the two calls. Returns 0 or -1. */
+int ng_gemm_int8_add(void* out, void* c, const void* a, const void* b, const void* scale,
+                     const void* residual, int M, int K, int N);
+
 #ifdef __cplusplus
 }
 #endif

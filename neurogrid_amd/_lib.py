@@ -98,6 +98,7 @@ SIGNATURES: dict[str, tuple] = {
     "ng_add_rmsnorm_gemm_int8_shared_a": (_i, [_i, _vp, _vp, C.POINTER(_vp), _cvp, _cvp, _cvp, _f,
                                                C.POINTER(_cvp), C.POINTER(_cvp), _ip, _i, _i]),
     "ng_gemm_int8_silu_mul": (_i, [_vp, _vp, _vp, _cvp, _cvp, _cvp, _cvp, _cvp, _i, _i, _i]),
+    "ng_gemm_int8_add": (_i, [_vp, _vp, _cvp, _cvp, _cvp, _cvp, _i, _i, _i]),
 }
 
 _LIB = None

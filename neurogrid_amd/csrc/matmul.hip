@@ -381,18 +381,14 @@ __device__ __forceinline__ void gemv_finish(const float (&acc)[R][MR], uint16_t*
     }
 }
 
-// One block of the GEMV kernels: rows blk R .. blk R + R - 1 of B.
+// One lane's sums of the GEMV kernels' block for rows n0 .. n0 + R - 1 of B.
 template <int MR, int R>
-__device__ __forceinline__ void gemv_i8w_block(uint16_t* __restrict__ c, const uint16_t* __restrict__ a,
-                                               const int8_t* __restrict__ b, const float* __restrict__ scale,
-                                               int M, int N, int K, int blk) {
+__device__ __forceinline__ void gemv_i8w_sums(float (&acc)[R][MR], const uint16_t* __restrict__ a,
+                                              const int8_t* __restrict__ b, int M, int N, int K, int n0) {
     const int tid = threadIdx.x;
     const int lane = tid & (kWave - 1);
     const int wave = __builtin_amdgcn_readfirstlane(tid / kWave);
-    const int n0 = blk * R;
     const int nseg = (K + kGvSeg - 1) / kGvSeg;
-
-    float acc[R][MR];
 #pragma unroll
     for (int r = 0; r < R; ++r)
 #pragma unroll
@@ -415,7 +411,16 @@ __device__ __forceinline__ void gemv_i8w_block(uint16_t* __restrict__ c, const u
         __builtin_amdgcn_sched_barrier(0);
         gemv_segment<MR, R>(acc, av, bv, kin);
     }
-    gemv_finish<MR, R>(acc, c, scale, M, N, n0);
+}
+
+// One block of the GEMV kernels: rows blk R .. blk R + R - 1 of B.
+template <int MR, int R>
+__device__ __forceinline__ void gemv_i8w_block(uint16_t* __restrict__ c, const uint16_t* __restrict__ a,
+                                               const int8_t* __restrict__ b, const float* __restrict__ scale,
+                                               int M, int N, int K, int blk) {
+    float acc[R][MR];
+    gemv_i8w_sums<MR, R>(acc, a, b, M, N, K, blk * R);
+    gemv_finish<MR, R>(acc, c, scale, M, N, blk * R);
 }
 
 template <int MR, int R>
@@ -497,6 +502,34 @@ __global__ __launch_bounds__(kGvWaves * kWave) void gemv_i8w_swiglu_kernel(Swigl
             sa.gate[o] = g;
             sa.up[o] = u;
             sa.out[o] = from_f32<f16>(swiglu_f32(to_f32<f16>(g), to_f32<f16>(u)));
+        }
+    }
+}
+
+// A product and the residual add after it (ng_gemm_int8_add): the GEMV
+// kernel's blocks, then out = fp16(c + residual) on the rounded product, as
+// cuda_add computes it. out may be c or the residual itself: each element is
+// written by one thread, out last.
+template <int MR, int R>
+__global__ __launch_bounds__(kGvWaves * kWave) void gemv_i8w_add_kernel(uint16_t* out, uint16_t* c,
+                                                                        const uint16_t* res,
+                                                                        const uint16_t* __restrict__ a,
+                                                                        const int8_t* __restrict__ b,
+                                                                        const float* __restrict__ scale, int M,
+                                                                        int N, int K) {
+    const int n0 = blockIdx.x * R;
+    float acc[R][MR];
+    gemv_i8w_sums<MR, R>(acc, a, b, M, N, K, n0);
+    const float v = gemv_reduce<MR, R>(acc);
+    const int tid = threadIdx.x;
+    if (tid < R * MR) {
+        const int r = tid / MR, m = tid % MR, n = n0 + r;
+        if (m < M && n < N) {
+            const size_t o = static_cast<size_t>(m) * N + n;
+            const uint16_t cv = from_f32<f16>(v * scale[n]);
+            const float sum = to_f32<f16>(cv) + to_f32<f16>(res[o]);
+            c[o] = cv;
+            out[o] = from_f32<f16>(sum);
         }
     }
 }
@@ -2162,5 +2195,47 @@ extern "C" int ng_gemm_int8_silu_mul(void* out, void* gate, void* up, const void
         gemv_i8w_swiglu_kernel<1, 8><<<dim3(static_cast<unsigned>((N + 7) / 8)), block, 0, stream()>>>(sa, ap, M, N, K);
     }
     NG_CHECK_LAUNCH("ng_gemm_int8_silu_mul");
+    return 0;
+}
+
+// A product (cuda_gemm_int8 with transpose_b) and the residual add after it
+// (cuda_add(out, c, residual)): one launch of gemv_i8w_add_kernel on the GEMV
+// kernel's shapes when no output overlaps an input or the other output (out
+// may be c or the residual exactly); otherwise the two calls. The same bits
+// either way.
+extern "C" int ng_gemm_int8_add(void* out, void* c, const void* a, const void* b, const void* scale,
+                                const void* residual, int M, int K, int N) {
+    NG_REQUIRE(out && c && a && b && scale && residual, "ng_gemm_int8_add: null pointer");
+    NG_REQUIRE(M > 0 && K > 0 && N > 0, "ng_gemm_int8_add: M=%d K=%d N=%d must be > 0", M, K, N);
+    const size_t cb = static_cast<size_t>(M) * N * 2, ab = static_cast<size_t>(M) * K * 2;
+    const size_t bb = static_cast<size_t>(N) * K, sb = static_cast<size_t>(N) * 4;
+    const int path = use_i8w(a, b, M, K, N, true) ? gemv_shape(M, K, N) : 0;
+    bool apart = !overlaps(c, cb, residual, cb) &&
+                 (out == c || out == residual || (!overlaps(out, cb, c, cb) && !overlaps(out, cb, residual, cb)));
+    for (const void* o : {out, c})
+        apart = apart && !overlaps(o, cb, a, ab) && !overlaps(o, cb, b, bb) && !overlaps(o, cb, scale, sb);
+    if (path < 1 || !apart) {
+        const int r = cuda_gemm_int8(c, a, b, scale, M, K, N, true);
+        if (r != 0) return r;
+        return cuda_add(out, c, residual, static_cast<size_t>(M) * N);
+    }
+    const auto o16 = static_cast<uint16_t*>(out);
+    const auto c16 = static_cast<uint16_t*>(c);
+    const auto r16 = static_cast<const uint16_t*>(residual);
+    const auto ap = static_cast<const uint16_t*>(a);
+    const auto bp = static_cast<const int8_t*>(b);
+    const auto sp = static_cast<const float*>(scale);
+    const dim3 block(kGvWaves * kWave);
+    if (path == 3) {
+        gemv_i8w_add_kernel<4, 4><<<dim3(static_cast<unsigned>((N + 3) / 4)), block, 0, stream()>>>(
+            o16, c16, r16, ap, bp, sp, M, N, K);
+    } else if (path == 2) {
+        gemv_i8w_add_kernel<2, 8><<<dim3(static_cast<unsigned>((N + 7) / 8)), block, 0, stream()>>>(
+            o16, c16, r16, ap, bp, sp, M, N, K);
+    } else {
+        gemv_i8w_add_kernel<1, 8><<<dim3(static_cast<unsigned>((N + 7) / 8)), block, 0, stream()>>>(
+            o16, c16, r16, ap, bp, sp, M, N, K);
+    }
+    NG_CHECK_LAUNCH("ng_gemm_int8_add");
     return 0;
 }

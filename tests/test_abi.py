@@ -116,6 +116,8 @@ def test_argument_errors_return_minus_one_without_touching_the_gpu(capfd):
     assert L.ng_add_rmsnorm_gemm_int8_shared_a(5, p, p, pv, p, p, p, e, pv, pv, nv, 1, 64) == -1
     assert L.ng_gemm_int8_silu_mul(p, p, p, p, None, p, p, p, 1, 64, 16) == -1     # null gate weights
     assert L.ng_gemm_int8_silu_mul(p, p, p, p, p, p, p, p, 1, 64, 0) == -1        # N == 0
+    assert L.ng_gemm_int8_add(p, p, p, p, p, None, 1, 64, 16) == -1                 # null residual
+    assert L.ng_gemm_int8_add(p, p, p, p, p, p, 0, 64, 16) == -1                    # M == 0
     err = capfd.readouterr().err
     assert "neurogrid-amd:" in err and "null pointer" in err
 

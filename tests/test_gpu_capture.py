@@ -220,6 +220,13 @@ def _ops():
     add("ng_gemm_int8_silu_mul_M16", {"o": (E2, (16, GN)), "g": (E2, (16, GN)), "u": (E2, (16, GN))},
         lambda L, i, o: L.ng_gemm_int8_silu_mul(o["o"].vp, o["g"].vp, o["u"].vp, i["a16"].vp, i["wq"].vp, i["wsc"].vp,
                                                 i["wq"].vp, i["wsc"].vp, 16, GK, GN))
+    # a product and the residual add after it: one launch at M = 1, the two calls at M = 16
+    add("ng_gemm_int8_add_M1", {"o": (E2, (1, GN)), "c": (E2, (1, GN))},
+        lambda L, i, o: L.ng_gemm_int8_add(o["o"].vp, o["c"].vp, i["a1"].vp, i["wq"].vp, i["wsc"].vp, i["xh"].vp,
+                                           1, GK, GN))
+    add("ng_gemm_int8_add_M16", {"o": (E2, (16, GN)), "c": (E2, (16, GN))},
+        lambda L, i, o: L.ng_gemm_int8_add(o["o"].vp, o["c"].vp, i["a16"].vp, i["wq"].vp, i["wsc"].vp, i["xh"].vp,
+                                           16, GK, GN))
     # from 4096 rows of A on: B dequantized into the stream's fp16 buffer, then hipBLASLt
     add("cuda_gemm_int8_M4096_library", {"y": (E2, (4096, GN))},
         lambda L, i, o: L.cuda_gemm_int8(o["y"].vp, i["a4096"].vp, i["wq"].vp, i["wsc"].vp, 4096, GK, GN, True),
