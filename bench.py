@@ -673,6 +673,7 @@ def extra_kernels(L, hip, stream):
     out["norm_gemm_int8_shared_a"] = norm_shared_extras(L, hip, stream)
     out["gemm_int8_silu_mul"] = silu_mul_gemm_extras(L, hip, stream)
     out["gemm_int8_add"] = gemm_add_extras(L, hip, stream)
+    out["int8_decode_layer"] = int8_decode_layer_extras(L, hip, stream)
     g = out["gemm_int8"]
     g["mistral7b_layer_M1"]["shared_a_us"] = (sh["qkv_M1"]["us"] + g["q_proj_M1"]["us"] + sh["gate_up_M1"]["us"]
                                               + g["down_proj_M1"]["us"])
@@ -968,6 +969,111 @@ def gemm_add_extras(L, hip, stream, K=14336, N=4096):
         rb.free()
     wp.free()
     sc.free()
+    return out
+
+
+def int8_decode_layer_extras(L, hip, stream):
+    """One Mistral-7B INT8 layer at decode (M = 1 and 2 tokens), everything
+    but attention, as one graph step on cache-cold weights (a pool of weight
+    sets, 218 MB each). engine_us: the engine's own calls
+    (gpu/engine/layer.cu:458-598) on this library, 17 launches: copy residual,
+    RMSNorm, q, k, v, RoPE Q, RoPE K, o, add, copy residual, RMSNorm in place,
+    gate, up, SiLU, mul, down, add. fused_us: the same layer through the fused
+    entry points, 6 launches: ng_rmsnorm_gemm_int8_shared_a (q/k/v),
+    ng_rope_qk_with_theta, o, cuda_add_rmsnorm (normed in place, the layer
+    input as residual), ng_gemm_int8_silu_mul (in place on gate),
+    ng_gemm_int8_add. The attention output is a fixed buffer."""
+    rng = np.random.Generator(np.random.PCG64(10))
+    H, I, NQ, NKV, D = 4096, 14336, 32, 8, 128
+    KV = NKV * D
+    eps, theta = C.c_float(1e-5), C.c_float(1e6)
+    shapes = {"q": (H, H), "k": (KV, H), "v": (KV, H), "o": (H, H), "gate": (I, H), "up": (I, H), "down": (H, I)}
+    n = pool_slots(sum(a * b for a, b in shapes.values()))
+    wp, ws = {}, {}
+    for name, (N, K) in shapes.items():
+        wq = rng.integers(-128, 128, (N, K)).astype(np.int8)
+        wp[name] = Pool(hip, wq.nbytes, n, wq)
+        ws[name] = DB.from_array(rng.uniform(1e-3, 1e-2, N).astype(np.float32))
+        del wq
+    w_attn = DB.from_array(W.round_to(1 + 0.05 * rng.standard_normal(H, dtype=np.float32), "f16"))
+    w_ffn = DB.from_array(W.round_to(1 + 0.05 * rng.standard_normal(H, dtype=np.float32), "f16"))
+    out = {}
+    for M in (1, 2):
+        f16 = lambda *shape: DB.from_array(W.round_to(rng.standard_normal(shape, dtype=np.float32), "f16"))
+        x, attn = f16(M, H), f16(M, H)
+        pos = DB.from_array(np.arange(100, 100 + M, dtype=np.int32))
+        normed, res, res2, q, o, out_b = (DB(2 * M * H) for _ in range(6))
+        gate, up = DB(2 * M * I), DB(2 * M * I)
+        k_b, v_b = DB(2 * M * KV), DB(2 * M * KV)
+        nb = 2 * M * H
+
+        def gemm(c, a, name, j, N, K):
+            return L.cuda_gemm_int8(c.vp, a.vp, wp[name].at(j), ws[name].vp, M, K, N, True)
+
+        def engine(j):
+            steps = (
+                lambda: hip.h.hipMemcpyAsync(res.vp, x.vp, nb, 3, stream),
+                lambda: L.cuda_rmsnorm(normed.vp, x.vp, w_attn.vp, M, H, eps),
+                lambda: gemm(q, normed, "q", j, H, H),
+                lambda: gemm(k_b, normed, "k", j, KV, H),
+                lambda: gemm(v_b, normed, "v", j, KV, H),
+                lambda: L.cuda_rope_with_theta(q.vp, q.vp, pos.ip, 1, M, NQ, D, 0, theta),
+                lambda: L.cuda_rope_with_theta(k_b.vp, k_b.vp, pos.ip, 1, M, NKV, D, 0, theta),
+                lambda: gemm(normed, attn, "o", j, H, H),
+                lambda: L.cuda_add(normed.vp, normed.vp, res.vp, M * H),
+                lambda: hip.h.hipMemcpyAsync(res.vp, normed.vp, nb, 3, stream),
+                lambda: L.cuda_rmsnorm(normed.vp, normed.vp, w_ffn.vp, M, H, eps),
+                lambda: gemm(gate, normed, "gate", j, I, H),
+                lambda: gemm(up, normed, "up", j, I, H),
+                lambda: L.cuda_silu(gate.vp, gate.vp, M * I),
+                lambda: L.cuda_mul(gate.vp, gate.vp, up.vp, M * I),
+                lambda: gemm(normed, gate, "down", j, H, I),
+                lambda: L.cuda_add(out_b.vp, normed.vp, res.vp, M * H),
+            )
+            for f in steps:
+                rc = f()
+                if rc:
+                    return rc
+            return 0
+
+        qkv_n = (C.c_int * 3)(H, KV, KV)
+        qkv_s = (C.c_void_p * 3)(ws["q"].ptr, ws["k"].ptr, ws["v"].ptr)
+        qkv_c = (C.c_void_p * 3)(q.ptr, k_b.ptr, v_b.ptr)
+
+        def fused(j):
+            steps = (
+                lambda: L.ng_rmsnorm_gemm_int8_shared_a(
+                    3, normed.vp, qkv_c, x.vp, w_attn.vp, eps,
+                    (C.c_void_p * 3)(wp["q"].at(j), wp["k"].at(j), wp["v"].at(j)), qkv_s, qkv_n, M, H),
+                lambda: L.ng_rope_qk_with_theta(q.vp, q.vp, k_b.vp, k_b.vp, pos.ip, 1, M, NQ, NKV, D, 0, theta),
+                lambda: gemm(o, attn, "o", j, H, H),
+                lambda: L.cuda_add_rmsnorm(normed.vp, res2.vp, o.vp, x.vp, w_ffn.vp, M, H, eps),
+                lambda: L.ng_gemm_int8_silu_mul(gate.vp, gate.vp, up.vp, normed.vp, wp["gate"].at(j), ws["gate"].vp,
+                                                wp["up"].at(j), ws["up"].vp, M, H, I),
+                lambda: L.ng_gemm_int8_add(out_b.vp, normed.vp, gate.vp, wp["down"].at(j), ws["down"].vp, res2.vp,
+                                           M, I, H),
+            )
+            for f in steps:
+                rc = f()
+                if rc:
+                    return rc
+            return 0
+
+        us_e = time_pool_kernel(hip, stream, [("engine", (lambda j=j: engine(j))) for j in range(n)], launches=12)
+        us_f = time_pool_kernel(hip, stream, [("fused", (lambda j=j: fused(j))) for j in range(n)], launches=12)
+        wbytes = sum(a * b + 4 * a for a, b in shapes.values())
+        out[f"M{M}"] = {"engine_us": us_e, "fused_us": us_f, "weight_bytes": wbytes,
+                        "fused_weight_GBps": wbytes / us_f / 1e3, "fused_frac": wbytes / us_f / 1e3 / PEAK_GBPS,
+                        "launches": {"engine": 17, "fused": 6}, "buffer_sets": n}
+        for b_ in (x, attn, pos, normed, res, res2, q, o, out_b, gate, up, k_b, v_b):
+            b_.free()
+    for name in shapes:
+        wp[name].free()
+        ws[name].free()
+    w_attn.free()
+    w_ffn.free()
+    out["note"] = ("attention excluded (its output is a fixed buffer); engine = the reference's call sequence on this "
+                   "library (its cuda_gemm_int8 calls take the fused GEMV kernels), fused = the six fused entry points")
     return out
 
 
@@ -1547,7 +1653,8 @@ def main():
                           "gemm_int8_shared_a": shared_a_extras(L, hip, stream),
                           "norm_gemm_int8_shared_a": norm_shared_extras(L, hip, stream),
                           "gemm_int8_silu_mul": silu_mul_gemm_extras(L, hip, stream),
-                          "gemm_int8_add": gemm_add_extras(L, hip, stream)}), flush=True)
+                          "gemm_int8_add": gemm_add_extras(L, hip, stream),
+                          "int8_decode_layer": int8_decode_layer_extras(L, hip, stream)}), flush=True)
         return
     if args.floors_only:
         print(json.dumps({"floors": floor_extras(hip, stream)}), flush=True)
