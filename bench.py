@@ -982,7 +982,9 @@ def int8_decode_layer_extras(L, hip, stream):
     entry points, 6 launches: ng_rmsnorm_gemm_int8_shared_a (q/k/v),
     ng_rope_qk_with_theta, o, cuda_add_rmsnorm (normed in place, the layer
     input as residual), ng_gemm_int8_silu_mul (in place on gate),
-    ng_gemm_int8_add. The attention output is a fixed buffer."""
+    ng_gemm_int8_add. fused_rope_us: the same with RMSNorm, q/k/v and RoPE in
+    one launch (ng_rmsnorm_qkv_rope_int8), 5 launches. The attention output is
+    a fixed buffer."""
     rng = np.random.Generator(np.random.PCG64(10))
     H, I, NQ, NKV, D = 4096, 14336, 32, 8, 128
     KV = NKV * D
@@ -1040,12 +1042,17 @@ def int8_decode_layer_extras(L, hip, stream):
         qkv_s = (C.c_void_p * 3)(ws["q"].ptr, ws["k"].ptr, ws["v"].ptr)
         qkv_c = (C.c_void_p * 3)(q.ptr, k_b.ptr, v_b.ptr)
 
-        def fused(j):
-            steps = (
-                lambda: L.ng_rmsnorm_gemm_int8_shared_a(
-                    3, normed.vp, qkv_c, x.vp, w_attn.vp, eps,
-                    (C.c_void_p * 3)(wp["q"].at(j), wp["k"].at(j), wp["v"].at(j)), qkv_s, qkv_n, M, H),
+        def fused(j, rope_in_qkv=False):
+            qkv_w = (C.c_void_p * 3)(wp["q"].at(j), wp["k"].at(j), wp["v"].at(j))
+            front = (
+                (lambda: L.ng_rmsnorm_qkv_rope_int8(normed.vp, q.vp, k_b.vp, v_b.vp, x.vp, w_attn.vp, eps, qkv_w,
+                                                    qkv_s, pos.ip, M, H, NQ, NKV, D, theta)),
+            ) if rope_in_qkv else (
+                lambda: L.ng_rmsnorm_gemm_int8_shared_a(3, normed.vp, qkv_c, x.vp, w_attn.vp, eps, qkv_w, qkv_s,
+                                                        qkv_n, M, H),
                 lambda: L.ng_rope_qk_with_theta(q.vp, q.vp, k_b.vp, k_b.vp, pos.ip, 1, M, NQ, NKV, D, 0, theta),
+            )
+            steps = front + (
                 lambda: gemm(o, attn, "o", j, H, H),
                 lambda: L.cuda_add_rmsnorm(normed.vp, res2.vp, o.vp, x.vp, w_ffn.vp, M, H, eps),
                 lambda: L.ng_gemm_int8_silu_mul(gate.vp, gate.vp, up.vp, normed.vp, wp["gate"].at(j), ws["gate"].vp,
@@ -1061,10 +1068,12 @@ def int8_decode_layer_extras(L, hip, stream):
 
         us_e = time_pool_kernel(hip, stream, [("engine", (lambda j=j: engine(j))) for j in range(n)], launches=12)
         us_f = time_pool_kernel(hip, stream, [("fused", (lambda j=j: fused(j))) for j in range(n)], launches=12)
+        us_r = time_pool_kernel(hip, stream, [("fused_rope", (lambda j=j: fused(j, True))) for j in range(n)],
+                                launches=12)
         wbytes = sum(a * b + 4 * a for a, b in shapes.values())
-        out[f"M{M}"] = {"engine_us": us_e, "fused_us": us_f, "weight_bytes": wbytes,
-                        "fused_weight_GBps": wbytes / us_f / 1e3, "fused_frac": wbytes / us_f / 1e3 / PEAK_GBPS,
-                        "launches": {"engine": 17, "fused": 6}, "buffer_sets": n}
+        out[f"M{M}"] = {"engine_us": us_e, "fused_us": us_f, "fused_rope_us": us_r, "weight_bytes": wbytes,
+                        "fused_weight_GBps": wbytes / us_r / 1e3, "fused_frac": wbytes / us_r / 1e3 / PEAK_GBPS,
+                        "launches": {"engine": 17, "fused": 6, "fused_rope": 5}, "buffer_sets": n}
         for b_ in (x, attn, pos, normed, res, res2, q, o, out_b, gate, up, k_b, v_b):
             b_.free()
     for name in shapes:

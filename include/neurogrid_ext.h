@@ -165,6 +165,21 @@ int ng_add_rmsnorm_gemm_int8_shared_a(int count, void* normed, void* residual_ou
                                       float eps, const void* const* b, const void* const* scales,
                                       const int* n, int M, int K);
 
+/* The front of the INT8 layer's attention block (gpu/engine/layer.cu:467,
+ * 487-501 and the RoPE pair that follows the projections, :1016-1018 in the
+ * fp16 layer): ng_rmsnorm_gemm_int8_shared_a(3, normed, {q, k, v}, x,
+ * norm_weight, eps, b, scales, {Hq D, Hkv D, Hkv D}, M, hidden), then
+ * ng_rope_qk_with_theta(q, q, k, k, positions, 1, M, Hq, Hkv, D, 0,
+ * rope_theta): split-half RoPE on q and k in place, one token per row of x
+ * with its position. b and scales hold q's, k's and v's. Bit for bit those
+ * two calls; where the norm folds into the products' launch (decode, see
+ * ng_rmsnorm_gemm_int8_shared_a) and D is a multiple of 8 and at most 256,
+ * the rotation runs in that launch too. Returns 0 or -1. */
+int ng_rmsnorm_qkv_rope_int8(void* normed, void* q, void* k, void* v, const void* x,
+                             const void* norm_weight, float eps, const void* const* b,
+                             const void* const* scales, const int* positions, int M, int hidden,
+                             int num_q_heads, int num_kv_heads, int head_dim, float rope_theta);
+
 /* The INT8 layer's gate and up projections and SwiGLU (gpu/engine/layer.cu:
  * 575-588: cuda_gemm_int8 twice on one A, then cuda_silu and cuda_mul, which
  * this library's cuda_silu_mul replaces with one rounding): gate and up as

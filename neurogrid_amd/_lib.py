@@ -99,6 +99,8 @@ SIGNATURES: dict[str, tuple] = {
                                                C.POINTER(_cvp), C.POINTER(_cvp), _ip, _i, _i]),
     "ng_gemm_int8_silu_mul": (_i, [_vp, _vp, _vp, _cvp, _cvp, _cvp, _cvp, _cvp, _i, _i, _i]),
     "ng_gemm_int8_add": (_i, [_vp, _vp, _cvp, _cvp, _cvp, _cvp, _i, _i, _i]),
+    "ng_rmsnorm_qkv_rope_int8": (_i, [_vp, _vp, _vp, _vp, _cvp, _cvp, _f, C.POINTER(_cvp), C.POINTER(_cvp), _ip, _i,
+                                      _i, _i, _i, _i, _f]),
 }
 
 _LIB = None

@@ -606,16 +606,40 @@ __device__ __noinline__ float norm_row_ss_exact(const NormArgs& na, int m, int K
 // the products of the GEMV kernel's block blk (rows blk R .. blk R + R - 1 of
 // B), exactly as that block computes them. SEGS: the most 1024-value segments
 // of K one wave takes (K <= 4096 SEGS).
-template <int MR, int R, int SEGS, bool ADD>
+// RoPE on two of the products (ng_rmsnorm_qkv_rope_int8): split-half pairs
+// (i, i + D/2) of each head of D values, as cuda_rope_with_theta style 0,
+// for the tokens' positions.
+constexpr int kRopeEpiMaxHalf = 128;  // D <= 256
+struct RopeEpi {
+    const int* pos;  // [M]
+    int D;
+    int half;  // D / 2
+    int bph;   // blocks per head: half / 4
+    float inv_freq[kRopeEpiMaxHalf];
+};
+
+template <int MR, int R, int SEGS, bool ADD, bool ROPE = false>
 __device__ __forceinline__ void gemv_i8w_norm_block(uint16_t* __restrict__ c, const int8_t* __restrict__ b,
                                                     const float* __restrict__ scale, const NormArgs& na, int M,
-                                                    int N, int K, int blk, bool store) {
+                                                    int N, int K, int blk, bool store, bool rope = false,
+                                                    const RopeEpi* re = nullptr) {
+    static_assert(!ROPE || R == 8, "a RoPE block holds four rotation pairs");
     __shared__ double s_part[kGvWaves][MR];
     const int tid = threadIdx.x;
     const int lane = tid & (kWave - 1);
     const int wave = __builtin_amdgcn_readfirstlane(tid / kWave);
     const int n0 = blk * R;
     const int nseg = (K + kGvSeg - 1) / kGvSeg;
+    // Row of B (and of C) in slot r: n0 + r, or for a rotated product the
+    // block's four pairs of one head, rows h D + q + r (r < 4) and
+    // h D + D/2 + q + r - 4. An output's sums do not depend on its slot, so
+    // each row gets the GEMV kernel's bits either way.
+    const bool rot = ROPE && rope;
+    const int rh = rot ? blk / re->bph : 0;
+    const int rq = rot ? (blk - rh * re->bph) * 4 : 0;
+    const auto row_of = [&](int r) {
+        return rot ? rh * re->D + (r < 4 ? rq + r : re->half + rq + r - 4) : n0 + r;
+    };
 
     // Loads: the lane's pieces of x (res) and w, then its rows of B. They are
     // issued without branches, so that waiting for the first ones does not
@@ -645,7 +669,8 @@ __device__ __forceinline__ void gemv_i8w_norm_block(uint16_t* __restrict__ c, co
 #pragma unroll
     for (int s = 0; s < SEGS; ++s)
 #pragma unroll
-        for (int r = 0; r < R; ++r) bv[s][r] = ld16_stream(b + static_cast<size_t>(min(n0 + r, N - 1)) * K + kc[s]);
+        for (int r = 0; r < R; ++r)
+            bv[s][r] = ld16_stream(b + static_cast<size_t>(min(row_of(r), N - 1)) * K + kc[s]);
     __builtin_amdgcn_sched_barrier(0);
 
     // o = x, or the rounded sum x + res; squares of x, or of the unrounded
@@ -737,7 +762,31 @@ __device__ __forceinline__ void gemv_i8w_norm_block(uint16_t* __restrict__ c, co
         }
         gemv_segment<MR, R>(acc, av, bv[s], kin[s]);
     }
-    gemv_finish<MR, R>(acc, c, scale, M, N, n0);
+    if (!rot) {
+        gemv_finish<MR, R>(acc, c, scale, M, N, n0);
+        return;
+    }
+    // Rotated product: C = fp16(sum * scale) as the GEMV kernel rounds it, then
+    // RoPE on the rounded pair, with cuda_rope_with_theta's angle, sincosf and
+    // expression, rounded once more. Slot r's partner is r ^ 4 (thread
+    // tid ^ 4 MR, in the first wave).
+    constexpr int V = R * MR;
+    const float v = gemv_reduce<MR, R>(acc);
+    float x = 0.0f;
+    int r = 0, m = 0, row = 0;
+    if (tid < V) {
+        r = tid / MR;
+        m = tid % MR;
+        row = row_of(r);
+        x = to_f32<f16>(from_f32<f16>(v * scale[row]));
+    }
+    const float xp = __shfl_xor(x, 4 * MR, kWave);
+    if (tid < V && m < M) {
+        float sn, cs;
+        sincosf(static_cast<float>(re->pos[m]) * re->inv_freq[rq + (r & 3)], &sn, &cs);
+        const float y = r < 4 ? x * cs - xp * sn : xp * sn + x * cs;
+        c[static_cast<size_t>(m) * N + row] = from_f32<f16>(y);
+    }
 }
 
 template <int MR, int R, int SEGS, bool ADD>
@@ -745,6 +794,15 @@ __global__ __launch_bounds__(kGvWaves * kWave) void gemv_i8w_norm_shared_kernel(
                                                                                 int K) {
     shared_dispatch(s, [&](uint16_t* c, const int8_t* b, const float* scale, int n, int blk, int) {
         gemv_i8w_norm_block<MR, R, SEGS, ADD>(c, b, scale, na, M, n, K, blk, blockIdx.x == 0);
+    });
+}
+
+// The same with RoPE on products 0 and 1 (q and k).
+template <int MR, int SEGS>
+__global__ __launch_bounds__(kGvWaves * kWave) void gemv_i8w_norm_rope_shared_kernel(SharedSet s, NormArgs na,
+                                                                                     RopeEpi re, int M, int K) {
+    shared_dispatch(s, [&](uint16_t* c, const int8_t* b, const float* scale, int n, int blk, int p) {
+        gemv_i8w_norm_block<MR, 8, SEGS, false, true>(c, b, scale, na, M, n, K, blk, blockIdx.x == 0, p < 2, &re);
     });
 }
 
@@ -2083,11 +2141,21 @@ static bool overlaps(const void* p, size_t pn, const void* q, size_t qn) {
 // kNormSharedMaxBlocks blocks and no output overlaps an input (the kernel's
 // blocks read the inputs while the first one stores); otherwise the norm
 // entry point followed by ng_gemm_int8_shared_a.
-// The same bits either way.
+// The same bits either way. With rs, RoPE (ng_rope_qk_with_theta, style 0)
+// follows on products 0 and 1 in place; the fused launch then also needs the
+// GEMV shape of one or two rows (8 rows of B per block), D a multiple of 8,
+// the three outputs apart from each other and the positions apart from every
+// output.
+struct RopeSpec {
+    const int* pos;
+    int nq, nkv, D;
+    float theta;
+};
+
 template <bool ADD>
 static int norm_shared(const char* name, int count, void* normed, void* res_out, void* const* c, const void* x,
                        const void* res, const void* w, float eps, const void* const* b, const void* const* scales,
-                       const int* n, int M, int K) {
+                       const int* n, int M, int K, const RopeSpec* rs = nullptr) {
     NG_REQUIRE(normed && x && w && c && b && scales && n && (!ADD || (res && res_out)), "%s: null pointer", name);
     NG_REQUIRE(count >= 1 && count <= kMaxShared, "%s: count=%d must be in [1, %d]", name, count, kMaxShared);
     NG_REQUIRE(M > 0 && K > 0, "%s: M=%d K=%d must be > 0", name, M, K);
@@ -2111,16 +2179,28 @@ static int norm_shared(const char* name, int count, void* normed, void* res_out,
                 clear_of_writes(scales[i], static_cast<size_t>(n[i]) * 4) && clear_of_writes(c[i], cb) &&
                 !overlaps(c[i], cb, x, rows) && !overlaps(c[i], cb, w, wb) && (!ADD || !overlaps(c[i], cb, res, rows));
     }
+    if (rs) {
+        const size_t pb = static_cast<size_t>(M) * 4;
+        apart = apart && !overlaps(rs->pos, pb, normed, rows) && (!ADD || !overlaps(rs->pos, pb, res_out, rows));
+        for (int i = 0; i < count; ++i) {
+            const size_t cb = static_cast<size_t>(M) * n[i] * 2;
+            apart = apart && !overlaps(rs->pos, pb, c[i], cb);
+            for (int j = i + 1; j < count; ++j) apart = apart && !overlaps(c[i], cb, c[j], static_cast<size_t>(M) * n[j] * 2);
+        }
+    }
     // GEMV blocks of the fused launch (rows of B per block as the GEMV kernel's).
     const int R = path == 3 ? 4 : 8;
     long long blocks = 0;
     for (int i = 0; i < count; ++i) blocks += (n[i] + R - 1) / R;
     const bool fused = path >= 1 && apart && K <= kNormSharedMaxK && blocks <= kNormSharedMaxBlocks && aligned16(x) &&
-                       aligned16(w) && aligned16(normed) && (!ADD || (aligned16(res) && aligned16(res_out)));
+                       aligned16(w) && aligned16(normed) && (!ADD || (aligned16(res) && aligned16(res_out))) &&
+                       (!rs || (path <= 2 && rs->D % 8 == 0 && rs->D <= 2 * kRopeEpiMaxHalf));
     if (!fused) {
-        const int r = ADD ? cuda_add_rmsnorm(normed, res_out, x, res, w, M, K, eps) : cuda_rmsnorm(normed, x, w, M, K, eps);
-        if (r != 0) return r;
-        return ng_gemm_int8_shared_a(count, c, normed, b, scales, n, M, K);
+        int r = ADD ? cuda_add_rmsnorm(normed, res_out, x, res, w, M, K, eps) : cuda_rmsnorm(normed, x, w, M, K, eps);
+        if (r == 0) r = ng_gemm_int8_shared_a(count, c, normed, b, scales, n, M, K);
+        if (r == 0 && rs)
+            r = ng_rope_qk_with_theta(c[0], c[0], c[1], c[1], rs->pos, 1, M, rs->nq, rs->nkv, rs->D, 0, rs->theta);
+        return r;
     }
     SharedSet set{};
     int first = 0;
@@ -2135,6 +2215,27 @@ static int norm_shared(const char* name, int count, void* normed, void* res_out,
     }
     const NormArgs na{static_cast<const uint16_t*>(x), static_cast<const uint16_t*>(res), static_cast<const uint16_t*>(w),
                       static_cast<uint16_t*>(normed), static_cast<uint16_t*>(res_out), eps};
+    if constexpr (!ADD) {
+        if (rs) {
+            RopeEpi re{};
+            re.pos = rs->pos;
+            re.D = rs->D;
+            re.half = rs->D / 2;
+            re.bph = rs->D / 8;
+            fill_inv_freq(rs->theta, rs->D, re.inv_freq);
+            const dim3 grid(static_cast<unsigned>(first)), block(kGvWaves * kWave);
+            const bool one = K <= kGvWaves * kGvSeg;
+            if (path == 1) {
+                if (one) gemv_i8w_norm_rope_shared_kernel<1, 1><<<grid, block, 0, stream()>>>(set, na, re, M, K);
+                else gemv_i8w_norm_rope_shared_kernel<1, 2><<<grid, block, 0, stream()>>>(set, na, re, M, K);
+            } else {
+                if (one) gemv_i8w_norm_rope_shared_kernel<2, 1><<<grid, block, 0, stream()>>>(set, na, re, M, K);
+                else gemv_i8w_norm_rope_shared_kernel<2, 2><<<grid, block, 0, stream()>>>(set, na, re, M, K);
+            }
+            NG_CHECK_LAUNCH(name);
+            return 0;
+        }
+    }
     if (path == 1) return launch_gemv_norm_shared<1, 8, ADD>(set, first, na, M, K);
     if (path == 2) return launch_gemv_norm_shared<2, 8, ADD>(set, first, na, M, K);
     return launch_gemv_norm_shared<4, 4, ADD>(set, first, na, M, K);
@@ -2153,6 +2254,22 @@ extern "C" int ng_add_rmsnorm_gemm_int8_shared_a(int count, void* normed, void* 
                                                  const int* n, int M, int K) {
     return norm_shared<true>("ng_add_rmsnorm_gemm_int8_shared_a", count, normed, residual_out, c, x, residual_in,
                              norm_weight, eps, b, scales, n, M, K);
+}
+
+extern "C" int ng_rmsnorm_qkv_rope_int8(void* normed, void* q, void* k, void* v, const void* x,
+                                        const void* norm_weight, float eps, const void* const* b,
+                                        const void* const* scales, const int* positions, int M, int hidden,
+                                        int num_q_heads, int num_kv_heads, int head_dim, float rope_theta) {
+    const char* name = "ng_rmsnorm_qkv_rope_int8";
+    NG_REQUIRE(q && k && v && positions && b && scales, "%s: null pointer", name);
+    NG_REQUIRE(num_q_heads > 0 && num_kv_heads > 0 && head_dim > 0 && head_dim % 2 == 0 && head_dim <= 256,
+               "%s: num_q_heads=%d num_kv_heads=%d head_dim=%d (even, at most 256)", name, num_q_heads, num_kv_heads,
+               head_dim);
+    NG_REQUIRE(static_cast<long long>(num_q_heads) * head_dim < (1ll << 31), "%s: too many rows of B", name);
+    void* c[3] = {q, k, v};
+    const int n[3] = {num_q_heads * head_dim, num_kv_heads * head_dim, num_kv_heads * head_dim};
+    const RopeSpec rs{positions, num_q_heads, num_kv_heads, head_dim, rope_theta};
+    return norm_shared<false>(name, 3, normed, nullptr, c, x, nullptr, norm_weight, eps, b, scales, n, M, hidden, &rs);
 }
 
 // gate/up (cuda_gemm_int8 on one A, as ng_gemm_int8_shared_a) and SwiGLU

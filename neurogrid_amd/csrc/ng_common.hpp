@@ -64,6 +64,10 @@ inline hipStream_t stream() { return ng_get_stream(); }
 // Number of compute units of the current device (cached per device id).
 int device_cu_count();
 
+// RoPE's inverse frequencies 1 / theta^(2 i / D), i < D / 2, as every RoPE
+// launch takes them (rope.hip; cached per theta and D).
+void fill_inv_freq(float theta, int D, float* dst);
+
 // Frees every buffer, plan and library handle held by the GEMM entry points
 // (matmul.hip), on every device. cuda_shutdown calls it before it resets the
 // device, which would otherwise leave them pointing at released memory.

@@ -410,7 +410,7 @@ __global__ __launch_bounds__(kRopeThreads) void rope_scalar_kernel(RopeArgs a, i
 }
 
 // inv_freq tables, cached per (theta bits, head_dim): 64 powf calls per miss.
-static void fill_inv_freq(float theta, int D, float* dst) {
+void fill_inv_freq(float theta, int D, float* dst) {
     static std::mutex mu;
     static std::unordered_map<uint64_t, std::vector<float>> cache;
     const uint64_t key = (static_cast<uint64_t>(__builtin_bit_cast(uint32_t, theta)) << 32) |

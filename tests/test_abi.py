@@ -118,6 +118,11 @@ def test_argument_errors_return_minus_one_without_touching_the_gpu(capfd):
     assert L.ng_gemm_int8_silu_mul(p, p, p, p, p, p, p, p, 1, 64, 0) == -1        # N == 0
     assert L.ng_gemm_int8_add(p, p, p, p, p, None, 1, 64, 16) == -1                 # null residual
     assert L.ng_gemm_int8_add(p, p, p, p, p, p, 0, 64, 16) == -1                    # M == 0
+    pv3 = (C.c_void_p * 3)(256, 512, 768)
+    f = C.c_float(1e4)
+    assert L.ng_rmsnorm_qkv_rope_int8(p, p, p, p, p, p, e, pv3, pv3, ip, 1, 64, 2, 1, 3, f) == -1   # odd head_dim
+    assert L.ng_rmsnorm_qkv_rope_int8(p, p, p, p, p, p, e, pv3, pv3, None, 1, 64, 2, 1, 8, f) == -1  # no positions
+    assert L.ng_rmsnorm_qkv_rope_int8(p, p, p, p, p, p, e, pv3, pv3, ip, 1, 64, 2, 1, 512, f) == -1  # head_dim > 256
     err = capfd.readouterr().err
     assert "neurogrid-amd:" in err and "null pointer" in err
 

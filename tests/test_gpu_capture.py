@@ -220,6 +220,14 @@ def _ops():
     add("ng_gemm_int8_silu_mul_M16", {"o": (E2, (16, GN)), "g": (E2, (16, GN)), "u": (E2, (16, GN))},
         lambda L, i, o: L.ng_gemm_int8_silu_mul(o["o"].vp, o["g"].vp, o["u"].vp, i["a16"].vp, i["wq"].vp, i["wsc"].vp,
                                                 i["wq"].vp, i["wsc"].vp, 16, GK, GN))
+    # RMSNorm, q/k/v and RoPE on q and k (heads of 64): one launch at M = 1 (1 token at position 7)
+    add("ng_rmsnorm_qkv_rope_int8_M1", {"n": (E2, (1, GK)), "q": (E2, (1, GN)), "k": (E2, (1, GN)),
+                                        "v": (E2, (1, GN))},
+        lambda L, i, o: L.ng_rmsnorm_qkv_rope_int8(
+            o["n"].vp, o["q"].vp, o["k"].vp, o["v"].vp, i["xh"].vp, i["wh"].vp, EPS,
+            (C.c_void_p * 3)(i["wq"].ptr, i["wq"].ptr, i["wq"].ptr), (C.c_void_p * 3)(i["wsc"].ptr, i["wsc"].ptr,
+                                                                                   i["wsc"].ptr),
+            i["pos"].ip, 1, GK, GN // 64, GN // 64, 64, THETA))
     # a product and the residual add after it: one launch at M = 1, the two calls at M = 16
     add("ng_gemm_int8_add_M1", {"o": (E2, (1, GN)), "c": (E2, (1, GN))},
         lambda L, i, o: L.ng_gemm_int8_add(o["o"].vp, o["c"].vp, i["a1"].vp, i["wq"].vp, i["wsc"].vp, i["xh"].vp,
