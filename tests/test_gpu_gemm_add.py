@@ -83,3 +83,25 @@ def test_gemm_add_consecutive_calls(lib):
     for M, K, N in ((2, 14336, 4096), (1, 2048, 300)):
         p = problem(M, K, N)
         check(run(lib, *p, fused=True), run(lib, *p, fused=False))
+
+
+def test_gemm_add_unaligned_is_the_two_calls(lib):
+    """A and the residual 2 bytes off 16-byte alignment: the two calls, their bits."""
+    banner("gemm_int8_add unaligned A and residual")
+    M, K, N = 1, 4096, 1000
+    a, b, s, res = problem(M, K, N)
+    outs = []
+    for fused in (True, False):
+        ab, rb = empty(a.nbytes + 2), empty(res.nbytes + 2)
+        ab.upload(np.concatenate([np.zeros(1, np.uint16), a.ravel()]))
+        rb.upload(np.concatenate([np.zeros(1, np.uint16), res.ravel()]))
+        bb, sb = dev(b), dev(s)
+        cb, ob = empty(M * N * 2), empty(M * N * 2)
+        if fused:
+            ok(lib.ng_gemm_int8_add(ob.vp, cb.vp, ab.offset(2), bb.vp, sb.vp, rb.offset(2), M, K, N), "ng_gemm_int8_add")
+        else:
+            ok(lib.cuda_gemm_int8(cb.vp, ab.offset(2), bb.vp, sb.vp, M, K, N, True), "cuda_gemm_int8")
+            ok(lib.cuda_add(ob.vp, cb.vp, rb.offset(2), M * N), "cuda_add")
+        outs.append((get(ob, np.uint16, (M, N)), get(cb, np.uint16, (M, N))))
+    assert_bits_equal(outs[0][0], outs[1][0], "out")
+    assert_bits_equal(outs[0][1], outs[1][1], "c")

@@ -99,3 +99,27 @@ def test_silu_mul_consecutive_calls(lib):
     for M, K, N in ((2, 4096, 14336), (1, 2048, 300)):
         p = problem(M, K, N)
         check(run(lib, *p, fused=True), run(lib, *p, fused=False))
+
+
+def test_silu_mul_unaligned_is_the_two_calls(lib):
+    """A 2 bytes off 16-byte alignment: the two calls, their bits."""
+    banner("gemm_int8_silu_mul unaligned A")
+    M, K, N = 2, 4096, 1000
+    a, bg, bu, sg, su = problem(M, K, N)
+    outs = []
+    for fused in (True, False):
+        ab = empty(a.nbytes + 2)
+        ab.upload(np.concatenate([np.zeros(1, np.uint16), a.ravel()]))
+        bgb, bub, sgb, sub = dev(bg), dev(bu), dev(sg), dev(su)
+        gb, ub, ob = empty(M * N * 2), empty(M * N * 2), empty(M * N * 2)
+        if fused:
+            ok(lib.ng_gemm_int8_silu_mul(ob.vp, gb.vp, ub.vp, ab.offset(2), bgb.vp, sgb.vp, bub.vp, sub.vp, M, K, N),
+               "ng_gemm_int8_silu_mul")
+        else:
+            ok(lib.ng_gemm_int8_shared_a(2, (C.c_void_p * 2)(gb.ptr, ub.ptr), ab.offset(2),
+                                         (C.c_void_p * 2)(bgb.ptr, bub.ptr), (C.c_void_p * 2)(sgb.ptr, sub.ptr),
+                                         (C.c_int * 2)(N, N), M, K), "ng_gemm_int8_shared_a")
+            ok(lib.cuda_silu_mul(ob.vp, gb.vp, ub.vp, M * N), "cuda_silu_mul")
+        outs.append([get(x, np.uint16, (M, N)) for x in (ob, gb, ub)])
+    for name, g, w in zip(("out", "gate", "up"), outs[0], outs[1]):
+        assert_bits_equal(g, w, name)

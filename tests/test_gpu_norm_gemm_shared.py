@@ -197,3 +197,39 @@ def test_norm_shared_consecutive_calls(lib):
     for M, K, ns in ((4, 4096, [2048, 1024, 1024]), (1, 2048, [300, 48])):
         x, r, w, qs, scales = problem(M, K, ns)
         check(fused(lib, x, r, w, qs, scales, True), two_calls(lib, x, r, w, qs, scales, True))
+
+
+@pytest.mark.parametrize("add", [False, True], ids=["rmsnorm", "add_rmsnorm"])
+def test_norm_shared_unaligned_is_the_two_calls(lib, add):
+    """x (and the residual) 2 bytes off 16-byte alignment: the two calls, their bits."""
+    banner(f"{'add_' if add else ''}rmsnorm_gemm_int8_shared_a unaligned rows")
+    M, K, ns = 1, 4096, [4096, 1024, 1024]
+    x, r, w, qs, scales = problem(M, K, ns)
+    outs = []
+    for fused_call in (True, False):
+        xb, rb = empty(x.nbytes + 2), empty(r.nbytes + 2)
+        xb.upload(np.concatenate([np.zeros(1, np.uint16), x.ravel()]))
+        rb.upload(np.concatenate([np.zeros(1, np.uint16), r.ravel()]))
+        wb = dev(w)
+        qb, sb = [dev(q) for q in qs], [dev(s) for s in scales]
+        yb, rob = empty(M * K * 2), empty(M * K * 2)
+        cb = [empty(M * n * 2) for n in ns]
+        b3, s3, n3 = ptrs(qb), ptrs(sb), (C.c_int * 3)(*ns)
+        if fused_call and add:
+            ok(lib.ng_add_rmsnorm_gemm_int8_shared_a(3, yb.vp, rob.vp, ptrs(cb), xb.offset(2), rb.offset(2), wb.vp,
+                                                     C.c_float(EPS), b3, s3, n3, M, K), "fused")
+        elif fused_call:
+            ok(lib.ng_rmsnorm_gemm_int8_shared_a(3, yb.vp, ptrs(cb), xb.offset(2), wb.vp, C.c_float(EPS), b3, s3, n3,
+                                                 M, K), "fused")
+        else:
+            if add:
+                ok(lib.cuda_add_rmsnorm(yb.vp, rob.vp, xb.offset(2), rb.offset(2), wb.vp, M, K, C.c_float(EPS)), "norm")
+            else:
+                ok(lib.cuda_rmsnorm(yb.vp, xb.offset(2), wb.vp, M, K, C.c_float(EPS)), "norm")
+            ok(lib.ng_gemm_int8_shared_a(3, ptrs(cb), yb.vp, b3, s3, n3, M, K), "ng_gemm_int8_shared_a")
+        o = [get(yb, np.uint16, (M, K))] + [get(c, np.uint16, (M, n)) for c, n in zip(cb, ns)]
+        if add:
+            o.append(get(rob, np.uint16, (M, K)))
+        outs.append(o)
+    for i, (g, wv) in enumerate(zip(outs[0], outs[1])):
+        assert_bits_equal(g, wv, f"output {i}")

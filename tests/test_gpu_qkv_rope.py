@@ -123,3 +123,31 @@ def test_qkv_rope_consecutive_calls(lib):
         got, want = run(lib, case, True, p), run(lib, case, False, p)
         for k in want:
             assert_bits_equal(got[k], want[k], k)
+
+
+def test_qkv_rope_unaligned_is_the_two_calls(lib):
+    """x 2 bytes off 16-byte alignment: the two calls, their bits."""
+    banner("rmsnorm_qkv_rope_int8 unaligned x")
+    M, hidden, hq, hkv, D, theta = 1, 2048, 32, 4, 64, 1e4
+    x, w, qs, scales = problem(M, hidden, hq, hkv, D)
+    ns = [q.shape[0] for q in qs]
+    outs = []
+    for fused in (True, False):
+        xb = empty(x.nbytes + 2)
+        xb.upload(np.concatenate([np.zeros(1, np.uint16), x.ravel()]))
+        wb, posb = dev(w), dev(np.array([42], np.int32))
+        ip = C.cast(C.c_void_p(posb.ptr), C.POINTER(C.c_int))
+        qb, sb = [dev(q) for q in qs], [dev(s) for s in scales]
+        yb = empty(M * hidden * 2)
+        cb = [empty(M * n * 2) for n in ns]
+        if fused:
+            ok(lib.ng_rmsnorm_qkv_rope_int8(yb.vp, cb[0].vp, cb[1].vp, cb[2].vp, xb.offset(2), wb.vp, C.c_float(EPS),
+                                            ptrs(qb), ptrs(sb), ip, M, hidden, hq, hkv, D, C.c_float(theta)), "fused")
+        else:
+            ok(lib.ng_rmsnorm_gemm_int8_shared_a(3, yb.vp, ptrs(cb), xb.offset(2), wb.vp, C.c_float(EPS), ptrs(qb),
+                                                 ptrs(sb), (C.c_int * 3)(*ns), M, hidden), "norm + q/k/v")
+            ok(lib.ng_rope_qk_with_theta(cb[0].vp, cb[0].vp, cb[1].vp, cb[1].vp, ip, 1, M, hq, hkv, D, 0,
+                                         C.c_float(theta)), "rope")
+        outs.append([get(yb, np.uint16, (M, hidden))] + [get(c, np.uint16, (M, n)) for c, n in zip(cb, ns)])
+    for name, g, wv in zip(("normed", "q", "k", "v"), outs[0], outs[1]):
+        assert_bits_equal(g, wv, name)
