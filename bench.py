@@ -973,7 +973,7 @@ def gemm_add_extras(L, hip, stream, K=14336, N=4096):
 
 
 def int8_decode_layer_extras(L, hip, stream):
-    """One Mistral-7B INT8 layer at decode (M = 1 and 2 tokens), everything
+    """One Mistral-7B INT8 layer at decode (M = 1, 2, 8 and 64 tokens), everything
     but attention, as one graph step on cache-cold weights (a pool of weight
     sets, 218 MB each). engine_us: the engine's own calls
     (gpu/engine/layer.cu:458-598) on this library, 17 launches: copy residual,
@@ -983,8 +983,10 @@ def int8_decode_layer_extras(L, hip, stream):
     ng_rope_qk_with_theta, o, cuda_add_rmsnorm (normed in place, the layer
     input as residual), ng_gemm_int8_silu_mul (in place on gate),
     ng_gemm_int8_add. fused_rope_us: the same with RMSNorm, q/k/v and RoPE in
-    one launch (ng_rmsnorm_qkv_rope_int8), 5 launches. The attention output is
-    a fixed buffer."""
+    one launch (ng_rmsnorm_qkv_rope_int8), 5 launches. From M = 3 on the fused
+    calls are their compositions (norm, then ng_gemm_int8_shared_a, ...), so
+    only the shared-A products and the fused memory-bound entry points remain
+    of the fusion. The attention output is a fixed buffer."""
     rng = np.random.Generator(np.random.PCG64(10))
     H, I, NQ, NKV, D = 4096, 14336, 32, 8, 128
     KV = NKV * D
@@ -1000,7 +1002,7 @@ def int8_decode_layer_extras(L, hip, stream):
     w_attn = DB.from_array(W.round_to(1 + 0.05 * rng.standard_normal(H, dtype=np.float32), "f16"))
     w_ffn = DB.from_array(W.round_to(1 + 0.05 * rng.standard_normal(H, dtype=np.float32), "f16"))
     out = {}
-    for M in (1, 2):
+    for M in (1, 2, 8, 64):
         f16 = lambda *shape: DB.from_array(W.round_to(rng.standard_normal(shape, dtype=np.float32), "f16"))
         x, attn = f16(M, H), f16(M, H)
         pos = DB.from_array(np.arange(100, 100 + M, dtype=np.int32))
@@ -1073,7 +1075,8 @@ def int8_decode_layer_extras(L, hip, stream):
         wbytes = sum(a * b + 4 * a for a, b in shapes.values())
         out[f"M{M}"] = {"engine_us": us_e, "fused_us": us_f, "fused_rope_us": us_r, "weight_bytes": wbytes,
                         "fused_weight_GBps": wbytes / us_r / 1e3, "fused_frac": wbytes / us_r / 1e3 / PEAK_GBPS,
-                        "launches": {"engine": 17, "fused": 6, "fused_rope": 5}, "buffer_sets": n}
+                        "launches": {"engine": 17, "fused": 6 if M <= 2 else None,
+                                     "fused_rope": 5 if M <= 2 else None}, "buffer_sets": n}
         for b_ in (x, attn, pos, normed, res, res2, q, o, out_b, gate, up, k_b, v_b):
             b_.free()
     for name in shapes:
