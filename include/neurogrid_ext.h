@@ -144,11 +144,11 @@ int ng_gemm_int8_shared_a(int count, void* const* c, const void* a, const void* 
 /* cuda_rmsnorm(normed, x, norm_weight, M, K, eps) followed by
  * ng_gemm_int8_shared_a(count, c, normed, b, scales, n, M, K), bit for bit:
  * the engine's INT8 layer normalises its input (gpu/engine/layer.cu:467) and
- * then runs q/k/v on it (:487-501). When every product takes the GEMV kernel
- * with one shape (M <= 4, aligned pointers), K <= 8192 and no output
- * overlaps an input, the norm is folded into the products' launch: each block
- * normalises the rows itself, and normed is still written. Otherwise this is
- * the two calls. Returns 0 or -1. */
+ * then runs q/k/v on it (:487-501). At decode (M <= 2, every product on the
+ * GEMV kernel with one shape, at most 1024 of its blocks of 8 rows, K <= 8192,
+ * aligned pointers, no output overlapping an input) the norm is folded into
+ * the products' launch: each block normalises the rows itself, and normed is
+ * still written. Otherwise this is the two calls. Returns 0 or -1. */
 int ng_rmsnorm_gemm_int8_shared_a(int count, void* normed, void* const* c, const void* x,
                                   const void* norm_weight, float eps, const void* const* b,
                                   const void* const* scales, const int* n, int M, int K);

@@ -536,7 +536,7 @@ __global__ __launch_bounds__(kGvWaves * kWave) void gemv_i8w_add_kernel(uint16_t
 
 // RMSNorm (or residual add + RMSNorm) folded into the shared GEMV launch
 // (ng_rmsnorm_gemm_int8_shared_a, ng_add_rmsnorm_gemm_int8_shared_a), for
-// M <= 4 rows of K <= 8192. Every block normalises the rows itself, and each
+// M <= 2 rows of K <= 8192. Every block normalises the rows itself, and each
 // thread normalises exactly the 16-value pieces of A that its lane multiplies
 // in the GEMV (segment sg = wave + 4 s, values 16 lane .. 16 lane + 15), so A
 // stays in registers: the thread loads its pieces of x (and the residual) and
@@ -822,7 +822,10 @@ constexpr int kNormSharedMaxK = 2 * kGvWaves * kGvSeg;
 // norm in saves its launch and its latency; with more blocks the launch is
 // bound by the codes in flight, and the two calls are faster (measured on
 // MI355X at Mistral-7B: q/k/v, 768 blocks, 7.2 against 8.3 us at one token;
-// gate/up, 3584 blocks, 23.1 against 21.8 us).
+// gate/up, 3584 blocks, 23.1 against 21.8 us). Only the GEMV shapes of one
+// and two rows (8 rows of B per block) are folded: with four rows the fused
+// kernel was slower at every block count measured (TinyLlama's q/k/v, 640
+// blocks, 3 rows: 7.9 against 6.4 us).
 constexpr int kNormSharedMaxBlocks = 1024;
 
 template <int MR, int R, bool ADD>
@@ -2137,15 +2140,14 @@ static bool overlaps(const void* p, size_t pn, const void* q, size_t qn) {
 
 // RMSNorm (ADD: residual add + RMSNorm) of A, then the products that share
 // the normalised A: one launch of gemv_i8w_norm_shared_kernel when every
-// product takes the same GEMV shape, K <= 8192, the launch has at most
-// kNormSharedMaxBlocks blocks and no output overlaps an input (the kernel's
+// product takes the same GEMV shape of one or two rows, K <= 8192, the launch
+// has at most kNormSharedMaxBlocks blocks and no output overlaps an input (the kernel's
 // blocks read the inputs while the first one stores); otherwise the norm
 // entry point followed by ng_gemm_int8_shared_a.
 // The same bits either way. With rs, RoPE (ng_rope_qk_with_theta, style 0)
-// follows on products 0 and 1 in place; the fused launch then also needs the
-// GEMV shape of one or two rows (8 rows of B per block), D a multiple of 8,
-// the three outputs apart from each other and the positions apart from every
-// output.
+// follows on products 0 and 1 in place; the fused launch then also needs D a
+// multiple of 8 (four rotation pairs per block of 8 rows of B), the three
+// outputs apart from each other and the positions apart from every output.
 struct RopeSpec {
     const int* pos;
     int nq, nkv, D;
@@ -2189,12 +2191,13 @@ static int norm_shared(const char* name, int count, void* normed, void* res_out,
         }
     }
     // GEMV blocks of the fused launch (rows of B per block as the GEMV kernel's).
-    const int R = path == 3 ? 4 : 8;
+    const int R = 8;
     long long blocks = 0;
     for (int i = 0; i < count; ++i) blocks += (n[i] + R - 1) / R;
-    const bool fused = path >= 1 && apart && K <= kNormSharedMaxK && blocks <= kNormSharedMaxBlocks && aligned16(x) &&
-                       aligned16(w) && aligned16(normed) && (!ADD || (aligned16(res) && aligned16(res_out))) &&
-                       (!rs || (path <= 2 && rs->D % 8 == 0 && rs->D <= 2 * kRopeEpiMaxHalf));
+    const bool fused = (path == 1 || path == 2) && apart && K <= kNormSharedMaxK && blocks <= kNormSharedMaxBlocks &&
+                       aligned16(x) && aligned16(w) && aligned16(normed) &&
+                       (!ADD || (aligned16(res) && aligned16(res_out))) &&
+                       (!rs || (rs->D % 8 == 0 && rs->D <= 2 * kRopeEpiMaxHalf));
     if (!fused) {
         int r = ADD ? cuda_add_rmsnorm(normed, res_out, x, res, w, M, K, eps) : cuda_rmsnorm(normed, x, w, M, K, eps);
         if (r == 0) r = ng_gemm_int8_shared_a(count, c, normed, b, scales, n, M, K);
@@ -2237,8 +2240,7 @@ static int norm_shared(const char* name, int count, void* normed, void* res_out,
         }
     }
     if (path == 1) return launch_gemv_norm_shared<1, 8, ADD>(set, first, na, M, K);
-    if (path == 2) return launch_gemv_norm_shared<2, 8, ADD>(set, first, na, M, K);
-    return launch_gemv_norm_shared<4, 4, ADD>(set, first, na, M, K);
+    return launch_gemv_norm_shared<2, 8, ADD>(set, first, na, M, K);
 }
 
 extern "C" int ng_rmsnorm_gemm_int8_shared_a(int count, void* normed, void* const* c, const void* x,

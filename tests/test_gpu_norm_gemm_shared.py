@@ -3,9 +3,10 @@
 Bar: normed, residual_out and every C_i are bit-identical to the two calls
 they replace, cuda_rmsnorm (cuda_add_rmsnorm) and then ng_gemm_int8_shared_a
 on the normalised rows, on the same inputs. That holds both in the fused
-launch (every product on the GEMV kernel with one shape, K <= 8192, at most
-1024 blocks, outputs apart from inputs) and where the call is the two calls
-(more blocks, M > 4, K past 8192, mixed shapes, in-place buffers). The two calls are pinned
+launch (one or two rows, every product on the GEMV kernel with one shape,
+K <= 8192, at most 1024 blocks, outputs apart from inputs) and where the call
+is the two calls (three or more rows, more blocks, K past 8192, mixed shapes,
+in-place buffers). The two calls are pinned
 elsewhere (the norms against the oracle, the shared products against
 cuda_gemm_int8); normed is also checked against the oracle here. Rows whose
 sum of squares sits on an fp32 rounding boundary take the norm's exact limb
@@ -24,29 +25,31 @@ pytestmark = pytest.mark.gpu
 RNG = np.random.Generator(np.random.PCG64(53))
 EPS = 1e-5
 
-# The fused launch takes every product on the GEMV kernel with one shape, K
-# <= 8192 and at most 1024 blocks (8 rows of B per block at M <= 2, 4 at M =
-# 3-4). FUSED: q/k/v at Mistral-7B (768 blocks) at 1-2 tokens, and at 3-4
-# tokens with fewer rows; K of one segment per wave (K <= 4096) and of two (up
-# to 8192, one wave with a single segment at K = 6160), waves with no segment
-# (K = 2064, 16), ragged K and rows of B, exactly 1024 blocks. TWO_CALLS:
-# more blocks (q/k/v at 3-4 tokens, gate/up, Llama-2-13B's q/k/v), K past
-# 8192, M > 4, products of two GEMV shapes, K not a multiple of 16.
+# The fused launch takes one or two rows, every product on the GEMV kernel
+# with one shape, K <= 8192 and at most 1024 blocks of 8 rows of B. FUSED:
+# q/k/v at Mistral-7B (768 blocks), Llama-2-13B widths with fewer rows, K of
+# one segment per wave (K <= 4096) and of two (up to 8192, one wave with a
+# single segment at K = 6160), waves with no segment (K = 2064, 16), ragged K
+# and rows of B. TWO_CALLS: three or four rows, more blocks (gate/up,
+# Llama-2-13B's q/k/v), K past 8192, M > 4, products of two GEMV shapes, K not
+# a multiple of 16.
 FUSED = [
     (1, 4096, [4096, 1024, 1024]),
     (2, 4096, [4096, 1024, 1024]),
-    (3, 4096, [1024, 1024]),
-    (4, 4096, [2048, 1024, 1024]),
     (1, 5120, [4096, 1024, 1024]),
-    (4, 5120, [1024, 1024, 1024]),
+    (2, 5120, [1024, 1024, 1024]),
     (1, 8192, [4096, 1000]),
     (2, 8192, [3000, 4096]),
-    (3, 6160, [1000, 77]),
+    (2, 6160, [1000, 77]),
     (1, 4112, [1000, 333, 7, 64]),
-    (3, 2064, [17, 1, 40]),
+    (2, 2064, [17, 1, 40]),
     (1, 16, [5, 9]),
 ]
 TWO_CALLS = [
+    (3, 4096, [1024, 1024]),
+    (4, 4096, [2048, 1024, 1024]),
+    (4, 5120, [1024, 1024, 1024]),
+    (3, 6160, [1000, 77]),
     (4, 4096, [4096, 1024, 1024]),
     (1, 4096, [14336, 14336]),
     (2, 4096, [14336, 14336]),
@@ -194,7 +197,7 @@ def test_norm_shared_in_place(lib, M, K, ns, add):
 
 def test_norm_shared_consecutive_calls(lib):
     banner("add_rmsnorm_gemm_int8_shared_a: a call, then a smaller one")
-    for M, K, ns in ((4, 4096, [2048, 1024, 1024]), (1, 2048, [300, 48])):
+    for M, K, ns in ((2, 4096, [2048, 1024, 1024]), (1, 2048, [300, 48])):
         x, r, w, qs, scales = problem(M, K, ns)
         check(fused(lib, x, r, w, qs, scales, True), two_calls(lib, x, r, w, qs, scales, True))
 
