@@ -34,6 +34,7 @@ Usage: python bench.py [--gpus 1] [--steps 50] [--warmup 5] [--no-cpu] [--no-ext
        python bench.py --profile-pass  (eager launches of every kernel for rocprofv3: the kernel trace and
                                         the --pmc FETCH_SIZE / WRITE_SIZE runs)
        python bench.py --gemm-only  (cuda_gemm_int8 timings only)
+       python bench.py --decode-only  (the INT8 layer's fused decode entry points and the decode layer only)
        python bench.py --floors-only  (the access-pattern floor kernels only)
 """
 from __future__ import annotations
@@ -1643,6 +1644,8 @@ def main():
                     help="eager launches of every kernel for rocprofv3 (kernel trace and --pmc runs)")
     ap.add_argument("--gemm-only", action="store_true",
                     help="time only cuda_gemm_int8 at Mistral-7B's INT8 projections and print that JSON")
+    ap.add_argument("--decode-only", action="store_true",
+                    help="time only the fused decode entry points and the INT8 decode layer, print that JSON")
     ap.add_argument("--floors-only", action="store_true",
                     help="time only the access-pattern floor kernels and print that JSON")
     args = ap.parse_args()
@@ -1659,6 +1662,12 @@ def main():
     L.ng_set_stream(stream)
     if args.profile_pass:
         profile_pass(L, hip, stream)
+        return
+    if args.decode_only:
+        print(json.dumps({"norm_gemm_int8_shared_a": norm_shared_extras(L, hip, stream),
+                          "gemm_int8_silu_mul": silu_mul_gemm_extras(L, hip, stream),
+                          "gemm_int8_add": gemm_add_extras(L, hip, stream),
+                          "int8_decode_layer": int8_decode_layer_extras(L, hip, stream)}), flush=True)
         return
     if args.gemm_only:
         print(json.dumps({"gemm_int8": gemm_extras(L, hip, stream),
