@@ -35,6 +35,7 @@ Usage: python bench.py [--gpus 1] [--steps 50] [--warmup 5] [--no-cpu] [--no-ext
                                         the --pmc FETCH_SIZE / WRITE_SIZE runs)
        python bench.py --gemm-only  (cuda_gemm_int8 timings only)
        python bench.py --decode-only  (the INT8 layer's fused decode entry points and the decode layer only)
+       python bench.py --profile-decode  (eager launches of the decode steps, fused and unfused, for rocprofv3)
        python bench.py --floors-only  (the access-pattern floor kernels only)
 """
 from __future__ import annotations
@@ -1537,6 +1538,84 @@ def profile_pass(L, hip, stream):
     log("profile pass done")
 
 
+def profile_decode(L, hip, stream):
+    """Eager launches (no graph, no device copies) of the INT8 layer's decode
+    steps at Mistral-7B and one token, for a rocprofv3 kernel trace: the fused
+    entry points (ng_rmsnorm_qkv_rope_int8, ng_gemm_int8_silu_mul,
+    ng_gemm_int8_add; one dispatch per call) and the calls they replace
+    (cuda_rmsnorm, ng_gemm_int8_shared_a on q/k/v, ng_rope_qk_with_theta,
+    gate/up through ng_gemm_int8_shared_a, cuda_silu_mul, cuda_gemm_int8 on
+    down, cuda_add), plus o (cuda_gemm_int8) and cuda_add_rmsnorm. Two weight
+    sets, uploaded from the host (436 MB, above the 256 MB Infinity Cache),
+    alternate between launches. Before each group a line "[profile] <label>
+    warmup=<w> dispatches=<n>" goes to stderr."""
+    rng = np.random.Generator(np.random.PCG64(11))
+    H, I, NQ, NKV, D, M = 4096, 14336, 32, 8, 128, 1
+    KV = NKV * D
+    eps, theta = C.c_float(1e-5), C.c_float(1e6)
+    shapes = {"q": (H, H), "k": (KV, H), "v": (KV, H), "o": (H, H), "gate": (I, H), "up": (I, H), "down": (H, I)}
+    sets = []
+    for _ in range(2):
+        ws = {}
+        for name, (N, K) in shapes.items():
+            ws[name] = (DB.from_array(rng.integers(-128, 128, (N, K)).astype(np.int8)),
+                        DB.from_array(rng.uniform(1e-3, 1e-2, N).astype(np.float32)))
+        sets.append(ws)
+    f16 = lambda *shape: DB.from_array(W.round_to(rng.standard_normal(shape, dtype=np.float32), "f16"))
+    x, attn, res = f16(M, H), f16(M, H), f16(M, H)
+    w_attn = DB.from_array(W.round_to(1 + 0.05 * rng.standard_normal(H, dtype=np.float32), "f16"))
+    pos = DB.from_array(np.array([100], np.int32))
+    normed, q, o, out, res2 = (DB(2 * M * H) for _ in range(5))
+    kb, vb = DB(2 * M * KV), DB(2 * M * KV)
+    gate, up, sw = DB(2 * M * I), DB(2 * M * I), DB(2 * M * I)
+    qkv_c = (C.c_void_p * 3)(q.ptr, kb.ptr, vb.ptr)
+    qkv_n = (C.c_int * 3)(H, KV, KV)
+    gu_n = (C.c_int * 2)(I, I)
+
+    def qkv_w(ws):
+        return (C.c_void_p * 3)(ws["q"][0].ptr, ws["k"][0].ptr, ws["v"][0].ptr)
+
+    def qkv_s(ws):
+        return (C.c_void_p * 3)(ws["q"][1].ptr, ws["k"][1].ptr, ws["v"][1].ptr)
+
+    groups = [
+        ("rmsnorm_qkv_rope_int8", 1, lambda ws: L.ng_rmsnorm_qkv_rope_int8(
+            normed.vp, q.vp, kb.vp, vb.vp, x.vp, w_attn.vp, eps, qkv_w(ws), qkv_s(ws), pos.ip, M, H, NQ, NKV, D,
+            theta)),
+        ("rmsnorm", 1, lambda ws: L.cuda_rmsnorm(normed.vp, x.vp, w_attn.vp, M, H, eps)),
+        ("qkv_shared_a", 1, lambda ws: L.ng_gemm_int8_shared_a(3, qkv_c, normed.vp, qkv_w(ws), qkv_s(ws), qkv_n, M,
+                                                                H)),
+        ("rope_qk", 1, lambda ws: L.ng_rope_qk_with_theta(q.vp, q.vp, kb.vp, kb.vp, pos.ip, 1, M, NQ, NKV, D, 0,
+                                                          theta)),
+        ("o", 1, lambda ws: L.cuda_gemm_int8(o.vp, attn.vp, ws["o"][0].vp, ws["o"][1].vp, M, H, H, True)),
+        ("add_rmsnorm", 1, lambda ws: L.cuda_add_rmsnorm(normed.vp, res2.vp, o.vp, x.vp, w_attn.vp, M, H, eps)),
+        ("gate_up_silu_mul", 1, lambda ws: L.ng_gemm_int8_silu_mul(sw.vp, gate.vp, up.vp, normed.vp, ws["gate"][0].vp,
+                                                                   ws["gate"][1].vp, ws["up"][0].vp, ws["up"][1].vp,
+                                                                   M, H, I)),
+        ("gate_up_shared_a", 1, lambda ws: L.ng_gemm_int8_shared_a(
+            2, (C.c_void_p * 2)(gate.ptr, up.ptr), normed.vp, (C.c_void_p * 2)(ws["gate"][0].ptr, ws["up"][0].ptr),
+            (C.c_void_p * 2)(ws["gate"][1].ptr, ws["up"][1].ptr), gu_n, M, H)),
+        ("silu_mul", 1, lambda ws: L.cuda_silu_mul(sw.vp, gate.vp, up.vp, M * I)),
+        ("down_add", 1, lambda ws: L.ng_gemm_int8_add(out.vp, o.vp, sw.vp, ws["down"][0].vp, ws["down"][1].vp,
+                                                      res.vp, M, I, H)),
+        ("down", 1, lambda ws: L.cuda_gemm_int8(o.vp, sw.vp, ws["down"][0].vp, ws["down"][1].vp, M, I, H, True)),
+        ("add", 1, lambda ws: L.cuda_add(out.vp, o.vp, res.vp, M * H)),
+    ]
+    for label, per_call, fn in groups:
+        seq = [sets[i % 2] for i in range(PROFILE_WARMUP + PROFILE_LAUNCHES)]
+        log_profile(f"mistral7b_int8_decode_M1/{label}", PROFILE_LAUNCHES * per_call, PROFILE_WARMUP * per_call)
+        for ws in seq:
+            if fn(ws) != 0:
+                raise RuntimeError(f"{label} failed")
+        hip.sync()
+    for ws in sets:
+        for wq, sc in ws.values():
+            wq.free()
+            sc.free()
+    for b_ in (x, attn, res, w_attn, pos, normed, q, o, out, res2, kb, vb, gate, up, sw):
+        b_.free()
+
+
 def log_profile(label, dispatches, warmup):
     print(f"[profile] {label} warmup={warmup} dispatches={dispatches}", file=sys.stderr, flush=True)
 
@@ -1644,6 +1723,8 @@ def main():
                     help="eager launches of every kernel for rocprofv3 (kernel trace and --pmc runs)")
     ap.add_argument("--gemm-only", action="store_true",
                     help="time only cuda_gemm_int8 at Mistral-7B's INT8 projections and print that JSON")
+    ap.add_argument("--profile-decode", action="store_true",
+                    help="eager launches of the INT8 layer's decode steps (fused and unfused) for rocprofv3")
     ap.add_argument("--decode-only", action="store_true",
                     help="time only the fused decode entry points and the INT8 decode layer, print that JSON")
     ap.add_argument("--floors-only", action="store_true",
@@ -1662,6 +1743,9 @@ def main():
     L.ng_set_stream(stream)
     if args.profile_pass:
         profile_pass(L, hip, stream)
+        return
+    if args.profile_decode:
+        profile_decode(L, hip, stream)
         return
     if args.decode_only:
         print(json.dumps({"norm_gemm_int8_shared_a": norm_shared_extras(L, hip, stream),
