@@ -2267,7 +2267,9 @@ extern "C" int ng_rmsnorm_qkv_rope_int8(void* normed, void* q, void* k, void* v,
     NG_REQUIRE(num_q_heads > 0 && num_kv_heads > 0 && head_dim > 0 && head_dim % 2 == 0 && head_dim <= 256,
                "%s: num_q_heads=%d num_kv_heads=%d head_dim=%d (even, at most 256)", name, num_q_heads, num_kv_heads,
                head_dim);
-    NG_REQUIRE(static_cast<long long>(num_q_heads) * head_dim < (1ll << 31), "%s: too many rows of B", name);
+    NG_REQUIRE(static_cast<long long>(num_q_heads) * head_dim < (1ll << 31) &&
+                   static_cast<long long>(num_kv_heads) * head_dim < (1ll << 31),
+               "%s: too many rows of B", name);
     void* c[3] = {q, k, v};
     const int n[3] = {num_q_heads * head_dim, num_kv_heads * head_dim, num_kv_heads * head_dim};
     const RopeSpec rs{positions, num_q_heads, num_kv_heads, head_dim, rope_theta};

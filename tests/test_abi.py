@@ -123,6 +123,7 @@ def test_argument_errors_return_minus_one_without_touching_the_gpu(capfd):
     assert L.ng_rmsnorm_qkv_rope_int8(p, p, p, p, p, p, e, pv3, pv3, ip, 1, 64, 2, 1, 3, f) == -1   # odd head_dim
     assert L.ng_rmsnorm_qkv_rope_int8(p, p, p, p, p, p, e, pv3, pv3, None, 1, 64, 2, 1, 8, f) == -1  # no positions
     assert L.ng_rmsnorm_qkv_rope_int8(p, p, p, p, p, p, e, pv3, pv3, ip, 1, 64, 2, 1, 512, f) == -1  # head_dim > 256
+    assert L.ng_rmsnorm_qkv_rope_int8(p, p, p, p, p, p, e, pv3, pv3, ip, 1, 64, 2, 1 << 24, 256, f) == -1  # kv rows
     err = capfd.readouterr().err
     assert "neurogrid-amd:" in err and "null pointer" in err
 
