@@ -937,8 +937,9 @@ def silu_mul_gemm_extras(L, hip, stream, K=4096, N=14336):
 
 def gemm_add_extras(L, hip, stream, K=14336, N=4096):
     """Mistral-7B's down projection and the layer's final residual add
-    (layer.cu:593-598) at M = 1, 2 and 4 tokens. us: ng_gemm_int8_add (one
-    launch on the GEMV kernel's shapes, M <= 2 here); two_calls_us:
+    (layer.cu:593-598) at M = 1, 2, 4, 8 and 64 tokens. us: ng_gemm_int8_add
+    (one launch on the GEMV kernel's shapes, M <= 2 here; from 3 tokens the
+    split kernel with the add in its reduction); two_calls_us:
     cuda_gemm_int8, then cuda_add. Both give the same bits; weight pools keep
     the codes cache-cold."""
     rng = np.random.Generator(np.random.PCG64(9))
@@ -948,7 +949,7 @@ def gemm_add_extras(L, hip, stream, K=14336, N=4096):
     del wq
     sc = DB.from_array(rng.uniform(1e-3, 1e-2, N).astype(np.float32))
     out = {}
-    for M in (1, 2, 4):
+    for M in (1, 2, 4, 8, 64):
         ab = DB.from_array(W.round_to(rng.standard_normal((M, K), dtype=np.float32), "f16"))
         rb = DB.from_array(W.round_to(rng.standard_normal((M, N), dtype=np.float32), "f16"))
         cb, ob = Pool(hip, 2 * M * N, n), Pool(hip, 2 * M * N, n)

@@ -1138,9 +1138,18 @@ __global__ __launch_bounds__(G * W * kWave) void gemm_i8w_split_shared_kernel(Sh
 // slice is loaded before the first addition (slices past S reload slice 0),
 // so the loads overlap: 1.3-1.5 us faster than a loop of dependent loads
 // with 8 slices.
-template <bool VEC4>
-__device__ __forceinline__ void split_reduce_block(uint16_t* __restrict__ c, const float* __restrict__ part,
-                                                   const float* __restrict__ scale, int M, int N, int S, int blk) {
+// The residual add after a product (ng_gemm_int8_add): out = fp16(C + res) on
+// the rounded C, as cuda_add computes it. out may be C or res itself (each
+// element is read and written by one thread, out last).
+struct ResEpi {
+    uint16_t* out;
+    const uint16_t* res;
+};
+
+template <bool VEC4, bool RES = false>
+__device__ __forceinline__ void split_reduce_block(uint16_t* c, const float* __restrict__ part,
+                                                   const float* __restrict__ scale, int M, int N, int S, int blk,
+                                                   const ResEpi& ep = ResEpi{}) {
     const size_t mn = static_cast<size_t>(M) * N;
     const size_t t = static_cast<size_t>(blk) * 256 + threadIdx.x;
     if (VEC4) {
@@ -1156,7 +1165,17 @@ __device__ __forceinline__ void split_reduce_block(uint16_t* __restrict__ c, con
             if (q < S) v += pv[q];
         const f32x4 sc = *reinterpret_cast<const f32x4*>(scale + i % N);
         const u32x2 out = {pack2<f16>(v[0] * sc[0], v[1] * sc[1]), pack2<f16>(v[2] * sc[2], v[3] * sc[3])};
-        *reinterpret_cast<u32x2*>(c + i) = out;
+        if (RES) {
+            const u32x2 rv = *reinterpret_cast<const u32x2*>(ep.res + i);
+            *reinterpret_cast<u32x2*>(c + i) = out;
+            u32x2 sum;
+#pragma unroll
+            for (int h = 0; h < 2; ++h)
+                sum[h] = pack2<f16>(el_add<f16, 0>(out[h], rv[h]), el_add<f16, 1>(out[h], rv[h]));
+            *reinterpret_cast<u32x2*>(ep.out + i) = sum;
+        } else {
+            *reinterpret_cast<u32x2*>(c + i) = out;
+        }
     } else {
         if (t >= mn) return;
         float pv[8];
@@ -1166,14 +1185,22 @@ __device__ __forceinline__ void split_reduce_block(uint16_t* __restrict__ c, con
 #pragma unroll
         for (int q = 1; q < 8; ++q)
             if (q < S) v += pv[q];
-        c[t] = from_f32<f16>(v * scale[t % N]);
+        const uint16_t cv = from_f32<f16>(v * scale[t % N]);
+        if (RES) {
+            const float sum = to_f32<f16>(cv) + to_f32<f16>(ep.res[t]);
+            c[t] = cv;
+            ep.out[t] = from_f32<f16>(sum);
+        } else {
+            c[t] = cv;
+        }
     }
 }
 
-template <bool VEC4>
-__global__ __launch_bounds__(256) void split_reduce_kernel(uint16_t* __restrict__ c, const float* __restrict__ part,
-                                                           const float* __restrict__ scale, int M, int N, int S) {
-    split_reduce_block<VEC4>(c, part, scale, M, N, S, blockIdx.x);
+template <bool VEC4, bool RES = false>
+__global__ __launch_bounds__(256) void split_reduce_kernel(uint16_t* c, const float* __restrict__ part,
+                                                           const float* __restrict__ scale, int M, int N, int S,
+                                                           ResEpi ep = ResEpi{}) {
+    split_reduce_block<VEC4, RES>(c, part, scale, M, N, S, blockIdx.x, ep);
 }
 
 // The reductions of the products of gemm_i8w_split_shared_kernel in one
@@ -1628,14 +1655,18 @@ int partial_buffer(hipStream_t s, int S, int M, int N, int K, float* scratch, si
 }
 
 // C = fp16(scale[n] * sum of the S slices of part), slices added in order.
-int launch_reduce(hipStream_t s, uint16_t* c, const float* part, const float* scale, int M, int N, int S) {
+int launch_reduce(hipStream_t s, uint16_t* c, const float* part, const float* scale, int M, int N, int S,
+                  const ResEpi* ep = nullptr) {
     const size_t mn = static_cast<size_t>(M) * N;
-    if (N % 4 == 0 && aligned16(scale) && aligned8(c))
-        split_reduce_kernel<true><<<dim3(static_cast<unsigned>((mn / 4 + 255) / 256)), dim3(256), 0, s>>>(
-            c, part, scale, M, N, S);
-    else
-        split_reduce_kernel<false><<<dim3(static_cast<unsigned>((mn + 255) / 256)), dim3(256), 0, s>>>(
-            c, part, scale, M, N, S);
+    const dim3 b4(static_cast<unsigned>((mn / 4 + 255) / 256)), b1(static_cast<unsigned>((mn + 255) / 256));
+    const bool vec4 = N % 4 == 0 && aligned16(scale) && aligned8(c) && (!ep || (aligned8(ep->out) && aligned8(ep->res)));
+    if (ep) {
+        if (vec4) split_reduce_kernel<true, true><<<b4, dim3(256), 0, s>>>(c, part, scale, M, N, S, *ep);
+        else split_reduce_kernel<false, true><<<b1, dim3(256), 0, s>>>(c, part, scale, M, N, S, *ep);
+    } else {
+        if (vec4) split_reduce_kernel<true><<<b4, dim3(256), 0, s>>>(c, part, scale, M, N, S);
+        else split_reduce_kernel<false><<<b1, dim3(256), 0, s>>>(c, part, scale, M, N, S);
+    }
     NG_CHECK_LAUNCH("cuda_gemm_int8");
     return 0;
 }
@@ -1655,7 +1686,7 @@ void split_slices(int tiles, int TT, int G, int K, int& S, int& cps) {
 
 template <int MT, int W, int G>
 int launch_split(uint16_t* c, const uint16_t* a, const int8_t* b, const float* scale, int M, int N, int K,
-                 float* scratch, size_t scratch_bytes, int TT = 1) {
+                 float* scratch, size_t scratch_bytes, int TT = 1, const ResEpi* ep = nullptr) {
     const int tiles = (N + 16 * W - 1) / (16 * W);
     int S = 0, cps = 0;
     split_slices(tiles, TT, G, K, S, cps);
@@ -1671,7 +1702,8 @@ int launch_split(uint16_t* c, const uint16_t* a, const int8_t* b, const float* s
     gemm_i8w_split_kernel<MT, W, G><<<dim3(static_cast<unsigned>(blocks)), dim3(G * W * kWave), 0, s>>>(
         c, a, b, scale, part, M, N, K, S, tiles, cps, TT);
     NG_CHECK_LAUNCH("cuda_gemm_int8");
-    return S > 1 ? launch_reduce(s, c, part, scale, M, N, S) : 0;
+    if (S > 1) return launch_reduce(s, c, part, scale, M, N, S, ep);
+    return ep ? cuda_add(ep->out, c, ep->res, static_cast<size_t>(M) * N) : 0;
 }
 
 // The GEMV kernel gemm_i8w runs for a product on the weight-streaming path:
@@ -1730,32 +1762,38 @@ int shared_path(int M, int K, int N) {
 // 14.8 us for gate/up, 13.7 vs 15.5 us for down), with token tiles of 32 rows
 // of A for N <= 2048 from M = 33 on, otherwise the MFMA kernel that reads A
 // from L2 directly.
+// With ep, the residual add after the product follows: in the split-K
+// reduction's epilogue where the launch has several K slices, else as
+// cuda_add.
 int gemm_i8w(void* c, const void* a, const void* b, const void* scale, int M, int K, int N,
-             float* scratch = nullptr, size_t scratch_bytes = 0) {
+             float* scratch = nullptr, size_t scratch_bytes = 0, const ResEpi* ep = nullptr) {
     auto* cp = static_cast<uint16_t*>(c);
     auto* ap = static_cast<const uint16_t*>(a);
     auto* bp = static_cast<const int8_t*>(b);
     auto* sp = static_cast<const float*>(scale);
+    const auto then_add = [&](int r) {
+        return r != 0 || !ep ? r : cuda_add(ep->out, c, ep->res, static_cast<size_t>(M) * N);
+    };
     switch (gemv_shape(M, K, N)) {
-        case 1: return launch_gemv<1, 8>(cp, ap, bp, sp, M, N, K);
-        case 2: return launch_gemv<2, 8>(cp, ap, bp, sp, M, N, K);
-        case 3: return launch_gemv<4, 4>(cp, ap, bp, sp, M, N, K);
+        case 1: return then_add(launch_gemv<1, 8>(cp, ap, bp, sp, M, N, K));
+        case 2: return then_add(launch_gemv<2, 8>(cp, ap, bp, sp, M, N, K));
+        case 3: return then_add(launch_gemv<4, 4>(cp, ap, bp, sp, M, N, K));
         default: break;
     }
     switch (split_config(M, K, N)) {
-        case kSplitTokenTiles: return launch_split<2, 4, 1>(cp, ap, bp, sp, M, N, K, scratch, scratch_bytes, (M + 31) / 32);
-        case kSplit881: return launch_split<8, 8, 1>(cp, ap, bp, sp, M, N, K, scratch, scratch_bytes);
-        case kSplit842: return launch_split<8, 4, 2>(cp, ap, bp, sp, M, N, K, scratch, scratch_bytes);
-        case kSplit841: return launch_split<8, 4, 1>(cp, ap, bp, sp, M, N, K, scratch, scratch_bytes);
-        case kSplit481: return launch_split<4, 8, 1>(cp, ap, bp, sp, M, N, K, scratch, scratch_bytes);
-        case kSplit442: return launch_split<4, 4, 2>(cp, ap, bp, sp, M, N, K, scratch, scratch_bytes);
-        case kSplit441: return launch_split<4, 4, 1>(cp, ap, bp, sp, M, N, K, scratch, scratch_bytes);
-        case kSplit281: return launch_split<2, 8, 1>(cp, ap, bp, sp, M, N, K, scratch, scratch_bytes);
-        case kSplit242: return launch_split<2, 4, 2>(cp, ap, bp, sp, M, N, K, scratch, scratch_bytes);
-        case kSplit241: return launch_split<2, 4, 1>(cp, ap, bp, sp, M, N, K, scratch, scratch_bytes);
-        case kSplit142: return launch_split<1, 4, 2>(cp, ap, bp, sp, M, N, K, scratch, scratch_bytes);
-        case kSplit141: return launch_split<1, 4, 1>(cp, ap, bp, sp, M, N, K, scratch, scratch_bytes);
-        default: return launch_i8w<1, 1, 8, 4>(cp, ap, bp, sp, M, N, K);
+        case kSplitTokenTiles: return launch_split<2, 4, 1>(cp, ap, bp, sp, M, N, K, scratch, scratch_bytes, (M + 31) / 32, ep);
+        case kSplit881: return launch_split<8, 8, 1>(cp, ap, bp, sp, M, N, K, scratch, scratch_bytes, 1, ep);
+        case kSplit842: return launch_split<8, 4, 2>(cp, ap, bp, sp, M, N, K, scratch, scratch_bytes, 1, ep);
+        case kSplit841: return launch_split<8, 4, 1>(cp, ap, bp, sp, M, N, K, scratch, scratch_bytes, 1, ep);
+        case kSplit481: return launch_split<4, 8, 1>(cp, ap, bp, sp, M, N, K, scratch, scratch_bytes, 1, ep);
+        case kSplit442: return launch_split<4, 4, 2>(cp, ap, bp, sp, M, N, K, scratch, scratch_bytes, 1, ep);
+        case kSplit441: return launch_split<4, 4, 1>(cp, ap, bp, sp, M, N, K, scratch, scratch_bytes, 1, ep);
+        case kSplit281: return launch_split<2, 8, 1>(cp, ap, bp, sp, M, N, K, scratch, scratch_bytes, 1, ep);
+        case kSplit242: return launch_split<2, 4, 2>(cp, ap, bp, sp, M, N, K, scratch, scratch_bytes, 1, ep);
+        case kSplit241: return launch_split<2, 4, 1>(cp, ap, bp, sp, M, N, K, scratch, scratch_bytes, 1, ep);
+        case kSplit142: return launch_split<1, 4, 2>(cp, ap, bp, sp, M, N, K, scratch, scratch_bytes, 1, ep);
+        case kSplit141: return launch_split<1, 4, 1>(cp, ap, bp, sp, M, N, K, scratch, scratch_bytes, 1, ep);
+        default: return then_add(launch_i8w<1, 1, 8, 4>(cp, ap, bp, sp, M, N, K));
     }
 }
 
@@ -2320,10 +2358,12 @@ extern "C" int ng_gemm_int8_silu_mul(void* out, void* gate, void* up, const void
 }
 
 // A product (cuda_gemm_int8 with transpose_b) and the residual add after it
-// (cuda_add(out, c, residual)): one launch of gemv_i8w_add_kernel on the GEMV
-// kernel's shapes when no output overlaps an input or the other output (out
-// may be c or the residual exactly); otherwise the two calls. The same bits
-// either way.
+// (cuda_add(out, c, residual)): when no output overlaps an input or the other
+// output (out may be c or the residual exactly), one launch of
+// gemv_i8w_add_kernel on the GEMV kernel's shapes, and up to 128 rows the
+// weight-streaming kernels with the add in the split-K reduction (after the
+// product as cuda_add where the launch has one K slice); otherwise the two
+// calls. The same bits either way.
 extern "C" int ng_gemm_int8_add(void* out, void* c, const void* a, const void* b, const void* scale,
                                 const void* residual, int M, int K, int N) {
     NG_REQUIRE(out && c && a && b && scale && residual, "ng_gemm_int8_add: null pointer");
@@ -2336,6 +2376,12 @@ extern "C" int ng_gemm_int8_add(void* out, void* c, const void* a, const void* b
     for (const void* o : {out, c})
         apart = apart && !overlaps(o, cb, a, ab) && !overlaps(o, cb, b, bb) && !overlaps(o, cb, scale, sb);
     if (path < 1 || !apart) {
+        // Up to 128 rows of A on the weight-streaming kernels, cuda_gemm_int8's
+        // own path: the add in the split-K reduction where it has one.
+        if (apart && use_i8w(a, b, M, K, N, true)) {
+            const ResEpi ep{static_cast<uint16_t*>(out), static_cast<const uint16_t*>(residual)};
+            return gemm_i8w(c, a, b, scale, M, K, N, nullptr, 0, &ep);
+        }
         const int r = cuda_gemm_int8(c, a, b, scale, M, K, N, true);
         if (r != 0) return r;
         return cuda_add(out, c, residual, static_cast<size_t>(M) * N);

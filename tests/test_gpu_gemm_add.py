@@ -2,11 +2,13 @@
 
 Bar: c and out are bit-identical to the calls they replace,
 cuda_gemm_int8(c, a, b, scale, M, K, N, true) and then cuda_add(out, c,
-residual, M N), on the same inputs: in the fused launch (the GEMV kernel's
-shapes, M <= 4) and where the call is the two calls (M > 4, M = 3-4 with K
-or N >= 8192, K not a multiple of 16), with out apart from c and the residual
-or in place on either (the engine writes the layer output apart,
-layer.cu:593-598).
+residual, M N), on the same inputs: in the fused GEMV launch (M <= 4 on the
+GEMV kernel's shapes), in the split-K reduction's epilogue (up to 128 rows on
+the split kernel with several K slices, with 4-wide and scalar reductions),
+after a split launch of one K slice or the small-M MFMA kernel (the add as
+its own launch), and as the two calls (K not a multiple of 16, M > 128), with
+out apart from c and the residual or in place on either (the engine writes
+the layer output apart, layer.cu:593-598).
 """
 from __future__ import annotations
 
@@ -20,10 +22,15 @@ pytestmark = pytest.mark.gpu
 RNG = np.random.Generator(np.random.PCG64(73))
 
 # (M, K, N): Mistral-7B's down projection at 1-2 tokens, Llama-2-7B's, M = 3-4
-# below 8192, ragged N and K, tiny shapes; then shapes that are the two calls.
+# below 8192, ragged N and K, tiny shapes (the fused GEMV launch); down at
+# 4, 8, 20 and 64 tokens and token tiles at 40 (the split reduction with the
+# add), N not a multiple of 4 (its scalar form), gate's shape at 8 tokens
+# (one K slice) and the small-M MFMA kernel; then the two calls.
 FUSED = [(1, 14336, 4096), (2, 14336, 4096), (1, 11008, 4096), (2, 13824, 5120), (3, 4096, 4096), (4, 2048, 5000),
          (1, 4112, 1000), (3, 2064, 17), (1, 16, 5)]
-TWO_CALLS = [(4, 14336, 4096), (8, 4096, 4096), (1, 4104, 64), (40, 1024, 2048)]
+SPLIT = [(4, 14336, 4096), (8, 14336, 4096), (20, 4096, 4096), (64, 14336, 4096), (40, 1024, 2048),
+         (24, 4096, 1002), (8, 4096, 14336), (8, 4096, 4096)]
+TWO_CALLS = [(1, 4104, 64), (200, 1024, 512)]
 
 
 def f16bits(x) -> np.ndarray:
@@ -61,7 +68,7 @@ def check(got, want):
         assert_bits_equal(got[k], want[k], k)
 
 
-@pytest.mark.parametrize("M,K,N", FUSED + TWO_CALLS)
+@pytest.mark.parametrize("M,K,N", FUSED + SPLIT + TWO_CALLS)
 def test_gemm_add_is_the_two_calls(lib, ora, M, K, N):
     banner(f"gemm_int8_add M={M} K={K} N={N}")
     p = problem(M, K, N)
@@ -71,7 +78,8 @@ def test_gemm_add_is_the_two_calls(lib, ora, M, K, N):
 
 
 @pytest.mark.parametrize("alias", ["c", "residual"])
-@pytest.mark.parametrize("M,K,N", [(1, 14336, 4096), (2, 4112, 1000), (8, 1024, 2048)])
+@pytest.mark.parametrize("M,K,N", [(1, 14336, 4096), (2, 4112, 1000), (8, 1024, 2048), (8, 14336, 4096),
+                                   (24, 4096, 1002)])
 def test_gemm_add_in_place(lib, M, K, N, alias):
     banner(f"gemm_int8_add in place on {alias} M={M} K={K} N={N}")
     p = problem(M, K, N)
@@ -80,15 +88,15 @@ def test_gemm_add_in_place(lib, M, K, N, alias):
 
 def test_gemm_add_consecutive_calls(lib):
     banner("gemm_int8_add: a call, then a smaller one")
-    for M, K, N in ((2, 14336, 4096), (1, 2048, 300)):
+    for M, K, N in ((2, 14336, 4096), (1, 2048, 300), (64, 14336, 4096), (8, 14336, 4096)):
         p = problem(M, K, N)
         check(run(lib, *p, fused=True), run(lib, *p, fused=False))
 
 
-def test_gemm_add_unaligned_is_the_two_calls(lib):
+@pytest.mark.parametrize("M,K,N", [(1, 4096, 1000), (8, 14336, 4096)])
+def test_gemm_add_unaligned_is_the_two_calls(lib, M, K, N):
     """A and the residual 2 bytes off 16-byte alignment: the two calls, their bits."""
-    banner("gemm_int8_add unaligned A and residual")
-    M, K, N = 1, 4096, 1000
+    banner(f"gemm_int8_add unaligned A and residual M={M}")
     a, b, s, res = problem(M, K, N)
     outs = []
     for fused in (True, False):
@@ -103,5 +111,28 @@ def test_gemm_add_unaligned_is_the_two_calls(lib):
             ok(lib.cuda_gemm_int8(cb.vp, ab.offset(2), bb.vp, sb.vp, M, K, N, True), "cuda_gemm_int8")
             ok(lib.cuda_add(ob.vp, cb.vp, rb.offset(2), M * N), "cuda_add")
         outs.append((get(ob, np.uint16, (M, N)), get(cb, np.uint16, (M, N))))
+    assert_bits_equal(outs[0][0], outs[1][0], "out")
+    assert_bits_equal(outs[0][1], outs[1][1], "c")
+
+
+@pytest.mark.parametrize("M,K,N", [(8, 14336, 4096), (1, 14336, 4096)])
+def test_gemm_add_unaligned_residual(lib, M, K, N):
+    """Only the residual (and out) 2 bytes off 8-byte alignment: the split
+    reduction takes its scalar form with the add; the GEMV launch is the two
+    calls. Their bits either way."""
+    banner(f"gemm_int8_add unaligned residual M={M}")
+    a, b, s, res = problem(M, K, N)
+    outs = []
+    for fused in (True, False):
+        ab, bb, sb = dev(a), dev(b), dev(s)
+        rb, ob = empty(res.nbytes + 2), empty(res.nbytes + 2)
+        rb.upload(np.concatenate([np.zeros(1, np.uint16), res.ravel()]))
+        cb = empty(M * N * 2)
+        if fused:
+            ok(lib.ng_gemm_int8_add(ob.offset(2), cb.vp, ab.vp, bb.vp, sb.vp, rb.offset(2), M, K, N), "ng_gemm_int8_add")
+        else:
+            ok(lib.cuda_gemm_int8(cb.vp, ab.vp, bb.vp, sb.vp, M, K, N, True), "cuda_gemm_int8")
+            ok(lib.cuda_add(ob.offset(2), cb.vp, rb.offset(2), M * N), "cuda_add")
+        outs.append((get(ob, np.uint16, (M * N + 1,))[1:].reshape(M, N), get(cb, np.uint16, (M, N))))
     assert_bits_equal(outs[0][0], outs[1][0], "out")
     assert_bits_equal(outs[0][1], outs[1][1], "c")
