@@ -63,6 +63,16 @@ def test_bench_refuses_more_than_one_gpu():
     assert "one GPU" in line["error"]
 
 
+def test_bench_lists_its_modes():
+    """Every mode of bench.py parses (--help exits before any GPU call)."""
+    proc = subprocess.run([sys.executable, str(ROOT / "bench.py"), "--help"], capture_output=True, text=True,
+                          timeout=120, cwd=ROOT)
+    assert proc.returncode == 0
+    for flag in ("--gpus", "--steps", "--warmup", "--profile-pass", "--profile-decode", "--decode-only",
+                 "--gemm-only", "--floors-only"):
+        assert flag in proc.stdout, flag
+
+
 def test_floor_kernels_compile_for_gfx950():
     """The access-pattern floor kernels bench.py times compile with hipRTC for
     gfx950 (compilation needs no GPU), so a GPU run never finds them broken."""
