@@ -634,12 +634,16 @@ __device__ __forceinline__ void gemv_i8w_norm_block(uint16_t* __restrict__ c, co
     // block's four pairs of one head, rows h D + q + r (r < 4) and
     // h D + D/2 + q + r - 4. An output's sums do not depend on its slot, so
     // each row gets the GEMV kernel's bits either way.
+    // The geometry is read whether or not this product rotates: a read under
+    // the product's flag put a branch and a scalar-load wait before every code
+    // load.
     const bool rot = ROPE && rope;
-    const int rh = rot ? blk / re->bph : 0;
-    const int rq = rot ? (blk - rh * re->bph) * 4 : 0;
-    const auto row_of = [&](int r) {
-        return rot ? rh * re->D + (r < 4 ? rq + r : re->half + rq + r - 4) : n0 + r;
-    };
+    const int rbph = ROPE ? re->bph : 1, rD = ROPE ? re->D : 0, rhalf = ROPE ? re->half : 0;
+    const int rh = rot ? blk / rbph : 0;
+    const int rq = rot ? (blk - rh * rbph) * 4 : 0;
+    const int lo = rot ? rh * rD + rq : n0;              // slots 0 .. 3: rows lo + r
+    const int hi = rot ? rh * rD + rhalf + rq - 4 : n0;  // slots 4 .. 7: rows hi + r
+    const auto row_of = [&](int r) { return (r < 4 ? lo : hi) + r; };
 
     // Loads: the lane's pieces of x (res) and w, then its rows of B. They are
     // issued without branches, so that waiting for the first ones does not
