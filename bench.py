@@ -893,9 +893,9 @@ def norm_shared_extras(L, hip, stream):
 
 def silu_mul_gemm_extras(L, hip, stream, K=4096, N=14336):
     """Mistral-7B's gate/up projections and SwiGLU (layer.cu:575-588) at M = 1,
-    2 and 4 tokens. us: ng_gemm_int8_silu_mul (one launch where both products
-    take the GEMV kernel, M <= 2 here); two_calls_us: ng_gemm_int8_shared_a,
-    then cuda_silu_mul. Both give the same bits; weight pools keep the codes
+    2, 4, 8 and 64 tokens. us: ng_gemm_int8_silu_mul (one launch: the GEMV
+    kernel at M <= 2 here, the split kernel's SwiGLU form from 3 rows);
+    two_calls_us: ng_gemm_int8_shared_a, then cuda_silu_mul. Both give the same bits; weight pools keep the codes
     cache-cold."""
     rng = np.random.Generator(np.random.PCG64(8))
     n = pool_slots(2 * N * K)
@@ -906,7 +906,7 @@ def silu_mul_gemm_extras(L, hip, stream, K=4096, N=14336):
         del wq
     (gp, gs), (up_, us_) = pools
     out = {}
-    for M in (1, 2, 4):
+    for M in (1, 2, 4, 8, 64):
         ab = DB.from_array(W.round_to(rng.standard_normal((M, K), dtype=np.float32), "f16"))
         gb, ub, ob = (Pool(hip, 2 * M * N, n) for _ in range(3))
         scv = (C.c_void_p * 2)(gs.ptr, us_.ptr)

@@ -184,11 +184,12 @@ int ng_rmsnorm_qkv_rope_int8(void* normed, void* q, void* k, void* v, const void
  * 575-588: cuda_gemm_int8 twice on one A, then cuda_silu and cuda_mul, which
  * this library's cuda_silu_mul replaces with one rounding): gate and up as
  * ng_gemm_int8_shared_a writes them, then out = cuda_silu_mul(gate, up), bit
- * for bit. When both products take the GEMV kernel (M <= 4, aligned
- * pointers) and no output overlaps an input or another output (out may be
- * gate or up itself, as the engine's in-place call), one launch computes all
- * three; otherwise this is the two calls. B is [N, K] (transpose_b). Returns
- * 0 or -1. */
+ * for bit. With no output overlapping an input or another output (out may
+ * be gate or up itself, as the engine's in-place call), one launch computes
+ * all three when both products take the GEMV kernel (M <= 4, aligned
+ * pointers) or, up to 128 rows, the split kernel with one K slice (wide
+ * products, e.g. Mistral-7B's gate/up); otherwise this is the two calls. B is
+ * [N, K] (transpose_b). Returns 0 or -1. */
 int ng_gemm_int8_silu_mul(void* out, void* gate, void* up, const void* a, const void* b_gate,
                           const void* scale_gate, const void* b_up, const void* scale_up, int M, int K, int N);
 

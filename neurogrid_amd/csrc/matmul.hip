@@ -885,11 +885,19 @@ int launch_gemv(uint16_t* c, const uint16_t* a, const int8_t* b, const float* sc
 // sums in memory and no second launch.
 constexpr int kBatch = 128;  // k per batch
 
-template <int MT, int W, int G>
+// SW (ng_gemm_int8_silu_mul, one K slice, no token tiles): the block's first
+// W/2 waves of each group take rows of the gate product and the last W/2 the
+// same rows of the up product (8 W row pairs per block instead of 16 W rows of
+// one product). A wave's sums depend only on its own 16 rows of B, which start
+// at a multiple of 16 either way, so gate and up are the values of their own
+// launches; the up waves hand their rounded values to the gate waves through
+// LDS, which write gate, up and fp16(silu(gate) * up).
+template <int MT, int W, int G, bool SW = false>
 __device__ __forceinline__ void gemm_i8w_split_block(
     uint16_t* __restrict__ c, const uint16_t* __restrict__ a, const int8_t* __restrict__ b,
     const float* __restrict__ scale, float* __restrict__ part, int M, int N, int K, int S, int tiles, int cps,
-    int TT, int blk) {
+    int TT, int blk, const SwigluArgs* sw = nullptr) {
+    static_assert(!SW || W % 2 == 0, "SW splits the waves of a group in two");
     // A batch of A in LDS. From 4 tiles of A on: 256 bytes per row, 16-byte
     // piece q of row m stored at piece q xor (m mod 16), so the MFMA reads
     // (16 rows, one piece each per lane group) are conflict-free; padded rows
@@ -939,8 +947,13 @@ __device__ __forceinline__ void gemm_i8w_split_block(
     const bool half_last = (K % kBatch) != 0;
     const int c0 = sl * cps;
     const int c1 = min(c0 + cps, nbatch);
-    const int nw = tile * (16 * W) + 16 * wv;  // first row of B of this wave
+    const bool upw = SW && wv >= W / 2;  // SW: this wave takes the up product's rows
+    const int nw = SW ? tile * (8 * W) + 16 * (wv % (W / 2)) : tile * (16 * W) + 16 * wv;  // first row of B
     const int n = nw + col;                                 // row of B this lane multiplies
+    if constexpr (SW) {
+        b = upw ? sw->bu : sw->bg;
+        scale = upw ? sw->su : sw->sg;
+    }
 
     // A and B are read with buffer loads: B from this wave's first row (rows
     // past N clamp to the last one), A from its start, so that per-load
@@ -1081,11 +1094,47 @@ __device__ __forceinline__ void gemm_i8w_split_block(
             for (int t = 0; t < MT; ++t) red[(((kg - 1) * W + wv) * MT + t) * kWave + lane] = acc[t];
         }
         __syncthreads();
-        if (kg > 0) return;
+        // SW keeps every wave to the epilogue's barriers.
+        if (!SW && kg > 0) return;
+        if (kg == 0) {
 #pragma unroll
-        for (int g = 1; g < G; ++g)
+            for (int g = 1; g < G; ++g)
 #pragma unroll
-            for (int t = 0; t < MT; ++t) acc[t] += red[(((g - 1) * W + wv) * MT + t) * kWave + lane];
+                for (int t = 0; t < MT; ++t) acc[t] += red[(((g - 1) * W + wv) * MT + t) * kWave + lane];
+        }
+    }
+    if constexpr (SW) {
+        // gate, up and SwiGLU (one K slice): the up waves of group 0 store
+        // their rounded values, the gate waves of group 0 combine.
+        __syncthreads();  // the group sums' reads of the A buffers are done
+        uint16_t* xch = reinterpret_cast<uint16_t*>(&lds_a[0][0][0]);  // [W/2][MT][4][64]
+        const int wp = wv % (W / 2);
+        if (kg == 0 && upw && n < N) {
+            const float sc = scale[n];
+#pragma unroll
+            for (int t = 0; t < MT; ++t)
+#pragma unroll
+                for (int e = 0; e < 4; ++e) xch[((wp * MT + t) * 4 + e) * kWave + lane] = from_f32<f16>(acc[t][e] * sc);
+        }
+        __syncthreads();
+        if (kg == 0 && !upw && n < N) {
+            const float sc = scale[n];
+#pragma unroll
+            for (int t = 0; t < MT; ++t)
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    const int m = 16 * t + 4 * grp + e;
+                    if (m < M) {
+                        const size_t o = static_cast<size_t>(m) * N + n;
+                        const uint16_t gv = from_f32<f16>(acc[t][e] * sc);
+                        const uint16_t uv = xch[((wp * MT + t) * 4 + e) * kWave + lane];
+                        sw->gate[o] = gv;
+                        sw->up[o] = uv;
+                        sw->out[o] = from_f32<f16>(swiglu_f32(to_f32<f16>(gv), to_f32<f16>(uv)));
+                    }
+                }
+        }
+        return;
     }
     if (S == 1) {
         if (n < N) {
@@ -1118,6 +1167,16 @@ __global__ __launch_bounds__(G * W * kWave) void gemm_i8w_split_kernel(
     const float* __restrict__ scale, float* __restrict__ part, int M, int N, int K, int S, int tiles, int cps,
     int TT) {
     gemm_i8w_split_block<MT, W, G>(c, a, b, scale, part, M, N, K, S, tiles, cps, TT, blockIdx.x);
+}
+
+// gate/up and SwiGLU on the split kernel (ng_gemm_int8_silu_mul from 3 rows):
+// one K slice, blocks of 8 W row pairs.
+template <int MT, int W, int G>
+__global__ __launch_bounds__(G * W * kWave) void gemm_i8w_split_swiglu_kernel(SwigluArgs sa,
+                                                                               const uint16_t* __restrict__ a,
+                                                                               int M, int N, int K, int cps) {
+    gemm_i8w_split_block<MT, W, G, true>(nullptr, a, nullptr, nullptr, nullptr, M, N, K, 1, 0, cps, 1, blockIdx.x,
+                                         &sa);
 }
 
 // Products that share A on one split-kernel shape (ng_gemm_int8_shared_a):
@@ -2318,11 +2377,38 @@ extern "C" int ng_rmsnorm_qkv_rope_int8(void* normed, void* q, void* k, void* v,
     return norm_shared<false>(name, 3, normed, nullptr, c, x, nullptr, norm_weight, eps, b, scales, n, M, hidden, &rs);
 }
 
+// The split kernel's SwiGLU form: the launch shape <MT, W, G> that
+// split_config gives each of gate and up, when it takes one K slice (the
+// wide two-group shapes); 1 when it does not, so that the caller runs the
+// two calls.
+template <int MT, int W, int G>
+int launch_split_swiglu(const SwigluArgs& sa, const uint16_t* a, int M, int N, int K) {
+    const int tn = (N + 16 * W - 1) / (16 * W);  // tiles of one product's own launch
+    int S = 0, cps = 0;
+    split_slices(tn, 1, G, K, S, cps);
+    if (S != 1) return 1;
+    const unsigned blocks = static_cast<unsigned>((N + 8 * W - 1) / (8 * W));
+    gemm_i8w_split_swiglu_kernel<MT, W, G><<<dim3(blocks), dim3(G * W * kWave), 0, stream()>>>(sa, a, M, N, K, cps);
+    NG_CHECK_LAUNCH("ng_gemm_int8_silu_mul");
+    return 0;
+}
+
+static int swiglu_split(const SwigluArgs& sa, const uint16_t* a, int M, int K, int N) {
+    switch (split_config(M, K, N)) {
+        case kSplit842: return launch_split_swiglu<8, 4, 2>(sa, a, M, N, K);
+        case kSplit442: return launch_split_swiglu<4, 4, 2>(sa, a, M, N, K);
+        case kSplit242: return launch_split_swiglu<2, 4, 2>(sa, a, M, N, K);
+        case kSplit142: return launch_split_swiglu<1, 4, 2>(sa, a, M, N, K);
+        default: return 1;
+    }
+}
+
 // gate/up (cuda_gemm_int8 on one A, as ng_gemm_int8_shared_a) and SwiGLU
-// (cuda_silu_mul): one launch of gemv_i8w_swiglu_kernel when both products
-// take the GEMV kernel and no output overlaps an input or another output
-// (out may be gate or up exactly); otherwise the two calls. The same bits
-// either way.
+// (cuda_silu_mul), when no output overlaps an input or another output (out
+// may be gate or up exactly): one launch of gemv_i8w_swiglu_kernel when both
+// products take the GEMV kernel, one of gemm_i8w_split_swiglu_kernel when
+// they take the split kernel with one K slice; otherwise the two calls. The
+// same bits either way.
 extern "C" int ng_gemm_int8_silu_mul(void* out, void* gate, void* up, const void* a, const void* b_gate,
                                      const void* scale_gate, const void* b_up, const void* scale_up, int M, int K,
                                      int N) {
@@ -2336,6 +2422,13 @@ extern "C" int ng_gemm_int8_silu_mul(void* out, void* gate, void* up, const void
     for (const void* o : {out, gate, up})
         apart = apart && !overlaps(o, cb, a, ab) && !overlaps(o, cb, b_gate, bb) && !overlaps(o, cb, b_up, bb) &&
                 !overlaps(o, cb, scale_gate, sb) && !overlaps(o, cb, scale_up, sb);
+    const SwigluArgs sa{static_cast<uint16_t*>(out), static_cast<uint16_t*>(gate), static_cast<uint16_t*>(up),
+                        static_cast<const int8_t*>(b_gate), static_cast<const int8_t*>(b_up),
+                        static_cast<const float*>(scale_gate), static_cast<const float*>(scale_up)};
+    if (path < 1 && apart && use_i8w(a, b_gate, M, K, N, true) && use_i8w(a, b_up, M, K, N, true)) {
+        const int r = swiglu_split(sa, static_cast<const uint16_t*>(a), M, K, N);
+        if (r <= 0) return r;
+    }
     if (path < 1 || !apart) {
         void* c[2] = {gate, up};
         const void* b[2] = {b_gate, b_up};
@@ -2345,9 +2438,6 @@ extern "C" int ng_gemm_int8_silu_mul(void* out, void* gate, void* up, const void
         if (r != 0) return r;
         return cuda_silu_mul(out, gate, up, static_cast<size_t>(M) * N);
     }
-    const SwigluArgs sa{static_cast<uint16_t*>(out), static_cast<uint16_t*>(gate), static_cast<uint16_t*>(up),
-                        static_cast<const int8_t*>(b_gate), static_cast<const int8_t*>(b_up),
-                        static_cast<const float*>(scale_gate), static_cast<const float*>(scale_up)};
     const auto ap = static_cast<const uint16_t*>(a);
     const dim3 block(kGvWaves * kWave);
     if (path == 3) {

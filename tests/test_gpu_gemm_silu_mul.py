@@ -3,10 +3,13 @@
 Bar: out, gate and up are bit-identical to the calls they replace,
 ng_gemm_int8_shared_a (gate and up on one A, each bit for bit its own
 cuda_gemm_int8) and then cuda_silu_mul(out, gate, up), on the same inputs:
-in the fused launch (both products on the GEMV kernel, M <= 4) and where the
-call is the two calls (M > 4, M = 3-4 with N >= 8192, K not a multiple of
-16), with out apart from gate and up or in place on either, as the engine
-runs SwiGLU in place on gate (layer.cu:585-588).
+in the fused GEMV launch (M <= 4 on the GEMV kernel's shapes), in the split
+kernel's SwiGLU form (3 to 128 rows where gate/up takes the two-group split
+kernel with one K slice: every one of its four shapes, ragged N), and where
+the call is the two calls (the small-M MFMA kernel, token tiles, split shapes
+with several K slices, K not a multiple of 16, M > 128), with out apart from
+gate and up or in place on either, as the engine runs SwiGLU in place on gate
+(layer.cu:585-588).
 """
 from __future__ import annotations
 
@@ -24,7 +27,13 @@ RNG = np.random.Generator(np.random.PCG64(71))
 # the two calls.
 FUSED = [(1, 4096, 14336), (2, 4096, 14336), (1, 4096, 11008), (2, 5120, 13824), (3, 4096, 4096), (4, 2048, 5000),
          (1, 4112, 1000), (3, 2064, 17), (1, 16, 5)]
-TWO_CALLS = [(4, 4096, 14336), (8, 4096, 14336), (1, 4104, 64), (40, 1024, 2048)]
+# the split kernel's SwiGLU form: <1,4,2> at 3-16 rows, <2,4,2> at 17-32,
+# <4,4,2> at 33-64, <8,4,2> at 65-128 (Mistral-7B), N not a multiple of 32
+# (12300), Llama-2-13B's width, K with a half last batch (4160)
+SPLIT = [(3, 4096, 14336), (4, 4096, 14336), (8, 4096, 14336), (16, 4096, 14336), (17, 4096, 14336),
+         (32, 4096, 14336), (40, 4096, 14336), (64, 4096, 14336), (65, 4096, 14336), (128, 4096, 14336),
+         (8, 4096, 12300), (20, 5120, 13824), (12, 4160, 12400)]
+TWO_CALLS = [(8, 4096, 4096), (8, 4096, 11008), (1, 4104, 64), (40, 1024, 2048), (200, 1024, 2048)]
 
 
 def f16bits(x) -> np.ndarray:
@@ -69,7 +78,7 @@ def check(got, want):
         assert_bits_equal(got[k], want[k], k)
 
 
-@pytest.mark.parametrize("M,K,N", FUSED + TWO_CALLS)
+@pytest.mark.parametrize("M,K,N", FUSED + SPLIT + TWO_CALLS)
 def test_silu_mul_is_the_two_calls(lib, M, K, N):
     banner(f"gemm_int8_silu_mul M={M} K={K} N={N}")
     p = problem(M, K, N)
@@ -77,7 +86,8 @@ def test_silu_mul_is_the_two_calls(lib, M, K, N):
 
 
 @pytest.mark.parametrize("alias", ["gate", "up"])
-@pytest.mark.parametrize("M,K,N", [(1, 4096, 14336), (2, 4112, 1000), (8, 1024, 2048)])
+@pytest.mark.parametrize("M,K,N", [(1, 4096, 14336), (2, 4112, 1000), (8, 1024, 2048), (8, 4096, 14336),
+                                   (100, 4096, 12300)])
 def test_silu_mul_in_place(lib, M, K, N, alias):
     banner(f"gemm_int8_silu_mul in place on {alias} M={M} K={K} N={N}")
     p = problem(M, K, N)
@@ -96,7 +106,7 @@ def test_silu_mul_large_and_nonfinite(lib):
 
 def test_silu_mul_consecutive_calls(lib):
     banner("gemm_int8_silu_mul: a call, then a smaller one")
-    for M, K, N in ((2, 4096, 14336), (1, 2048, 300)):
+    for M, K, N in ((2, 4096, 14336), (1, 2048, 300), (64, 4096, 14336), (8, 4096, 14336)):
         p = problem(M, K, N)
         check(run(lib, *p, fused=True), run(lib, *p, fused=False))
 
