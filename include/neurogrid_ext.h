@@ -198,9 +198,9 @@ int ng_gemm_int8_silu_mul(void* out, void* gate, void* up, const void* a, const 
  * true), then cuda_add(out, c, residual, M N), bit for bit. With no output
  * overlapping an input or the other output (out may be c or residual
  * itself): on the GEMV kernel's shapes (M <= 4, aligned pointers) one launch
- * writes both; up to 128 rows on the split-K kernel the add runs in the
- * reduction of its K slices. Otherwise this is the two calls. Returns 0 or
- * -1. */
+ * writes both; on the split-K kernel (up to 128 rows) and the prefill kernel
+ * (up to 4095) the add runs in the reduction of their K slices. Otherwise
+ * this is the two calls. Returns 0 or -1. */
 int ng_gemm_int8_add(void* out, void* c, const void* a, const void* b, const void* scale,
                      const void* residual, int M, int K, int N);
 

@@ -1878,7 +1878,7 @@ void prefill_slices(int tiles, int area, int K, int& S, int& cps) {
 
 template <int TM, int TN, int WM, int WN>
 int launch_prefill(uint16_t* c, const uint16_t* a, const int8_t* b, const float* scale, int M, int N, int K,
-                   float* scratch, size_t scratch_bytes) {
+                   float* scratch, size_t scratch_bytes, const ResEpi* ep = nullptr) {
     constexpr int BM = WM * TM * 16, BN = WN * TN * 16;
     const int tiles_m = (M + BM - 1) / BM, tiles_n = (N + BN - 1) / BN;
     const int tiles = tiles_m * tiles_n;
@@ -1891,7 +1891,8 @@ int launch_prefill(uint16_t* c, const uint16_t* a, const int8_t* b, const float*
     gemm_i8w_prefill_kernel<TM, TN, WM, WN><<<dim3(static_cast<unsigned>(tiles * S)), dim3(WM * WN * kWave), 0, s>>>(
         c, a, b, scale, part, M, N, K, tiles_m, tiles_n, S, cps);
     NG_CHECK_LAUNCH("cuda_gemm_int8");
-    return S > 1 ? launch_reduce(s, c, part, scale, M, N, S) : 0;
+    if (S > 1) return launch_reduce(s, c, part, scale, M, N, S, ep);
+    return ep ? cuda_add(ep->out, c, ep->res, static_cast<size_t>(M) * N) : 0;
 }
 
 // Tile shape by the number of tiles (see the prefill kernel): 256 x 256
@@ -1901,14 +1902,17 @@ bool prefill_wide_tiles(int M, int N) {
     return static_cast<long long>((M + 255) / 256) * ((N + 255) / 256) >= 192;
 }
 
+// With ep, the residual add after the product follows, in the split-K
+// reduction's epilogue where the launch slices K, else as cuda_add.
 int gemm_prefill(void* c, const void* a, const void* b, const void* scale, int M, int K, int N,
-                 float* scratch = nullptr, size_t scratch_bytes = 0) {
+                 float* scratch = nullptr, size_t scratch_bytes = 0, const ResEpi* ep = nullptr) {
     auto* cp = static_cast<uint16_t*>(c);
     auto* ap = static_cast<const uint16_t*>(a);
     auto* bp = static_cast<const int8_t*>(b);
     auto* sp = static_cast<const float*>(scale);
-    if (prefill_wide_tiles(M, N)) return launch_prefill<4, 4, 4, 4>(cp, ap, bp, sp, M, N, K, scratch, scratch_bytes);
-    return launch_prefill<4, 4, 2, 2>(cp, ap, bp, sp, M, N, K, scratch, scratch_bytes);
+    if (prefill_wide_tiles(M, N))
+        return launch_prefill<4, 4, 4, 4>(cp, ap, bp, sp, M, N, K, scratch, scratch_bytes, ep);
+    return launch_prefill<4, 4, 2, 2>(cp, ap, bp, sp, M, N, K, scratch, scratch_bytes, ep);
 }
 
 // The weight-streaming path takes transpose_b, M <= kMaxFusedM, 16-byte aligned
@@ -2454,10 +2458,11 @@ extern "C" int ng_gemm_int8_silu_mul(void* out, void* gate, void* up, const void
 // A product (cuda_gemm_int8 with transpose_b) and the residual add after it
 // (cuda_add(out, c, residual)): when no output overlaps an input or the other
 // output (out may be c or the residual exactly), one launch of
-// gemv_i8w_add_kernel on the GEMV kernel's shapes, and up to 128 rows the
-// weight-streaming kernels with the add in the split-K reduction (after the
-// product as cuda_add where the launch has one K slice); otherwise the two
-// calls. The same bits either way.
+// gemv_i8w_add_kernel on the GEMV kernel's shapes, and on cuda_gemm_int8's
+// other fused paths (the weight-streaming kernels up to 128 rows, the prefill
+// kernel below kLtMinM) the add in the split-K reduction (after the product as
+// cuda_add where the launch has one K slice); otherwise the two calls. The
+// same bits either way.
 extern "C" int ng_gemm_int8_add(void* out, void* c, const void* a, const void* b, const void* scale,
                                 const void* residual, int M, int K, int N) {
     NG_REQUIRE(out && c && a && b && scale && residual, "ng_gemm_int8_add: null pointer");
@@ -2470,12 +2475,13 @@ extern "C" int ng_gemm_int8_add(void* out, void* c, const void* a, const void* b
     for (const void* o : {out, c})
         apart = apart && !overlaps(o, cb, a, ab) && !overlaps(o, cb, b, bb) && !overlaps(o, cb, scale, sb);
     if (path < 1 || !apart) {
-        // Up to 128 rows of A on the weight-streaming kernels, cuda_gemm_int8's
-        // own path: the add in the split-K reduction where it has one.
-        if (apart && use_i8w(a, b, M, K, N, true)) {
-            const ResEpi ep{static_cast<uint16_t*>(out), static_cast<const uint16_t*>(residual)};
-            return gemm_i8w(c, a, b, scale, M, K, N, nullptr, 0, &ep);
-        }
+        // cuda_gemm_int8's own fused paths (the weight-streaming kernels up to
+        // 128 rows of A, the prefill kernel below kLtMinM): the add in the
+        // split-K reduction where the launch has one.
+        const ResEpi ep{static_cast<uint16_t*>(out), static_cast<const uint16_t*>(residual)};
+        if (apart && use_i8w(a, b, M, K, N, true)) return gemm_i8w(c, a, b, scale, M, K, N, nullptr, 0, &ep);
+        if (apart && M < kLtMinM && use_prefill(a, b, M, K, N, true))
+            return gemm_prefill(c, a, b, scale, M, K, N, nullptr, 0, &ep);
         const int r = cuda_gemm_int8(c, a, b, scale, M, K, N, true);
         if (r != 0) return r;
         return cuda_add(out, c, residual, static_cast<size_t>(M) * N);

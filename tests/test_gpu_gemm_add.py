@@ -4,9 +4,10 @@ Bar: c and out are bit-identical to the calls they replace,
 cuda_gemm_int8(c, a, b, scale, M, K, N, true) and then cuda_add(out, c,
 residual, M N), on the same inputs: in the fused GEMV launch (M <= 4 on the
 GEMV kernel's shapes), in the split-K reduction's epilogue (up to 128 rows on
-the split kernel with several K slices, with 4-wide and scalar reductions),
-after a split launch of one K slice or the small-M MFMA kernel (the add as
-its own launch), and as the two calls (K not a multiple of 16, M > 128), with
+the split kernel with several K slices, with 4-wide and scalar reductions, and
+on the prefill kernel's 128 x 128 tiles with K slices), after a launch of one K
+slice or the small-M MFMA kernel (the add as its own launch), and as the two
+calls (K not a multiple of 16, 4096 rows and more), with
 out apart from c and the residual or in place on either (the engine writes
 the layer output apart, layer.cu:593-598).
 """
@@ -30,7 +31,11 @@ FUSED = [(1, 14336, 4096), (2, 14336, 4096), (1, 11008, 4096), (2, 13824, 5120),
          (1, 4112, 1000), (3, 2064, 17), (1, 16, 5)]
 SPLIT = [(4, 14336, 4096), (8, 14336, 4096), (20, 4096, 4096), (64, 14336, 4096), (40, 1024, 2048),
          (24, 4096, 1002), (8, 4096, 14336), (8, 4096, 4096)]
-TWO_CALLS = [(1, 4104, 64), (200, 1024, 512)]
+# the prefill kernel: 128 x 128 tiles with K slices (512, 1000 and 2048 rows,
+# the add in the reduction), 256 x 256 tiles in one slice (3072 rows: the add
+# after it)
+PREFILL = [(512, 14336, 4096), (1000, 4096, 1000), (2048, 14336, 4096), (3072, 4096, 4096)]
+TWO_CALLS = [(1, 4104, 64), (4096, 1024, 512)]
 
 
 def f16bits(x) -> np.ndarray:
@@ -68,7 +73,7 @@ def check(got, want):
         assert_bits_equal(got[k], want[k], k)
 
 
-@pytest.mark.parametrize("M,K,N", FUSED + SPLIT + TWO_CALLS)
+@pytest.mark.parametrize("M,K,N", FUSED + SPLIT + PREFILL + TWO_CALLS)
 def test_gemm_add_is_the_two_calls(lib, ora, M, K, N):
     banner(f"gemm_int8_add M={M} K={K} N={N}")
     p = problem(M, K, N)
