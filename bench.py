@@ -536,15 +536,17 @@ def time_pool_kernel(hip, stream, thunks, launches=24, reps=4):
     return us
 
 
-def time_rotating(hip, stream, variants, rounds=3, launches=24):
-    """Median duration (us) of each variant (a list of thunks, one per buffer
-    slot), timed over `rounds` rounds with the order rotated each round: the
-    first variant timed in a run comes out slower on this GPU, by up to 5-10%."""
+def time_rotating(hip, stream, variants, rounds=3, launches=24, timer=None):
+    """Median duration (us) of each variant (what `timer` takes: by default
+    time_pool_kernel's thunks, one per buffer slot), timed over `rounds` rounds
+    with the order rotated each round: the first variant timed in a run comes
+    out slower on this GPU, by up to 5-10% (15% for the prefill GEMMs)."""
+    timer = timer or time_pool_kernel
     names = list(variants)
     times = {nm: [] for nm in names}
     for r in range(rounds):
         for nm in names[r % len(names):] + names[:r % len(names)]:
-            times[nm].append(time_pool_kernel(hip, stream, variants[nm], launches=launches))
+            times[nm].append(timer(hip, stream, variants[nm], launches=launches))
     return {nm: statistics.median(v) for nm, v in times.items()}
 
 
@@ -748,11 +750,12 @@ def gemm_extras(L, hip, stream):
         for M in PREFILL_M:
             ab = DB.from_array(W.round_to(rng.standard_normal((M, K), dtype=np.float32), "f16"))
             cb = DB(2 * M * N)
-            us = time_kernel(hip, stream, [lambda: L.cuda_gemm_int8(cb.vp, ab.vp, wp.at(0), sc.vp, M, K, N, True)],
-                             launches=8, reps=2)
-            usf = time_kernel(hip, stream,
-                              [lambda: L.ng_gemm_int8_noalloc(cb.vp, ab.vp, wp.at(0), sc.vp, M, K, N, True)],
-                              launches=8, reps=2)
+            # The same kernel below 4096 tokens: timed in rotated order.
+            tr = time_rotating(hip, stream, {
+                "gemm": [lambda: L.cuda_gemm_int8(cb.vp, ab.vp, wp.at(0), sc.vp, M, K, N, True)],
+                "noalloc": [lambda: L.ng_gemm_int8_noalloc(cb.vp, ab.vp, wp.at(0), sc.vp, M, K, N, True)]},
+                launches=8, timer=lambda *a, **k: time_kernel(*a, reps=2, **k))
+            us, usf = tr["gemm"], tr["noalloc"]
 
             def comp(M=M, ab=ab, cb=cb):
                 rc = L.cuda_dequantize_weights(deq.vp, wp.at(0), sc.vp, N, K, 1)
