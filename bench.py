@@ -335,6 +335,40 @@ class Pool:
         self.buf.free()
 
 
+class GroupPool:
+    """Pool slots that each hold several weight tensors one after another, as
+    an engine allocates a layer's weights in sequence: member(p).at(j) is
+    tensor p of slot j. One split-kernel launch over two such tensors (gate
+    and up) runs up to 20% faster or slower with their distance in memory,
+    and separate pools would leave that distance to the allocator."""
+
+    class _Member:
+        def __init__(self, group, p):
+            self.group, self.p = group, p
+
+        def at(self, j):
+            return C.c_void_p(self.group.pool.at(j).value + self.group.offs[self.p])
+
+        def free(self):
+            pass
+
+    def __init__(self, hip, arrays, n):
+        self.offs, off = [], 0
+        for a in arrays:
+            self.offs.append(off)
+            off += -(-a.nbytes // 256) * 256
+        cat = np.zeros(off, np.uint8)
+        for a, o in zip(arrays, self.offs):
+            cat[o:o + a.nbytes] = np.ascontiguousarray(a).view(np.uint8).reshape(-1)
+        self.pool = Pool(hip, off, n, cat)
+
+    def member(self, p):
+        return GroupPool._Member(self, p)
+
+    def free(self):
+        self.pool.free()
+
+
 def pool_slots(footprint_bytes, min_slots=3, max_slots=64):
     """Slots so that at least POOL_BYTES of other buffers are touched between
     two launches on the same slot (the Infinity Cache is 256 MB)."""
@@ -803,11 +837,13 @@ def shared_a_extras(L, hip, stream):
     out = {}
     for name, ns in sets.items():
         n = pool_slots(sum(ns) * K)
-        pools = []
+        wqs, scs = [], []
         for N in ns:
-            wq = rng.integers(-128, 128, (N, K)).astype(np.int8)
-            pools.append((N, Pool(hip, wq.nbytes, n, wq), DB.from_array(rng.uniform(1e-3, 1e-2, N).astype(np.float32))))
-            del wq
+            wqs.append(rng.integers(-128, 128, (N, K)).astype(np.int8))
+            scs.append(DB.from_array(rng.uniform(1e-3, 1e-2, N).astype(np.float32)))
+        grp = GroupPool(hip, wqs, n)
+        pools = [(N, grp.member(p), sc) for p, (N, sc) in enumerate(zip(ns, scs))]
+        del wqs
         cnt = len(ns)
         for M in (1, 2, 8, 32, 64, 512, 2048):
             ab = DB.from_array(W.round_to(rng.standard_normal((M, K), dtype=np.float32), "f16"))
@@ -836,8 +872,8 @@ def shared_a_extras(L, hip, stream):
                 cp.free()
             ab.free()
         for _, wp, sc in pools:
-            wp.free()
             sc.free()
+        grp.free()
     out["note"] = ("us: one ng_gemm_int8_shared_a call (one launch per group of products with the same launch "
                    "shape: the GEMV kernel at 1-2 tokens, the small-M MFMA kernel for q/k/v at 8, the split kernel "
                    "and its reduction up to 128 tokens (at 64 q alone and k/v together), the fused prefill kernel "
@@ -863,11 +899,13 @@ def norm_shared_extras(L, hip, stream):
     for name, ns, add in (("rmsnorm_qkv", [4096, 1024, 1024], False), ("add_rmsnorm_qkv", [4096, 1024, 1024], True),
                           ("add_rmsnorm_gate_up", [14336, 14336], True)):
         n = pool_slots(sum(ns) * K)
-        pools = []
+        wqs, scs = [], []
         for N in ns:
-            wq = rng.integers(-128, 128, (N, K)).astype(np.int8)
-            pools.append((N, Pool(hip, wq.nbytes, n, wq), DB.from_array(rng.uniform(1e-3, 1e-2, N).astype(np.float32))))
-            del wq
+            wqs.append(rng.integers(-128, 128, (N, K)).astype(np.int8))
+            scs.append(DB.from_array(rng.uniform(1e-3, 1e-2, N).astype(np.float32)))
+        grp = GroupPool(hip, wqs, n)
+        pools = [(N, grp.member(p), sc) for p, (N, sc) in enumerate(zip(ns, scs))]
+        del wqs
         cnt = len(ns)
         scv = (C.c_void_p * cnt)(*[sc.ptr for _, _, sc in pools])
         nv = (C.c_int * cnt)(*ns)
@@ -904,8 +942,8 @@ def norm_shared_extras(L, hip, stream):
             for x in (xb, rb, yb, rob):
                 x.free()
         for _, wp, sc in pools:
-            wp.free()
             sc.free()
+        grp.free()
     w.free()
     return out
 
@@ -918,12 +956,13 @@ def silu_mul_gemm_extras(L, hip, stream, K=4096, N=14336):
     cache-cold."""
     rng = np.random.Generator(np.random.PCG64(8))
     n = pool_slots(2 * N * K)
-    pools = []
+    wqs, scs = [], []
     for _ in range(2):
-        wq = rng.integers(-128, 128, (N, K)).astype(np.int8)
-        pools.append((Pool(hip, wq.nbytes, n, wq), DB.from_array(rng.uniform(1e-3, 1e-2, N).astype(np.float32))))
-        del wq
-    (gp, gs), (up_, us_) = pools
+        wqs.append(rng.integers(-128, 128, (N, K)).astype(np.int8))
+        scs.append(DB.from_array(rng.uniform(1e-3, 1e-2, N).astype(np.float32)))
+    grp = GroupPool(hip, wqs, n)
+    del wqs
+    (gp, gs), (up_, us_) = (grp.member(0), scs[0]), (grp.member(1), scs[1])
     out = {}
     for M in (1, 2, 4, 8, 64):
         ab = DB.from_array(W.round_to(rng.standard_normal((M, K), dtype=np.float32), "f16"))
@@ -949,9 +988,9 @@ def silu_mul_gemm_extras(L, hip, stream, K=4096, N=14336):
         for x in (gb, ub, ob):
             x.free()
         ab.free()
-    for p, s in pools:
-        p.free()
+    for s in scs:
         s.free()
+    grp.free()
     return out
 
 
@@ -1018,12 +1057,13 @@ def int8_decode_layer_extras(L, hip, stream):
     eps, theta = C.c_float(1e-5), C.c_float(1e6)
     shapes = {"q": (H, H), "k": (KV, H), "v": (KV, H), "o": (H, H), "gate": (I, H), "up": (I, H), "down": (H, I)}
     n = pool_slots(sum(a * b for a, b in shapes.values()))
-    wp, ws = {}, {}
+    wqs, ws = [], {}
     for name, (N, K) in shapes.items():
-        wq = rng.integers(-128, 128, (N, K)).astype(np.int8)
-        wp[name] = Pool(hip, wq.nbytes, n, wq)
+        wqs.append(rng.integers(-128, 128, (N, K)).astype(np.int8))
         ws[name] = DB.from_array(rng.uniform(1e-3, 1e-2, N).astype(np.float32))
-        del wq
+    grp = GroupPool(hip, wqs, n)   # the layer's weights one after another, as an engine loads them
+    wp = {name: grp.member(p) for p, name in enumerate(shapes)}
+    del wqs
     w_attn = DB.from_array(W.round_to(1 + 0.05 * rng.standard_normal(H, dtype=np.float32), "f16"))
     w_ffn = DB.from_array(W.round_to(1 + 0.05 * rng.standard_normal(H, dtype=np.float32), "f16"))
     out = {}
@@ -1106,8 +1146,8 @@ def int8_decode_layer_extras(L, hip, stream):
         for b_ in (x, attn, pos, normed, res, res2, q, o, out_b, gate, up, k_b, v_b):
             b_.free()
     for name in shapes:
-        wp[name].free()
         ws[name].free()
+    grp.free()
     w_attn.free()
     w_ffn.free()
     out["note"] = ("attention excluded (its output is a fixed buffer); engine = the reference's call sequence on this "
