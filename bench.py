@@ -1757,8 +1757,8 @@ def engine_int8_report(cfg, per, seq):
                   "sequence": ["rmsnorm", "rope_q", "rope_k", "add_rmsnorm (residual_in = layer input, normed in "
                                "place)", "silu_mul (in place)", "add"]},
         "saved_us": us - fus,
-        "note": "the engine's INT8 layer (layer.cu:458-598) around its GEMMs and attention; fused = the call-site "
-                "change written in INTEGRATION.md (cuda_add + copy + cuda_rmsnorm -> cuda_add_rmsnorm, "
+        "note": "the engine's INT8 layer (layer.cu:458-598) around its GEMMs and attention; fused = the call sites "
+                "changed to the fused entry points (cuda_add + copy + cuda_rmsnorm -> cuda_add_rmsnorm, "
                 "cuda_silu + cuda_mul -> cuda_silu_mul, the first copy dropped)"}
 
 
