@@ -188,8 +188,10 @@ int ng_rmsnorm_qkv_rope_int8(void* normed, void* q, void* k, void* v, const void
  * be gate or up itself, as the engine's in-place call), one launch computes
  * all three when both products take the GEMV kernel (M <= 4, aligned
  * pointers) or, up to 128 rows, the split kernel with one K slice (wide
- * products, e.g. Mistral-7B's gate/up); otherwise this is the two calls. B is
- * [N, K] (transpose_b). Returns 0 or -1. */
+ * products, e.g. Mistral-7B's gate/up); with several K slices (e.g.
+ * Llama-2-7B's gate/up) one shared split launch and one reduction that also
+ * writes SwiGLU; otherwise this is the two calls. B is [N, K] (transpose_b).
+ * Returns 0 or -1. */
 int ng_gemm_int8_silu_mul(void* out, void* gate, void* up, const void* a, const void* b_gate,
                           const void* scale_gate, const void* b_up, const void* scale_up, int M, int K, int N);
 

@@ -1209,6 +1209,33 @@ struct ResEpi {
     const uint16_t* res;
 };
 
+// Outputs i .. i + 3 (N % 4 == 0) and output t of the reduction, rounded.
+__device__ __forceinline__ u32x2 reduce_slices4(const float* __restrict__ part, const float* __restrict__ scale,
+                                                size_t mn, int N, int S, size_t i) {
+    f32x4 pv[8];
+#pragma unroll
+    for (int q = 0; q < 8; ++q)
+        pv[q] = *reinterpret_cast<const f32x4*>(part + static_cast<size_t>(q < S ? q : 0) * mn + i);
+    f32x4 v = pv[0];
+#pragma unroll
+    for (int q = 1; q < 8; ++q)
+        if (q < S) v += pv[q];
+    const f32x4 sc = *reinterpret_cast<const f32x4*>(scale + i % N);
+    return u32x2{pack2<f16>(v[0] * sc[0], v[1] * sc[1]), pack2<f16>(v[2] * sc[2], v[3] * sc[3])};
+}
+
+__device__ __forceinline__ uint16_t reduce_slices1(const float* __restrict__ part, const float* __restrict__ scale,
+                                                   size_t mn, int N, int S, size_t t) {
+    float pv[8];
+#pragma unroll
+    for (int q = 0; q < 8; ++q) pv[q] = part[static_cast<size_t>(q < S ? q : 0) * mn + t];
+    float v = pv[0];
+#pragma unroll
+    for (int q = 1; q < 8; ++q)
+        if (q < S) v += pv[q];
+    return from_f32<f16>(v * scale[t % N]);
+}
+
 template <bool VEC4, bool RES = false>
 __device__ __forceinline__ void split_reduce_block(uint16_t* c, const float* __restrict__ part,
                                                    const float* __restrict__ scale, int M, int N, int S, int blk,
@@ -1218,16 +1245,7 @@ __device__ __forceinline__ void split_reduce_block(uint16_t* c, const float* __r
     if (VEC4) {
         const size_t i = 4 * t;
         if (i >= mn) return;
-        f32x4 pv[8];
-#pragma unroll
-        for (int q = 0; q < 8; ++q)
-            pv[q] = *reinterpret_cast<const f32x4*>(part + static_cast<size_t>(q < S ? q : 0) * mn + i);
-        f32x4 v = pv[0];
-#pragma unroll
-        for (int q = 1; q < 8; ++q)
-            if (q < S) v += pv[q];
-        const f32x4 sc = *reinterpret_cast<const f32x4*>(scale + i % N);
-        const u32x2 out = {pack2<f16>(v[0] * sc[0], v[1] * sc[1]), pack2<f16>(v[2] * sc[2], v[3] * sc[3])};
+        const u32x2 out = reduce_slices4(part, scale, mn, N, S, i);
         if (RES) {
             const u32x2 rv = *reinterpret_cast<const u32x2*>(ep.res + i);
             *reinterpret_cast<u32x2*>(c + i) = out;
@@ -1241,14 +1259,7 @@ __device__ __forceinline__ void split_reduce_block(uint16_t* c, const float* __r
         }
     } else {
         if (t >= mn) return;
-        float pv[8];
-#pragma unroll
-        for (int q = 0; q < 8; ++q) pv[q] = part[static_cast<size_t>(q < S ? q : 0) * mn + t];
-        float v = pv[0];
-#pragma unroll
-        for (int q = 1; q < 8; ++q)
-            if (q < S) v += pv[q];
-        const uint16_t cv = from_f32<f16>(v * scale[t % N]);
+        const uint16_t cv = reduce_slices1(part, scale, mn, N, S, t);
         if (RES) {
             const float sum = to_f32<f16>(cv) + to_f32<f16>(ep.res[t]);
             c[t] = cv;
@@ -1264,6 +1275,39 @@ __global__ __launch_bounds__(256) void split_reduce_kernel(uint16_t* c, const fl
                                                            const float* __restrict__ scale, int M, int N, int S,
                                                            ResEpi ep = ResEpi{}) {
     split_reduce_block<VEC4, RES>(c, part, scale, M, N, S, blockIdx.x, ep);
+}
+
+// gate/up with several K slices and SwiGLU (ng_gemm_int8_silu_mul): each
+// thread reduces its outputs of both products as split_reduce_block does,
+// stores gate and up, then out = fp16(silu(gate) * up) (out may be gate or
+// up itself: each element is written by one thread, out last).
+template <bool VEC4>
+__global__ __launch_bounds__(256) void split_reduce_swiglu_kernel(SwigluArgs sa, const float* __restrict__ pg,
+                                                                  const float* __restrict__ pu, int M, int N,
+                                                                  int S) {
+    const size_t mn = static_cast<size_t>(M) * N;
+    const size_t t = static_cast<size_t>(blockIdx.x) * 256 + threadIdx.x;
+    if (VEC4) {
+        const size_t i = 4 * t;
+        if (i >= mn) return;
+        const u32x2 g = reduce_slices4(pg, sa.sg, mn, N, S, i);
+        const u32x2 u = reduce_slices4(pu, sa.su, mn, N, S, i);
+        u32x2 o;
+#pragma unroll
+        for (int h = 0; h < 2; ++h)
+            o[h] = pack2<f16>(swiglu_f32(el_get<f16, 0>(g[h]), el_get<f16, 0>(u[h])),
+                              swiglu_f32(el_get<f16, 1>(g[h]), el_get<f16, 1>(u[h])));
+        *reinterpret_cast<u32x2*>(sa.gate + i) = g;
+        *reinterpret_cast<u32x2*>(sa.up + i) = u;
+        *reinterpret_cast<u32x2*>(sa.out + i) = o;
+    } else {
+        if (t >= mn) return;
+        const uint16_t g = reduce_slices1(pg, sa.sg, mn, N, S, t);
+        const uint16_t u = reduce_slices1(pu, sa.su, mn, N, S, t);
+        sa.gate[t] = g;
+        sa.up[t] = u;
+        sa.out[t] = from_f32<f16>(swiglu_f32(to_f32<f16>(g), to_f32<f16>(u)));
+    }
 }
 
 // The reductions of the products of gemm_i8w_split_shared_kernel in one
@@ -2038,9 +2082,13 @@ struct SharedPlan {
 // more than one slice of K, each product with its own slices and its own
 // region of the stream's partial-sum buffer (the lock is held until both
 // kernels are enqueued, as in launch_split).
+// With sw (gate and up, both with several K slices, as count 2), the
+// reduction is split_reduce_swiglu_kernel's; otherwise it returns 1 before
+// launching anything.
 template <typename L>
 int run_shared_split(int count, void* const* c, const void* const* b, const void* const* scales, const int* n,
-                     int M, int K, const SharedPlan& pl, L&& launch) {
+                     int M, int K, const SharedPlan& pl, L&& launch, const SwigluArgs* sw = nullptr) {
+    if (sw && !(count == 2 && n[0] == n[1] && pl.S[0] > 1 && pl.S[1] == pl.S[0])) return 1;
     long long cols = 0;
     for (int i = 0; i < count; ++i)
         if (pl.S[i] > 1) cols += static_cast<long long>(pl.S[i]) * n[i];
@@ -2081,6 +2129,20 @@ int run_shared_split(int count, void* const* c, const void* const* b, const void
     }
     launch(set, sp, static_cast<unsigned>(blocks), st);
     NG_CHECK_LAUNCH("ng_gemm_int8_shared_a");
+    if (sw) {
+        const bool v4 = n[0] % 4 == 0 && aligned16(sw->sg) && aligned16(sw->su) && aligned8(sw->gate) &&
+                        aligned8(sw->up) && aligned8(sw->out);
+        const long long mn = static_cast<long long>(M) * n[0];
+        const unsigned sb = static_cast<unsigned>(v4 ? (mn / 4 + 255) / 256 : (mn + 255) / 256);
+        if (v4)
+            split_reduce_swiglu_kernel<true><<<dim3(sb), dim3(256), 0, st>>>(*sw, sp.part[0], sp.part[1], M, n[0],
+                                                                             pl.S[0]);
+        else
+            split_reduce_swiglu_kernel<false><<<dim3(sb), dim3(256), 0, st>>>(*sw, sp.part[0], sp.part[1], M, n[0],
+                                                                              pl.S[0]);
+        NG_CHECK_LAUNCH("ng_gemm_int8_silu_mul");
+        return 0;
+    }
     if (rblocks == 0) return 0;
     if (vec4_all || !vec4_any) {
         if (vec4_all)
@@ -2101,7 +2163,8 @@ int run_shared_split(int count, void* const* c, const void* const* b, const void
 // The split kernel's shared form: slices and blocks as launch_split.
 template <int MT, int W, int G>
 int launch_split_shared(int count, void* const* c, const uint16_t* a, const void* const* b,
-                        const void* const* scales, const int* n, int M, int K, int TT) {
+                        const void* const* scales, const int* n, int M, int K, int TT,
+                        const SwigluArgs* sw = nullptr) {
     SharedPlan pl{};
     for (int i = 0; i < count; ++i) {
         pl.tn[i] = (n[i] + 16 * W - 1) / (16 * W);
@@ -2114,7 +2177,7 @@ int launch_split_shared(int count, void* const* c, const uint16_t* a, const void
                             [&](const SharedSet& set, const SplitSet& sp, unsigned blocks, hipStream_t st) {
                                 gemm_i8w_split_shared_kernel<MT, W, G>
                                     <<<dim3(blocks), dim3(G * W * kWave), 0, st>>>(set, sp, a, M, K);
-                            });
+                            }, sw);
 }
 
 // The prefill kernel's shared form: tiles and slices as launch_prefill.
@@ -2150,7 +2213,10 @@ int shared_group(int path, int count, void* const* c, const void* a, const void*
         switch (path) {
             case 10 + kSplitTokenTiles:
                 return launch_split_shared<2, 4, 1>(count, c, ap, b, scales, n, M, K, (M + 31) / 32);
+            case 10 + kSplit141: return launch_split_shared<1, 4, 1>(count, c, ap, b, scales, n, M, K, 1);
             case 10 + kSplit241: return launch_split_shared<2, 4, 1>(count, c, ap, b, scales, n, M, K, 1);
+            case 10 + kSplit441: return launch_split_shared<4, 4, 1>(count, c, ap, b, scales, n, M, K, 1);
+            case 10 + kSplit841: return launch_split_shared<8, 4, 1>(count, c, ap, b, scales, n, M, K, 1);
             case 10 + kSplit142: return launch_split_shared<1, 4, 2>(count, c, ap, b, scales, n, M, K, 1);
             case 10 + kSplit242: return launch_split_shared<2, 4, 2>(count, c, ap, b, scales, n, M, K, 1);
             case 10 + kSplit442: return launch_split_shared<4, 4, 2>(count, c, ap, b, scales, n, M, K, 1);
@@ -2397,6 +2463,22 @@ int launch_split_swiglu(const SwigluArgs& sa, const uint16_t* a, int M, int N, i
     return 0;
 }
 
+// gate/up with several K slices on a one-group split shape: the shared launch
+// (partial sums only) and split_reduce_swiglu_kernel; 1 for other shapes.
+static int swiglu_sliced(const SwigluArgs& sa, const uint16_t* a, int M, int K, int N) {
+    void* c[2] = {sa.gate, sa.up};
+    const void* b[2] = {sa.bg, sa.bu};
+    const void* sc[2] = {sa.sg, sa.su};
+    const int n[2] = {N, N};
+    switch (shared_path(M, K, N)) {
+        case 10 + kSplit141: return launch_split_shared<1, 4, 1>(2, c, a, b, sc, n, M, K, 1, &sa);
+        case 10 + kSplit241: return launch_split_shared<2, 4, 1>(2, c, a, b, sc, n, M, K, 1, &sa);
+        case 10 + kSplit441: return launch_split_shared<4, 4, 1>(2, c, a, b, sc, n, M, K, 1, &sa);
+        case 10 + kSplit841: return launch_split_shared<8, 4, 1>(2, c, a, b, sc, n, M, K, 1, &sa);
+        default: return 1;
+    }
+}
+
 static int swiglu_split(const SwigluArgs& sa, const uint16_t* a, int M, int K, int N) {
     switch (split_config(M, K, N)) {
         case kSplit842: return launch_split_swiglu<8, 4, 2>(sa, a, M, N, K);
@@ -2411,8 +2493,9 @@ static int swiglu_split(const SwigluArgs& sa, const uint16_t* a, int M, int K, i
 // (cuda_silu_mul), when no output overlaps an input or another output (out
 // may be gate or up exactly): one launch of gemv_i8w_swiglu_kernel when both
 // products take the GEMV kernel, one of gemm_i8w_split_swiglu_kernel when
-// they take the split kernel with one K slice; otherwise the two calls. The
-// same bits either way.
+// they take the split kernel with one K slice, the shared split launch and
+// split_reduce_swiglu_kernel when they take a one-group split shape with
+// several K slices; otherwise the two calls. The same bits either way.
 extern "C" int ng_gemm_int8_silu_mul(void* out, void* gate, void* up, const void* a, const void* b_gate,
                                      const void* scale_gate, const void* b_up, const void* scale_up, int M, int K,
                                      int N) {
@@ -2430,7 +2513,8 @@ extern "C" int ng_gemm_int8_silu_mul(void* out, void* gate, void* up, const void
                         static_cast<const int8_t*>(b_gate), static_cast<const int8_t*>(b_up),
                         static_cast<const float*>(scale_gate), static_cast<const float*>(scale_up)};
     if (path < 1 && apart && use_i8w(a, b_gate, M, K, N, true) && use_i8w(a, b_up, M, K, N, true)) {
-        const int r = swiglu_split(sa, static_cast<const uint16_t*>(a), M, K, N);
+        int r = swiglu_split(sa, static_cast<const uint16_t*>(a), M, K, N);
+        if (r == 1) r = swiglu_sliced(sa, static_cast<const uint16_t*>(a), M, K, N);
         if (r <= 0) return r;
     }
     if (path < 1 || !apart) {

@@ -56,6 +56,13 @@ SETS = [
     (20, 4096, [14336, 14336]),
     (64, 4096, [14336, 14336]),
     (100, 4096, [14336, 14336]),
+    # the one-group split shapes with several K slices (Llama-2-7B's gate/up at
+    # 3-16, 17-32, 33-64 and 65-128 tokens, q/k/v of TinyLlama's width at 24)
+    (8, 4096, [11008, 11008]),
+    (24, 4096, [11008, 11008]),
+    (40, 4096, [11008, 11008]),
+    (100, 4096, [11008, 11008]),
+    (24, 2048, [5632, 5634]),
     # the fused prefill kernel (129-4095 tokens): q/k/v on 128 x 128 tiles with
     # K slices of several counts, ragged shapes, gate/up on 256 x 256 tiles,
     # and q on 256 x 256 tiles beside k/v on 128 x 128 (two launches); from

@@ -5,9 +5,11 @@ ng_gemm_int8_shared_a (gate and up on one A, each bit for bit its own
 cuda_gemm_int8) and then cuda_silu_mul(out, gate, up), on the same inputs:
 in the fused GEMV launch (M <= 4 on the GEMV kernel's shapes), in the split
 kernel's SwiGLU form (3 to 128 rows where gate/up takes the two-group split
-kernel with one K slice: every one of its four shapes, ragged N), and where
-the call is the two calls (the small-M MFMA kernel, token tiles, split shapes
-with several K slices, K not a multiple of 16, M > 128), with out apart from
+kernel with one K slice: every one of its four shapes, ragged N), in the
+split-K reduction's SwiGLU form (the one-group split shapes with several K
+slices: Llama-2-7B and TinyLlama widths, each of the four shapes, N not a
+multiple of 4), and where the call is the two calls (the small-M MFMA kernel,
+token tiles, K not a multiple of 16, M > 128), with out apart from
 gate and up or in place on either, as the engine runs SwiGLU in place on gate
 (layer.cu:585-588).
 """
@@ -33,7 +35,13 @@ FUSED = [(1, 4096, 14336), (2, 4096, 14336), (1, 4096, 11008), (2, 5120, 13824),
 SPLIT = [(3, 4096, 14336), (4, 4096, 14336), (8, 4096, 14336), (16, 4096, 14336), (17, 4096, 14336),
          (32, 4096, 14336), (40, 4096, 14336), (64, 4096, 14336), (65, 4096, 14336), (128, 4096, 14336),
          (8, 4096, 12300), (20, 5120, 13824), (12, 4160, 12400)]
-TWO_CALLS = [(8, 4096, 4096), (8, 4096, 11008), (1, 4104, 64), (40, 1024, 2048), (200, 1024, 2048)]
+# the reduction's SwiGLU form: <1,4,1> at 3-16 rows, <2,4,1> at 17-32,
+# <4,4,1> at 33-64, <8,4,1> at 65-128 (Llama-2-7B: 2 K slices), TinyLlama's
+# width (3 slices), N % 4 != 0 (one output per thread), K with a half last
+# batch
+SLICED = [(3, 4096, 11008), (8, 4096, 11008), (16, 4096, 11008), (17, 4096, 11008), (40, 4096, 11008),
+          (100, 4096, 11008), (24, 2048, 5632), (24, 2048, 5634), (8, 4160, 11000)]
+TWO_CALLS = [(8, 4096, 4096), (1, 4104, 64), (40, 1024, 2048), (200, 1024, 2048)]
 
 
 def f16bits(x) -> np.ndarray:
@@ -78,7 +86,7 @@ def check(got, want):
         assert_bits_equal(got[k], want[k], k)
 
 
-@pytest.mark.parametrize("M,K,N", FUSED + SPLIT + TWO_CALLS)
+@pytest.mark.parametrize("M,K,N", FUSED + SPLIT + SLICED + TWO_CALLS)
 def test_silu_mul_is_the_two_calls(lib, M, K, N):
     banner(f"gemm_int8_silu_mul M={M} K={K} N={N}")
     p = problem(M, K, N)
@@ -87,7 +95,7 @@ def test_silu_mul_is_the_two_calls(lib, M, K, N):
 
 @pytest.mark.parametrize("alias", ["gate", "up"])
 @pytest.mark.parametrize("M,K,N", [(1, 4096, 14336), (2, 4112, 1000), (8, 1024, 2048), (8, 4096, 14336),
-                                   (100, 4096, 12300)])
+                                   (100, 4096, 12300), (8, 4096, 11008), (24, 2048, 5634)])
 def test_silu_mul_in_place(lib, M, K, N, alias):
     banner(f"gemm_int8_silu_mul in place on {alias} M={M} K={K} N={N}")
     p = problem(M, K, N)
