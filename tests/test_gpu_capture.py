@@ -213,13 +213,17 @@ def _ops():
             2, o["n"].vp, o["ro"].vp, (C.c_void_p * 2)(o["y"].ptr, o["y2"].ptr), i["xh"].vp, i["rh"].vp, i["wh"].vp,
             EPS, (C.c_void_p * 2)(i["wq"].ptr, i["wq_wide"].ptr), (C.c_void_p * 2)(i["wsc"].ptr, i["wsc_wide"].ptr),
             (C.c_int * 2)(GN, GNW), 1, GK))
-    # gate/up and SwiGLU: one launch at M = 1 (in place on gate), the two calls at M = 16
+    # gate/up and SwiGLU: one launch at M = 1 (in place on gate), the two calls at M = 16, the shared split
+    # launch and the reduction's SwiGLU form at M = 24 (two K slices; the first 24 rows of a40)
     add("ng_gemm_int8_silu_mul_M1", {"g": (E2, (1, GN)), "u": (E2, (1, GN))},
         lambda L, i, o: L.ng_gemm_int8_silu_mul(o["g"].vp, o["g"].vp, o["u"].vp, i["a1"].vp, i["wq"].vp, i["wsc"].vp,
                                                 i["wq"].vp, i["wsc"].vp, 1, GK, GN))
     add("ng_gemm_int8_silu_mul_M16", {"o": (E2, (16, GN)), "g": (E2, (16, GN)), "u": (E2, (16, GN))},
         lambda L, i, o: L.ng_gemm_int8_silu_mul(o["o"].vp, o["g"].vp, o["u"].vp, i["a16"].vp, i["wq"].vp, i["wsc"].vp,
                                                 i["wq"].vp, i["wsc"].vp, 16, GK, GN))
+    add("ng_gemm_int8_silu_mul_M24_sliced", {"o": (E2, (24, GN)), "g": (E2, (24, GN)), "u": (E2, (24, GN))},
+        lambda L, i, o: L.ng_gemm_int8_silu_mul(o["o"].vp, o["g"].vp, o["u"].vp, i["a40"].vp, i["wq"].vp, i["wsc"].vp,
+                                                i["wq"].vp, i["wsc"].vp, 24, GK, GN))
     # RMSNorm, q/k/v and RoPE on q and k (heads of 64): one launch at M = 1 (1 token at position 7)
     add("ng_rmsnorm_qkv_rope_int8_M1", {"n": (E2, (1, GK)), "q": (E2, (1, GN)), "k": (E2, (1, GN)),
                                         "v": (E2, (1, GN))},
