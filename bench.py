@@ -723,6 +723,7 @@ def extra_kernels(L, hip, stream):
     out["gemm_int8_shared_a"] = sh = shared_a_extras(L, hip, stream)
     out["norm_gemm_int8_shared_a"] = norm_shared_extras(L, hip, stream)
     out["gemm_int8_silu_mul"] = silu_mul_gemm_extras(L, hip, stream)
+    out["gemm_int8_silu_mul_llama2_7b"] = silu_mul_gemm_extras(L, hip, stream, N=11008)
     out["gemm_int8_add"] = gemm_add_extras(L, hip, stream)
     out["int8_decode_layer"] = int8_decode_layer_extras(L, hip, stream)
     g = out["gemm_int8"]
@@ -949,9 +950,11 @@ def norm_shared_extras(L, hip, stream):
 
 
 def silu_mul_gemm_extras(L, hip, stream, K=4096, N=14336):
-    """Mistral-7B's gate/up projections and SwiGLU (layer.cu:575-588) at M = 1,
-    2, 4, 8 and 64 tokens. us: ng_gemm_int8_silu_mul (one launch: the GEMV
-    kernel at M <= 2 here, the split kernel's SwiGLU form from 3 rows);
+    """The gate/up projections and SwiGLU (layer.cu:575-588) at M = 1, 2, 4, 8
+    and 64 tokens, Mistral-7B's by default (N = 11008: Llama-2-7B's). us:
+    ng_gemm_int8_silu_mul (the GEMV kernel at M <= 2 here; from 3 rows the
+    split kernel's SwiGLU form, or with K slices (N = 11008) one shared split
+    launch and the reduction's SwiGLU form);
     two_calls_us: ng_gemm_int8_shared_a, then cuda_silu_mul. Both give the same bits; weight pools keep the codes
     cache-cold."""
     rng = np.random.Generator(np.random.PCG64(8))
@@ -1814,6 +1817,7 @@ def main():
     if args.decode_only:
         print(json.dumps({"norm_gemm_int8_shared_a": norm_shared_extras(L, hip, stream),
                           "gemm_int8_silu_mul": silu_mul_gemm_extras(L, hip, stream),
+                          "gemm_int8_silu_mul_llama2_7b": silu_mul_gemm_extras(L, hip, stream, N=11008),
                           "gemm_int8_add": gemm_add_extras(L, hip, stream),
                           "int8_decode_layer": int8_decode_layer_extras(L, hip, stream)}), flush=True)
         return
@@ -1822,6 +1826,7 @@ def main():
                           "gemm_int8_shared_a": shared_a_extras(L, hip, stream),
                           "norm_gemm_int8_shared_a": norm_shared_extras(L, hip, stream),
                           "gemm_int8_silu_mul": silu_mul_gemm_extras(L, hip, stream),
+                          "gemm_int8_silu_mul_llama2_7b": silu_mul_gemm_extras(L, hip, stream, N=11008),
                           "gemm_int8_add": gemm_add_extras(L, hip, stream),
                           "int8_decode_layer": int8_decode_layer_extras(L, hip, stream)}), flush=True)
         return
